@@ -1,0 +1,640 @@
+// gsd_capi.hip -- C ABI of libgsdhip.so (declared in include/gsdhip.h):
+// operator twins of the reference CPU engine and the model runtime that runs
+// a whole token as one HIP graph.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "gsd_internal.h"
+#include "../../include/gsdhip.h"
+
+using namespace gsd;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code ? code : -1;
+}
+
+#define HIPCHK(expr)                                                                        \
+    do {                                                                                    \
+        hipError_t e_ = (expr);                                                             \
+        if (e_ != hipSuccess) return fail((int)e_, "%s: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Codebook of radius R as float2 (gsd_lq_cpu_runtime.py:111-118).
+std::vector<float> host_table(int R) {
+    std::vector<float> t;
+    const double s32 = std::sqrt(3.0) / 2.0;
+    for (int a = -R; a <= R; a++)
+        for (int b = -R; b <= R; b++) {
+            if (std::abs(a + b) > R) continue;
+            t.push_back((float)((double)a + 0.5 * (double)b));
+            t.push_back((float)((double)b * s32));
+        }
+    return t;
+}
+
+// RoPE angles exactly as gsd_lq_cpu_engine.c:213-218 evaluates them (C library
+// powf/cosf/sinf in float), so the device rotation sees identical cos/sin.
+__attribute__((noinline)) void rope_cs(float theta, int hd, int pos, float* out /* 2*hd/2 */) {
+    const int half = hd / 2;
+    for (int i = 0; i < half; i++) {
+        const float freq = 1.0f / powf(theta, (float)(2 * i) / (float)hd);
+        const float ang = (float)pos * freq;
+        out[2 * i] = cosf(ang);
+        out[2 * i + 1] = sinf(ang);
+    }
+}
+
+// Scratch of the attention twin: partials + per-KV-head counters.
+struct AttnScratch {
+    std::mutex mu;
+    float* ws = nullptr;
+    size_t ws_floats = 0;
+    unsigned* counters = nullptr;
+    size_t n_counters = 0;
+} g_attn;
+
+int choose_chunk(int n_ctx, int n_kv) {
+    int c = (n_ctx * n_kv + 511) / 512;
+    c = (c + 31) / 32 * 32;
+    if (c < 64) c = 64;
+    if (c > 256) c = 256;
+    return c;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* gsdh_last_error(void) { return g_err.c_str(); }
+
+int gsdh_device_info(char* name, int name_len, uint64_t* total_bytes, int* n_cu) {
+    int dev = 0;
+    HIPCHK(hipGetDevice(&dev));
+    hipDeviceProp_t p;
+    HIPCHK(hipGetDeviceProperties(&p, dev));
+    if (name && name_len > 0) {
+        snprintf(name, name_len, "%s (%s)", p.name[0] ? p.name : "AMD Instinct", p.gcnArchName);
+    }
+    if (total_bytes) *total_bytes = p.totalGlobalMem;
+    if (n_cu) *n_cu = p.multiProcessorCount;
+    return 0;
+}
+
+int gsdh_malloc(void** ptr, uint64_t nbytes) {
+    HIPCHK(hipMalloc(ptr, nbytes ? nbytes : 4));
+    return 0;
+}
+int gsdh_free(void* ptr) {
+    HIPCHK(hipFree(ptr));
+    return 0;
+}
+int gsdh_memcpy_h2d(void* dst, const void* src, uint64_t n, void* stream) {
+    HIPCHK(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, S(stream)));
+    return 0;
+}
+int gsdh_memcpy_d2h(void* dst, const void* src, uint64_t n, void* stream) {
+    HIPCHK(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, S(stream)));
+    return 0;
+}
+int gsdh_stream_sync(void* stream) {
+    HIPCHK(hipStreamSynchronize(S(stream)));
+    return 0;
+}
+
+// ---------------------------------------------------------------------------
+// operator twins
+// ---------------------------------------------------------------------------
+int gsdh_rmsnorm(void* stream, const float* x, const float* w, float* out, int dim, float eps) {
+    if (dim <= 0) return fail(-1, "rmsnorm: dim %d", dim);
+    HIPCHK(launch_rmsnorm(x, w, out, dim, eps, S(stream)));
+    return 0;
+}
+
+int gsdh_vec_add(void* stream, float* y, const float* a, const float* b, int dim) {
+    HIPCHK(launch_vec_add(y, a, b, dim, S(stream)));
+    return 0;
+}
+
+int gsdh_swiglu(void* stream, const float* g, const float* u, float* out, int dim) {
+    HIPCHK(launch_swiglu(g, u, out, dim, S(stream)));
+    return 0;
+}
+
+int gsdh_lowrank_proj(void* stream, const float* x, const uint16_t* Vt, const float* Sv, float* tmp_k,
+                      int k_dim, int cols) {
+    if (k_dim < 0 || k_dim > kMaxRank) return fail(-1, "lowrank_proj: k_dim %d outside 0..%d", k_dim, kMaxRank);
+    HIPCHK(launch_lowrank(x, Vt, Sv, tmp_k, k_dim, cols, S(stream)));
+    return 0;
+}
+
+int gsdh_hex2d_matvec(void* stream, const float* x, const uint8_t* codes, const uint16_t* scales,
+                      const float* xy_table, const uint16_t* U, const float* tmp_k, const uint32_t* kink_row_ptr,
+                      const uint16_t* kink_cols, const float* kink_deltas, float* y, int rows, int cols, int k_dim,
+                      int n_pts) {
+    if (rows < 0) return fail(-1, "hex2d_matvec: rows %d", rows);
+    if (cols <= 0 || cols % 64) return fail(-1, "hex2d_matvec: cols %d is not a positive multiple of 64", cols);
+    if (cols > 65536) return fail(-1, "hex2d_matvec: cols %d > 65536", cols);
+    if (k_dim < 0 || k_dim > kMaxRank) return fail(-1, "hex2d_matvec: k_dim %d outside 0..%d", k_dim, kMaxRank);
+    if (n_pts <= 0 || n_pts > kTableSlots) return fail(-1, "hex2d_matvec: n_pts %d outside 1..256", n_pts);
+    if (k_dim > 0 && (!U || !tmp_k)) return fail(-1, "hex2d_matvec: k_dim > 0 needs U and tmp_k");
+    HexArgs a{};
+    a.nseg = 1;
+    HexSeg& s = a.seg[0];
+    s.codes = codes; s.scales = scales; s.row_ptr = kink_row_ptr; s.kcols = kink_cols; s.kdel = kink_deltas;
+    s.U = U; s.Vt = nullptr; s.S = nullptr; s.tmp_k = tmp_k; s.table = xy_table; s.out = y;
+    s.rows = rows; s.k = k_dim; s.n_pts = n_pts;
+    a.x = x; a.norm_w = nullptr; a.eps = 0.f; a.resid = nullptr; a.cols = cols; a.epilogue = kEpiStore;
+    HIPCHK(launch_hexmv(a, S(stream)));
+    return 0;
+}
+
+int gsdh_rope_and_store_kv(void* stream, float* q, const float* k, const float* v, uint16_t* k_cache,
+                           uint16_t* v_cache, int layer_idx, int pos, int n_heads, int n_kv_heads, int head_dim,
+                           int max_seq_len, float rope_theta, int interleaved) {
+    if (head_dim <= 0 || head_dim % 2 || head_dim > 256) return fail(-1, "rope: head_dim %d", head_dim);
+    if (pos < 0 || pos >= max_seq_len) return fail(-1, "rope: pos %d outside 0..%d", pos, max_seq_len - 1);
+    std::vector<float> cs(head_dim);
+    rope_cs(rope_theta, head_dim, pos, cs.data());
+    RopeKV r{};
+    r.cs = nullptr; r.pos_dev = nullptr; r.pos = pos; r.k_cache = k_cache; r.v_cache = v_cache;
+    r.layer = layer_idx; r.n_heads = n_heads; r.n_kv = n_kv_heads; r.hd = head_dim; r.max_seq = max_seq_len;
+    r.interleaved = interleaved;
+    HIPCHK(launch_rope_kv(q, k, v, r, reinterpret_cast<const float2*>(cs.data()), S(stream)));
+    return 0;
+}
+
+int gsdh_gqa_attention(void* stream, const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                       float* attn_out, int layer_idx, int pos, int n_heads, int n_kv_heads, int head_dim,
+                       int max_seq_len, float sm_scale) {
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256) return fail(-1, "attention: head_dim %d not in {64,128,256}", head_dim);
+    if (n_kv_heads <= 0 || n_heads % n_kv_heads || n_heads / n_kv_heads > 8)
+        return fail(-1, "attention: n_heads %d / n_kv_heads %d", n_heads, n_kv_heads);
+    if (pos < 0 || pos >= max_seq_len) return fail(-1, "attention: pos %d outside 0..%d", pos, max_seq_len - 1);
+    const int n = pos + 1, G = n_heads / n_kv_heads;
+    AttnArgs a{};
+    a.q = q; a.k_cache = k_cache; a.v_cache = v_cache; a.out = attn_out; a.pos_dev = nullptr; a.pos = pos;
+    a.layer = layer_idx; a.n_heads = n_heads; a.n_kv = n_kv_heads; a.hd = head_dim; a.max_seq = max_seq_len;
+    a.sm_scale = sm_scale;
+    a.chunk = choose_chunk(n, n_kv_heads);
+    a.max_splits = (n + a.chunk - 1) / a.chunk;
+    std::lock_guard<std::mutex> lk(g_attn.mu);
+    const size_t need = attention_ws_floats(n_kv_heads, a.max_splits, G, head_dim);
+    if (need > g_attn.ws_floats) {
+        if (g_attn.ws) HIPCHK(hipFree(g_attn.ws));
+        g_attn.ws = nullptr;
+        g_attn.ws_floats = 0;
+        HIPCHK(hipMalloc(&g_attn.ws, need * sizeof(float)));
+        g_attn.ws_floats = need;
+    }
+    if ((size_t)n_kv_heads > g_attn.n_counters) {
+        if (g_attn.counters) HIPCHK(hipFree(g_attn.counters));
+        g_attn.counters = nullptr;
+        g_attn.n_counters = 0;
+        HIPCHK(hipMalloc(&g_attn.counters, (size_t)n_kv_heads * sizeof(unsigned)));
+        HIPCHK(launch_fill_u32(g_attn.counters, 0u, (size_t)n_kv_heads, S(stream)));
+        g_attn.n_counters = (size_t)n_kv_heads;
+    }
+    a.ws = g_attn.ws;
+    a.counters = g_attn.counters;
+    HIPCHK(launch_attention(a, S(stream)));
+    return 0;
+}
+
+int gsdh_unpack_codes(void* stream, const uint8_t* codes, int64_t n, int radius, int32_t* idx_out, int8_t* r01_out) {
+    if (radius < 1 || radius > 8) return fail(-1, "unpack: radius %d outside 1..8", radius);
+    HIPCHK(launch_unpack(codes, n, radius, idx_out, r01_out, S(stream)));
+    return 0;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// model runtime
+// ---------------------------------------------------------------------------
+struct HexDev {
+    int set = 0, radius = 0, rows = 0, cols = 0, k = 0;
+    int64_t nk = 0;
+    uint8_t* codes = nullptr;
+    uint16_t* scales = nullptr;
+    uint32_t* row_ptr = nullptr;
+    uint16_t* kcols = nullptr;
+    float* kdel = nullptr;
+    uint16_t* U = nullptr;
+    float* Sv = nullptr;
+    uint16_t* Vt = nullptr;
+    void* block = nullptr;
+    size_t bytes = 0;
+};
+
+struct gsdh_model {
+    gsdh_model_config c{};
+    hipStream_t stream = nullptr;
+    float* tables[9] = {};          // by radius
+    uint16_t* embed = nullptr;
+    float* norms = nullptr;         // [n_layers][2][hidden] + output [hidden]
+    std::vector<HexDev> hex;        // n_layers * 7 + 1
+    float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *h = nullptr, *logits = nullptr;
+    uint16_t *kc = nullptr, *vc = nullptr;
+    float2* cs = nullptr;
+    float* ws = nullptr;
+    unsigned* counters = nullptr;
+    int chunk = 64, max_splits = 1;
+    StepState* st = nullptr;        // device
+    StepState* st_host = nullptr;   // pinned
+    int* gen_tok = nullptr;
+    float* gen_margin = nullptr;
+    hipGraphExec_t g_full = nullptr, g_prefill = nullptr;
+    hipGraph_t capture_graph = nullptr;
+    size_t dev_bytes = 0;
+    bool finalized = false;
+    std::vector<void*> allocs;
+
+    HexDev& slot(int layer, int s) { return s == GSDH_LM_HEAD ? hex.back() : hex[(size_t)layer * 7 + s]; }
+    float* norm(int layer, int which) {
+        return layer < 0 ? norms + (size_t)c.n_layers * 2 * c.hidden : norms + ((size_t)layer * 2 + which) * c.hidden;
+    }
+};
+
+namespace {
+
+int dalloc(gsdh_model* m, void** p, size_t n) {
+    hipError_t e = hipMalloc(p, n ? n : 4);
+    if (e != hipSuccess) return fail((int)e, "hipMalloc(%zu): %s", n, hipGetErrorString(e));
+    m->allocs.push_back(*p);
+    m->dev_bytes += n;
+    return 0;
+}
+
+void fill_seg(HexSeg& s, const HexDev& t, float* const* tables, float* out) {
+    s.codes = t.codes; s.scales = t.scales; s.row_ptr = t.nk ? t.row_ptr : nullptr;
+    s.kcols = t.kcols; s.kdel = t.kdel; s.U = t.U; s.Vt = t.Vt; s.S = t.Sv; s.tmp_k = nullptr;
+    s.table = tables[t.radius]; s.out = out; s.rows = t.rows; s.k = t.k;
+    s.n_pts = 3 * t.radius * t.radius + 3 * t.radius + 1;
+}
+
+int issue_linear(gsdh_model* m, int l, int mask) {
+    const auto& c = m->c;
+    if (mask & 1) {   // q, k, v with fused attention RMSNorm
+        HexArgs a{};
+        a.nseg = 3;
+        fill_seg(a.seg[0], m->slot(l, GSDH_Q), m->tables, m->q);
+        fill_seg(a.seg[1], m->slot(l, GSDH_K), m->tables, m->k);
+        fill_seg(a.seg[2], m->slot(l, GSDH_V), m->tables, m->v);
+        a.x = m->x; a.norm_w = m->norm(l, 0); a.eps = c.rms_eps; a.cols = c.hidden; a.epilogue = kEpiStore;
+        HIPCHK(launch_hexmv(a, m->stream));
+    }
+    if (mask & 2) {   // o projection + residual
+        HexArgs a{};
+        a.nseg = 1;
+        fill_seg(a.seg[0], m->slot(l, GSDH_O), m->tables, m->x);
+        a.x = m->attn; a.cols = c.n_heads * c.head_dim; a.epilogue = kEpiResidual; a.resid = m->x;
+        HIPCHK(launch_hexmv(a, m->stream));
+    }
+    if (mask & 4) {   // gate + up with fused FFN RMSNorm and SwiGLU
+        HexArgs a{};
+        a.nseg = 2;
+        fill_seg(a.seg[0], m->slot(l, GSDH_GATE), m->tables, m->h);
+        fill_seg(a.seg[1], m->slot(l, GSDH_UP), m->tables, nullptr);
+        a.x = m->x; a.norm_w = m->norm(l, 1); a.eps = c.rms_eps; a.cols = c.hidden; a.epilogue = kEpiSwiGLU;
+        HIPCHK(launch_hexmv(a, m->stream));
+    }
+    if (mask & 8) {   // down projection + residual
+        HexArgs a{};
+        a.nseg = 1;
+        fill_seg(a.seg[0], m->slot(l, GSDH_DOWN), m->tables, m->x);
+        a.x = m->h; a.cols = c.ffn; a.epilogue = kEpiResidual; a.resid = m->x;
+        HIPCHK(launch_hexmv(a, m->stream));
+    }
+    return 0;
+}
+
+// The per-token launch sequence (run_gpu_native_chat.py:892-969, fused).
+int issue_token(gsdh_model* m, bool with_head) {
+    const auto& c = m->c;
+    HIPCHK(launch_embed(m->embed, &m->st->token, m->x, c.hidden, m->stream));
+    for (int l = 0; l < c.n_layers; l++) {
+        int rc = issue_linear(m, l, 1);
+        if (rc) return rc;
+        RopeKV r{};
+        r.cs = m->cs; r.pos_dev = &m->st->pos; r.k_cache = m->kc; r.v_cache = m->vc; r.layer = l;
+        r.n_heads = c.n_heads; r.n_kv = c.n_kv_heads; r.hd = c.head_dim; r.max_seq = c.max_seq_len;
+        r.interleaved = c.rope_interleaved;
+        HIPCHK(launch_rope_kv(m->q, m->k, m->v, r, nullptr, m->stream));
+        AttnArgs a{};
+        a.q = m->q; a.k_cache = m->kc; a.v_cache = m->vc; a.out = m->attn; a.pos_dev = &m->st->pos;
+        a.layer = l; a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.hd = c.head_dim; a.max_seq = c.max_seq_len;
+        a.sm_scale = 1.0f / (float)std::sqrt((double)c.head_dim);
+        a.chunk = m->chunk; a.max_splits = m->max_splits; a.ws = m->ws; a.counters = m->counters;
+        HIPCHK(launch_attention(a, m->stream));
+        rc = issue_linear(m, l, 2 | 4 | 8);
+        if (rc) return rc;
+    }
+    if (with_head) {
+        HexArgs a{};
+        a.nseg = 1;
+        fill_seg(a.seg[0], m->slot(0, GSDH_LM_HEAD), m->tables, m->logits);
+        a.x = m->x; a.norm_w = m->norm(-1, 0); a.eps = c.rms_eps; a.cols = c.hidden; a.epilogue = kEpiStore;
+        HIPCHK(launch_hexmv(a, m->stream));
+        HIPCHK(launch_argmax(m->logits, c.vocab, m->st, m->gen_tok, m->gen_margin, 1, m->stream));
+    }
+    return 0;
+}
+
+int capture(gsdh_model* m, bool with_head, hipGraphExec_t* out) {
+    hipGraph_t g = nullptr;
+    HIPCHK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+    int rc = issue_token(m, with_head);
+    hipError_t e = hipStreamEndCapture(m->stream, &g);
+    if (rc) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+    }
+    if (e != hipSuccess) return fail((int)e, "hipStreamEndCapture: %s", hipGetErrorString(e));
+    e = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return fail((int)e, "hipGraphInstantiate: %s", hipGetErrorString(e));
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int gsdh_model_create(const gsdh_model_config* cfg, gsdh_model** out) {
+    if (!cfg || !out) return fail(-1, "model_create: null argument");
+    const gsdh_model_config& c = *cfg;
+    if (c.n_layers <= 0 || c.hidden <= 0 || c.ffn <= 0 || c.vocab <= 0 || c.max_seq_len <= 0)
+        return fail(-1, "model_create: non-positive dimension");
+    if (c.hidden % 64 || c.ffn % 64 || (c.n_heads * c.head_dim) % 64)
+        return fail(-1, "model_create: hidden %d, ffn %d and n_heads*head_dim must be multiples of 64", c.hidden, c.ffn);
+    if (c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256)
+        return fail(-1, "model_create: head_dim %d not in {64,128,256}", c.head_dim);
+    if (c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads || c.n_heads / c.n_kv_heads > 8)
+        return fail(-1, "model_create: n_heads %d / n_kv_heads %d", c.n_heads, c.n_kv_heads);
+    if (c.hidden > 65536 || c.ffn > 65536) return fail(-1, "model_create: dimension > 65536");
+    gsdh_model* m = new gsdh_model();
+    m->c = c;
+    m->hex.resize((size_t)c.n_layers * 7 + 1);
+    int rc = 0;
+    auto A = [&](void** p, size_t n) { if (!rc) rc = dalloc(m, p, n); };
+    hipError_t e = hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) { delete m; return fail((int)e, "hipStreamCreate: %s", hipGetErrorString(e)); }
+    const size_t qd = (size_t)c.n_heads * c.head_dim, kvd = (size_t)c.n_kv_heads * c.head_dim;
+    A((void**)&m->x, c.hidden * 4);
+    A((void**)&m->q, qd * 4);
+    A((void**)&m->k, kvd * 4);
+    A((void**)&m->v, kvd * 4);
+    A((void**)&m->attn, qd * 4);
+    A((void**)&m->h, (size_t)c.ffn * 4);
+    A((void**)&m->logits, (size_t)c.vocab * 4);
+    const size_t kvn = (size_t)c.n_layers * c.max_seq_len * kvd;
+    A((void**)&m->kc, kvn * 2);
+    A((void**)&m->vc, kvn * 2);
+    A((void**)&m->norms, ((size_t)c.n_layers * 2 + 1) * c.hidden * 4);
+    A((void**)&m->embed, (size_t)c.vocab * c.hidden * 2);
+    A((void**)&m->cs, (size_t)c.max_seq_len * (c.head_dim / 2) * sizeof(float2));
+    m->chunk = choose_chunk(c.max_seq_len, c.n_kv_heads);
+    m->max_splits = (c.max_seq_len + m->chunk - 1) / m->chunk;
+    A((void**)&m->ws, attention_ws_floats(c.n_kv_heads, m->max_splits, c.n_heads / c.n_kv_heads, c.head_dim) * 4);
+    A((void**)&m->counters, (size_t)c.n_kv_heads * 4);
+    A((void**)&m->st, sizeof(StepState));
+    A((void**)&m->gen_tok, (size_t)c.max_seq_len * 4);
+    A((void**)&m->gen_margin, (size_t)c.max_seq_len * 4);
+    for (int R = 1; R <= 8; R++) {
+        std::vector<float> t = host_table(R);
+        A((void**)&m->tables[R], t.size() * 4);
+        if (!rc) {
+            e = hipMemcpy(m->tables[R], t.data(), t.size() * 4, hipMemcpyHostToDevice);
+            if (e != hipSuccess) rc = fail((int)e, "hipMemcpy table: %s", hipGetErrorString(e));
+        }
+    }
+    if (!rc) {
+        e = hipHostMalloc((void**)&m->st_host, sizeof(StepState) * 2, 0);
+        if (e != hipSuccess) rc = fail((int)e, "hipHostMalloc: %s", hipGetErrorString(e));
+    }
+    if (!rc) {
+        // zero the KV cache and counters with kernels (no memset nodes anywhere)
+        e = launch_fill_u32(m->counters, 0u, (size_t)c.n_kv_heads, m->stream);
+        if (e == hipSuccess) e = launch_fill_u32((unsigned*)m->kc, 0u, kvn / 2, m->stream);
+        if (e == hipSuccess) e = launch_fill_u32((unsigned*)m->vc, 0u, kvn / 2, m->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+        if (e != hipSuccess) rc = fail((int)e, "model init: %s", hipGetErrorString(e));
+    }
+    if (!rc) {
+        // RoPE table [pos][i] = (cos, sin), evaluated like the reference engine
+        std::vector<float> cs((size_t)c.max_seq_len * c.head_dim);
+        for (int p = 0; p < c.max_seq_len; p++) rope_cs(c.rope_theta, c.head_dim, p, cs.data() + (size_t)p * c.head_dim);
+        e = hipMemcpy(m->cs, cs.data(), cs.size() * 4, hipMemcpyHostToDevice);
+        if (e != hipSuccess) rc = fail((int)e, "hipMemcpy rope: %s", hipGetErrorString(e));
+    }
+    if (rc) {
+        gsdh_model_destroy(m);
+        return rc;
+    }
+    *out = m;
+    return 0;
+}
+
+int gsdh_model_destroy(gsdh_model* m) {
+    if (!m) return 0;
+    if (m->stream) (void)hipStreamSynchronize(m->stream);
+    if (m->g_full) (void)hipGraphExecDestroy(m->g_full);
+    if (m->g_prefill) (void)hipGraphExecDestroy(m->g_prefill);
+    for (auto& t : m->hex)
+        if (t.block) (void)hipFree(t.block);
+    for (void* p : m->allocs) (void)hipFree(p);
+    if (m->st_host) (void)hipHostFree(m->st_host);
+    if (m->stream) (void)hipStreamDestroy(m->stream);
+    delete m;
+    return 0;
+}
+
+int gsdh_model_set_embedding(gsdh_model* m, const uint16_t* embed) {
+    HIPCHK(hipMemcpy(m->embed, embed, (size_t)m->c.vocab * m->c.hidden * 2, hipMemcpyHostToDevice));
+    return 0;
+}
+
+int gsdh_model_set_norm(gsdh_model* m, int layer, int which, const float* w) {
+    if (layer >= m->c.n_layers || which < 0 || which > 1) return fail(-1, "set_norm: layer %d which %d", layer, which);
+    HIPCHK(hipMemcpy(m->norm(layer, which), w, (size_t)m->c.hidden * 4, hipMemcpyHostToDevice));
+    return 0;
+}
+
+int gsdh_model_set_hex(gsdh_model* m, int layer, int slot, int radius, int rows, int cols, int k_dim,
+                       const uint8_t* codes, const uint16_t* scales, const uint32_t* row_ptr,
+                       const uint16_t* kink_cols, const float* kink_deltas, int64_t nk, const uint16_t* U,
+                       const float* Sv, const uint16_t* Vt) {
+    const auto& c = m->c;
+    if (slot < 0 || slot > GSDH_LM_HEAD) return fail(-1, "set_hex: slot %d", slot);
+    if (slot != GSDH_LM_HEAD && (layer < 0 || layer >= c.n_layers)) return fail(-1, "set_hex: layer %d", layer);
+    const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
+    int er = 0, ec = 0;
+    switch (slot) {
+        case GSDH_Q: er = qd; ec = c.hidden; break;
+        case GSDH_K: case GSDH_V: er = kvd; ec = c.hidden; break;
+        case GSDH_O: er = c.hidden; ec = qd; break;
+        case GSDH_GATE: case GSDH_UP: er = c.ffn; ec = c.hidden; break;
+        case GSDH_DOWN: er = c.hidden; ec = c.ffn; break;
+        default: er = c.vocab; ec = c.hidden; break;
+    }
+    if (rows != er || cols != ec) return fail(-1, "set_hex: layer %d slot %d shape %dx%d, expected %dx%d", layer, slot, rows, cols, er, ec);
+    if (radius < 1 || radius > 8) return fail(-1, "set_hex: radius %d outside 1..8", radius);
+    if (k_dim < 0 || k_dim > kMaxRank) return fail(-1, "set_hex: k_dim %d outside 0..%d", k_dim, kMaxRank);
+    if (k_dim > 0 && (!U || !Sv || !Vt)) return fail(-1, "set_hex: k_dim %d without U/S/Vt", k_dim);
+    if (nk < 0 || (nk > 0 && (!kink_cols || !kink_deltas))) return fail(-1, "set_hex: nk %lld", (long long)nk);
+    const int n_pts = 3 * radius * radius + 3 * radius + 1;
+    const size_t ncodes = (size_t)rows * cols / 2;
+    // validate: codes < n_pts, CSR monotone and ending at nk, kink columns < cols
+    for (size_t i = 0; i < ncodes; i++)
+        if (codes[i] >= n_pts) return fail(-1, "set_hex: code %u at %zu >= n_pts %d (layer %d slot %d)", codes[i], i, n_pts, layer, slot);
+    if (row_ptr[0] != 0) return fail(-1, "set_hex: row_ptr[0] != 0");
+    for (int r = 0; r < rows; r++)
+        if (row_ptr[r + 1] < row_ptr[r]) return fail(-1, "set_hex: row_ptr not monotone at row %d", r);
+    if ((int64_t)row_ptr[rows] != nk) return fail(-1, "set_hex: row_ptr[rows]=%u but %lld kinks", row_ptr[rows], (long long)nk);
+    for (int64_t i = 0; i < nk; i++)
+        if (kink_cols[i] >= cols) return fail(-1, "set_hex: kink column %u >= cols %d", kink_cols[i], cols);
+
+    HexDev& t = m->slot(layer, slot);
+    if (t.block) { (void)hipFree(t.block); m->dev_bytes -= t.bytes; t = HexDev(); }
+    auto al = [](size_t n) { return (n + 255) / 256 * 256; };
+    const size_t o_codes = 0, o_sc = o_codes + al(ncodes), o_rp = o_sc + al((size_t)rows * cols / 64 * 2);
+    const size_t o_kc = o_rp + al((size_t)(rows + 1) * 4), o_kd = o_kc + al((size_t)nk * 2);
+    const size_t o_u = o_kd + al((size_t)nk * 4), o_s = o_u + al((size_t)rows * k_dim * 2);
+    const size_t o_vt = o_s + al((size_t)k_dim * 4), total = o_vt + al((size_t)k_dim * cols * 2);
+    void* blk = nullptr;
+    HIPCHK(hipMalloc(&blk, total));
+    char* b = static_cast<char*>(blk);
+    t.block = blk; t.bytes = total; m->dev_bytes += total;
+    t.codes = (uint8_t*)(b + o_codes); t.scales = (uint16_t*)(b + o_sc); t.row_ptr = (uint32_t*)(b + o_rp);
+    t.kcols = (uint16_t*)(b + o_kc); t.kdel = (float*)(b + o_kd); t.U = (uint16_t*)(b + o_u);
+    t.Sv = (float*)(b + o_s); t.Vt = (uint16_t*)(b + o_vt);
+    HIPCHK(hipMemcpy(t.codes, codes, ncodes, hipMemcpyHostToDevice));
+    HIPCHK(hipMemcpy(t.scales, scales, (size_t)rows * cols / 64 * 2, hipMemcpyHostToDevice));
+    HIPCHK(hipMemcpy(t.row_ptr, row_ptr, (size_t)(rows + 1) * 4, hipMemcpyHostToDevice));
+    if (nk > 0) {
+        HIPCHK(hipMemcpy(t.kcols, kink_cols, (size_t)nk * 2, hipMemcpyHostToDevice));
+        HIPCHK(hipMemcpy(t.kdel, kink_deltas, (size_t)nk * 4, hipMemcpyHostToDevice));
+    }
+    if (k_dim > 0) {
+        HIPCHK(hipMemcpy(t.U, U, (size_t)rows * k_dim * 2, hipMemcpyHostToDevice));
+        HIPCHK(hipMemcpy(t.Sv, Sv, (size_t)k_dim * 4, hipMemcpyHostToDevice));
+        HIPCHK(hipMemcpy(t.Vt, Vt, (size_t)k_dim * cols * 2, hipMemcpyHostToDevice));
+    }
+    t.set = 1; t.radius = radius; t.rows = rows; t.cols = cols; t.k = k_dim; t.nk = nk;
+    return 0;
+}
+
+int gsdh_model_finalize(gsdh_model* m) {
+    for (int l = 0; l < m->c.n_layers; l++)
+        for (int s = 0; s < 7; s++)
+            if (!m->slot(l, s).set) return fail(-1, "finalize: layer %d slot %d not set", l, s);
+    if (!m->slot(0, GSDH_LM_HEAD).set) return fail(-1, "finalize: lm_head not set");
+    int rc = capture(m, true, &m->g_full);
+    if (!rc) rc = capture(m, false, &m->g_prefill);
+    if (rc) return rc;
+    m->finalized = true;
+    return 0;
+}
+
+uint64_t gsdh_model_device_bytes(gsdh_model* m) { return m ? m->dev_bytes : 0; }
+
+int gsdh_forward_token(gsdh_model* m, int token_id, int pos, int want_logits, float* logits_host, int* argmax_out) {
+    if (!m->finalized) return fail(-1, "forward_token: model not finalized");
+    if (token_id < 0 || token_id >= m->c.vocab) return fail(-1, "forward_token: token %d outside vocab %d", token_id, m->c.vocab);
+    if (pos < 0 || pos >= m->c.max_seq_len) return fail(-1, "forward_token: pos %d outside 0..%d", pos, m->c.max_seq_len - 1);
+    StepState* h = m->st_host;
+    h->token = token_id; h->pos = pos; h->gen_count = 0; h->pad = 0;
+    HIPCHK(hipMemcpyAsync(m->st, h, sizeof(StepState), hipMemcpyHostToDevice, m->stream));
+    HIPCHK(hipGraphLaunch(want_logits ? m->g_full : m->g_prefill, m->stream));
+    if (want_logits) {
+        if (logits_host) HIPCHK(hipMemcpyAsync(logits_host, m->logits, (size_t)m->c.vocab * 4, hipMemcpyDeviceToHost, m->stream));
+        HIPCHK(hipMemcpyAsync(m->st_host + 1, m->st, sizeof(StepState), hipMemcpyDeviceToHost, m->stream));
+    }
+    HIPCHK(hipStreamSynchronize(m->stream));
+    if (want_logits && argmax_out) *argmax_out = m->st_host[1].token;
+    return 0;
+}
+
+int gsdh_generate_greedy(gsdh_model* m, const int* prompt, int n_prompt, int start_pos, int n_new, int* tokens_out,
+                         float* margins_out) {
+    if (!m->finalized) return fail(-1, "generate: model not finalized");
+    if (n_prompt <= 0 || n_new <= 0) return fail(-1, "generate: n_prompt %d n_new %d", n_prompt, n_new);
+    if (start_pos < 0 || start_pos + n_prompt + n_new - 1 > m->c.max_seq_len)
+        return fail(-1, "generate: positions %d..%d exceed max_seq_len %d", start_pos, start_pos + n_prompt + n_new - 1, m->c.max_seq_len);
+    for (int i = 0; i < n_prompt; i++)
+        if (prompt[i] < 0 || prompt[i] >= m->c.vocab) return fail(-1, "generate: prompt token %d outside vocab", prompt[i]);
+    StepState* ring = nullptr;
+    HIPCHK(hipHostMalloc((void**)&ring, sizeof(StepState) * (size_t)n_prompt, 0));
+    int rc = 0;
+    for (int i = 0; i < n_prompt && !rc; i++) {
+        ring[i].token = prompt[i]; ring[i].pos = start_pos + i; ring[i].gen_count = 0; ring[i].pad = 0;
+        hipError_t e = hipMemcpyAsync(m->st, &ring[i], sizeof(StepState), hipMemcpyHostToDevice, m->stream);
+        if (e == hipSuccess) e = hipGraphLaunch(i == n_prompt - 1 ? m->g_full : m->g_prefill, m->stream);
+        if (e != hipSuccess) rc = fail((int)e, "generate prefill: %s", hipGetErrorString(e));
+    }
+    for (int i = 1; i < n_new && !rc; i++) {
+        hipError_t e = hipGraphLaunch(m->g_full, m->stream);
+        if (e != hipSuccess) rc = fail((int)e, "generate decode: %s", hipGetErrorString(e));
+    }
+    if (!rc) {
+        hipError_t e = hipMemcpyAsync(tokens_out, m->gen_tok, (size_t)n_new * 4, hipMemcpyDeviceToHost, m->stream);
+        if (e == hipSuccess && margins_out) e = hipMemcpyAsync(margins_out, m->gen_margin, (size_t)n_new * 4, hipMemcpyDeviceToHost, m->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+        if (e != hipSuccess) rc = fail((int)e, "generate readback: %s", hipGetErrorString(e));
+    }
+    (void)hipStreamSynchronize(m->stream);
+    (void)hipHostFree(ring);
+    return rc;
+}
+
+int gsdh_model_run_linear(gsdh_model* m, int layer, int mask) {
+    if (layer < 0 || layer >= m->c.n_layers) return fail(-1, "run_linear: layer %d", layer);
+    return issue_linear(m, layer, mask);
+}
+
+int gsdh_model_capture_begin(gsdh_model* m) {
+    HIPCHK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+    return 0;
+}
+
+int gsdh_model_capture_end(gsdh_model* m, void** graph_exec_out) {
+    hipGraph_t g = nullptr;
+    HIPCHK(hipStreamEndCapture(m->stream, &g));
+    hipGraphExec_t ge = nullptr;
+    hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return fail((int)e, "hipGraphInstantiate: %s", hipGetErrorString(e));
+    *graph_exec_out = ge;
+    return 0;
+}
+
+int gsdh_graph_launch(gsdh_model* m, void* ge, int n) {
+    for (int i = 0; i < n; i++) HIPCHK(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(ge), m->stream));
+    return 0;
+}
+
+int gsdh_graph_destroy(void* ge) {
+    HIPCHK(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(ge)));
+    return 0;
+}
+
+void* gsdh_model_stream(gsdh_model* m) { return m ? (void*)m->stream : nullptr; }
+
+}  // extern "C"

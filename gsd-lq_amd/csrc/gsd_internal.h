@@ -1,0 +1,110 @@
+// gsd_internal.h -- launch interface between the kernels (gsd_kernels.hip) and
+// the C ABI / model runtime (gsd_capi.hip).  Internal to libgsdhip.so.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gsd {
+
+constexpr int kMaxSeg = 3;        // q, k, v share one launch
+constexpr int kMaxRank = 16;      // tmp_k scratch of the reference is 16 floats
+constexpr int kTableSlots = 256;  // LDS codebook slots (codes are u8)
+
+// One packed tensor of a fused matvec launch.  All pointers are device
+// pointers in the .gsd2 field layout (codes row-major u8 pairs, fp16 scales
+// per 64 weights, CSR kinks, U [rows,k], Vt [k,cols]).
+struct HexSeg {
+    const uint8_t* codes;
+    const uint16_t* scales;
+    const uint32_t* row_ptr;   // null: no kinks
+    const uint16_t* kcols;
+    const float* kdel;
+    const uint16_t* U;         // k > 0
+    const uint16_t* Vt;        // k > 0 and tmp_k == null: computed in-kernel
+    const float* S;
+    const float* tmp_k;        // k > 0: precomputed low-rank projection, or null
+    const float* table;        // float2 [n_pts]
+    float* out;
+    int rows, k, n_pts, batch0;
+};
+
+enum HexEpilogue : int {
+    kEpiStore = 0,     // out[r] = y[r]
+    kEpiResidual = 1,  // out[r] = resid[r] + y[r]          (x += W x')
+    kEpiSwiGLU = 2,    // seg0/seg1 paired rows: out[r] = silu(y0[r]) * y1[r]
+    kEpiRopeKV = 3,    // q/k/v segments: RoPE(q), RoPE(k) -> fp16 cache, v -> fp16 cache
+};
+
+// RoPE + KV append state for kEpiRopeKV (and the stand-alone rope kernel).
+struct RopeKV {
+    const float2* cs;       // [max_seq][hd/2] (cos, sin); row pos used
+    const int* pos_dev;     // device position (graph replay); null -> pos
+    int pos;
+    uint16_t* k_cache;
+    uint16_t* v_cache;
+    int layer, n_heads, n_kv, hd, max_seq, interleaved;
+};
+
+struct HexArgs {
+    HexSeg seg[kMaxSeg];
+    int nseg;
+    const float* x;        // input vector [cols]
+    const float* norm_w;   // non-null: input = rmsnorm(x) * norm_w
+    float eps;
+    float* resid;          // kEpiResidual target (read-modify-write)
+    int cols;
+    int nbatch;            // row batches in total
+    int epilogue;
+    RopeKV rope;
+};
+
+// Launches (all asynchronous on `stream`).
+hipError_t launch_hexmv(const HexArgs& a, hipStream_t stream);
+hipError_t launch_lowrank(const float* x, const uint16_t* Vt, const float* S, float* tmp_k,
+                          int k, int cols, hipStream_t stream);
+hipError_t launch_rmsnorm(const float* x, const float* w, float* out, int dim, float eps,
+                          hipStream_t stream);
+hipError_t launch_vec_add(float* y, const float* a, const float* b, int dim, hipStream_t stream);
+hipError_t launch_swiglu(const float* g, const float* u, float* out, int dim, hipStream_t stream);
+hipError_t launch_rope_kv(float* q, const float* k, const float* v, const RopeKV& r,
+                          const float2* cs_inline, hipStream_t stream);
+
+struct AttnArgs {
+    const float* q;
+    const uint16_t* k_cache;
+    const uint16_t* v_cache;
+    float* out;
+    const int* pos_dev;   // null -> pos
+    int pos;
+    int layer, n_heads, n_kv, hd, max_seq;
+    float sm_scale;
+    int chunk;            // positions per split
+    int max_splits;       // grid.y
+    float* ws;            // partials [n_kv][max_splits][group][2 + hd]
+    unsigned* counters;   // [n_kv], zero between launches
+};
+hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
+size_t attention_ws_floats(int n_kv, int max_splits, int group, int hd);
+
+hipError_t launch_embed(const uint16_t* embed, const int* token_dev, float* x, int hidden,
+                        hipStream_t stream);
+
+// Greedy argmax with the reference's nan_to_num (gsd_lq_cpu_runtime.py:423);
+// writes token to *tok_out, margin top1-top2 to *margin_out and, when
+// gen != null, appends both to gen arrays at *gen_count and advances the
+// step state (token_dev = argmax, pos_dev += 1).
+struct StepState {
+    int token;
+    int pos;
+    int gen_count;
+    int pad;
+};
+hipError_t launch_argmax(const float* logits, int n, StepState* st, int* gen_tokens,
+                         float* gen_margins, int advance, hipStream_t stream);
+hipError_t launch_fill_u32(unsigned* p, unsigned v, size_t n, hipStream_t stream);
+hipError_t launch_unpack(const uint8_t* codes, int64_t n, int radius, int32_t* idx,
+                         int8_t* r01, hipStream_t stream);
+
+int device_cu_count();
+
+}  // namespace gsd

@@ -1,0 +1,122 @@
+"""ctypes binding of libgsdhip.so (C ABI in include/gsdhip.h).
+
+There is no CPU fallback: loading fails with RuntimeError when the library is
+not built, and every call raises RuntimeError with the library's error text
+when it returns a nonzero status (the reference raised RuntimeError on OpenCL
+buffer/launch failures, gsd_lq_v2/run_gpu_native_chat.py:606-607,648-649).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(_PKG_DIR, "libgsdhip.so")
+
+vp, i32, i64, u64, f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_uint64, ctypes.c_float
+
+# name -> argtypes (restype int unless noted)
+SIGNATURES = {
+    "gsdh_device_info": [ctypes.c_char_p, i32, ctypes.POINTER(u64), ctypes.POINTER(i32)],
+    "gsdh_malloc": [ctypes.POINTER(vp), u64],
+    "gsdh_free": [vp],
+    "gsdh_memcpy_h2d": [vp, vp, u64, vp],
+    "gsdh_memcpy_d2h": [vp, vp, u64, vp],
+    "gsdh_stream_sync": [vp],
+    "gsdh_rmsnorm": [vp, vp, vp, vp, i32, f32],
+    "gsdh_vec_add": [vp, vp, vp, vp, i32],
+    "gsdh_swiglu": [vp, vp, vp, vp, i32],
+    "gsdh_lowrank_proj": [vp, vp, vp, vp, vp, i32, i32],
+    "gsdh_hex2d_matvec": [vp] + [vp] * 10 + [i32] * 4,
+    "gsdh_rope_and_store_kv": [vp] + [vp] * 5 + [i32] * 6 + [f32, i32],
+    "gsdh_gqa_attention": [vp] + [vp] * 4 + [i32] * 6 + [f32],
+    "gsdh_unpack_codes": [vp, vp, i64, i32, vp, vp],
+    "gsdh_model_create": [vp, ctypes.POINTER(vp)],
+    "gsdh_model_destroy": [vp],
+    "gsdh_model_set_embedding": [vp, vp],
+    "gsdh_model_set_norm": [vp, i32, i32, vp],
+    "gsdh_model_set_hex": [vp, i32, i32, i32, i32, i32, i32, vp, vp, vp, vp, vp, i64, vp, vp, vp],
+    "gsdh_model_finalize": [vp],
+    "gsdh_forward_token": [vp, i32, i32, i32, vp, ctypes.POINTER(i32)],
+    "gsdh_generate_greedy": [vp, vp, i32, i32, i32, vp, vp],
+    "gsdh_model_run_linear": [vp, i32, i32],
+    "gsdh_model_capture_begin": [vp],
+    "gsdh_model_capture_end": [vp, ctypes.POINTER(vp)],
+    "gsdh_graph_launch": [vp, vp, i32],
+    "gsdh_graph_destroy": [vp],
+}
+RESTYPES = {"gsdh_model_device_bytes": (u64, [vp]), "gsdh_model_stream": (vp, [vp]),
+            "gsdh_last_error": (ctypes.c_char_p, [])}
+
+
+class GsdModelConfig(ctypes.Structure):
+    _fields_ = [("n_layers", i32), ("hidden", i32), ("ffn", i32), ("n_heads", i32),
+                ("n_kv_heads", i32), ("head_dim", i32), ("vocab", i32), ("max_seq_len", i32),
+                ("rope_interleaved", i32), ("rms_eps", f32), ("rope_theta", f32)]
+
+
+SLOTS = {"attn_q": 0, "attn_k": 1, "attn_v": 2, "attn_output": 3, "ffn_gate": 4, "ffn_up": 5,
+         "ffn_down": 6, "output": 7}
+
+
+class HipError(RuntimeError):
+    pass
+
+
+class _Lib:
+    def __init__(self, path: str = LIB_PATH):
+        if not os.path.exists(path):
+            raise RuntimeError(f"HIP engine library {path} is not built (run __graft_entry__.build()); "
+                               "there is no CPU fallback")
+        self.path = path
+        self.cdll = ctypes.CDLL(path)
+        for name, args in SIGNATURES.items():
+            fn = getattr(self.cdll, name)
+            fn.argtypes = args
+            fn.restype = i32
+        for name, (rt, args) in RESTYPES.items():
+            fn = getattr(self.cdll, name)
+            fn.argtypes = args
+            fn.restype = rt
+
+    def last_error(self) -> str:
+        e = self.cdll.gsdh_last_error()
+        return e.decode() if e else ""
+
+    def __getattr__(self, name):
+        fn = getattr(self.cdll, name)
+        if name in SIGNATURES:
+            def call(*args):
+                rc = fn(*args)
+                if rc != 0:
+                    raise HipError(f"{name} failed ({rc}): {self.last_error()}")
+                return rc
+            return call
+        return fn
+
+
+_lib = None
+
+
+def lib() -> _Lib:
+    global _lib
+    if _lib is None:
+        _lib = _Lib()
+    return _lib
+
+
+def device_info():
+    name = ctypes.create_string_buffer(256)
+    total = u64(0)
+    ncu = i32(0)
+    lib().gsdh_device_info(name, 256, ctypes.byref(total), ctypes.byref(ncu))
+    return name.value.decode(errors="replace"), int(total.value), int(ncu.value)
+
+
+def ptr(a):
+    """Device pointer of a torch tensor, host pointer of a numpy array, or None."""
+    if a is None:
+        return None
+    if hasattr(a, "data_ptr"):
+        return ctypes.c_void_p(a.data_ptr())
+    return a.ctypes.data_as(ctypes.c_void_p)

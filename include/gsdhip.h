@@ -1,0 +1,169 @@
+/*
+ * gsdhip.h -- C ABI of libgsdhip.so, the MI355X (gfx950) GSD-LQ decode engine.
+ *
+ * Two layers:
+ *
+ *  1. Operator twins of the reference CPU engine (gsd_lq_v2/gsd_lq_cpu_engine.c).
+ *     Same names with a gsdh_ prefix, same argument order and meaning, plus a
+ *     leading stream argument; every pointer is a DEVICE pointer in the
+ *     reference's own data layout; the call is asynchronous on `stream`
+ *     (a hipStream_t, 0 = null stream) and returns 0 or a nonzero status
+ *     whose text gsdh_last_error() returns.  They replace the ctypes bindings
+ *     of gsd_lq_v2/gsd_lq_cpu_runtime.py:91-108 and the OpenCL kernels of
+ *     gsd_lq_v2/run_gpu_native_chat.py:101-421 one for one.
+ *
+ *  2. A model context that owns the packed weights in the engine's device
+ *     layout, the fp16 KV cache and the activations, and runs a whole token
+ *     (32 layers, ~195 kernels captured in one HIP graph) per call.  It replaces
+ *     GPUMistralV2Model.forward_token (run_gpu_native_chat.py:892-969) and the
+ *     per-kernel Python launches of _matvec_gpu (run_gpu_native_chat.py:858-890).
+ *
+ * No torch types cross this boundary: plain pointers, sizes and ints.
+ */
+#ifndef GSDHIP_H
+#define GSDHIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* Library status                                                            */
+/* ------------------------------------------------------------------------ */
+
+/* Text of the last error raised on the calling thread ("" if none). */
+const char* gsdh_last_error(void);
+
+/* Name and total memory of the current HIP device (the reference exposes the
+ * OpenCL device name and VRAM, run_gpu_native_chat.py:503-509). */
+int gsdh_device_info(char* name, int name_len, uint64_t* total_bytes, int* n_cu);
+
+/* Device memory helpers for callers without another allocator. */
+int gsdh_malloc(void** ptr, uint64_t nbytes);
+int gsdh_free(void* ptr);
+int gsdh_memcpy_h2d(void* dst, const void* src, uint64_t nbytes, void* stream);
+int gsdh_memcpy_d2h(void* dst, const void* src, uint64_t nbytes, void* stream);
+int gsdh_stream_sync(void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* 1. Operator twins of gsd_lq_cpu_engine.c                                  */
+/* ------------------------------------------------------------------------ */
+
+/* gsd_cpu_rmsnorm (gsd_lq_cpu_engine.c:66-82): out = x * (1/sqrtf(mean(x^2)+eps)) * w */
+int gsdh_rmsnorm(void* stream, const float* x, const float* weight, float* out, int dim, float eps);
+
+/* gsd_cpu_vec_add (gsd_lq_cpu_engine.c:84-94): y = a + b */
+int gsdh_vec_add(void* stream, float* y, const float* a, const float* b, int dim);
+
+/* gsd_cpu_swiglu (gsd_lq_cpu_engine.c:96-108): out = gate/(1+exp(-gate)) * up */
+int gsdh_swiglu(void* stream, const float* gate, const float* up, float* out, int dim);
+
+/* gsd_cpu_lowrank_proj (gsd_lq_cpu_engine.c:110-127):
+ * tmp_k[j] = S[j] * sum_c x[c] * fp16(Vt[j,c]), j < k_dim <= 16 */
+int gsdh_lowrank_proj(void* stream, const float* x, const uint16_t* Vt, const float* S,
+                      float* tmp_k, int k_dim, int cols);
+
+/* gsd_cpu_hex2d_matvec (gsd_lq_cpu_engine.c:129-183):
+ * y[r] = sum_p (T[code].x*x[2p] + T[code].y*x[2p+1]) * fp16(scale[r*cols/64 + p/32])
+ *      + sum_{kinks of r} delta * x[col] + sum_j fp16(U[r,j]) * tmp_k[j]
+ * codes: u8 [rows*cols/2]; scales: fp16 bits [rows*cols/64]; xy_table: float2
+ * [n_pts]; cols must be a positive multiple of 64 and n_pts <= 256. */
+int gsdh_hex2d_matvec(void* stream, const float* x, const uint8_t* codes, const uint16_t* scales,
+                      const float* xy_table, const uint16_t* U, const float* tmp_k,
+                      const uint32_t* kink_row_ptr, const uint16_t* kink_cols,
+                      const float* kink_deltas, float* y, int rows, int cols, int k_dim, int n_pts);
+
+/* gsd_cpu_rope_and_store_kv (gsd_lq_cpu_engine.c:185-262): rotates q in place
+ * and k, stores fp16(k') and fp16(v) at cache[((layer*max_seq+pos)*n_kv+h)*hd+d].
+ * cos/sin are evaluated on the host with the C library exactly as the
+ * reference does, so the cache bits match it for equal inputs. */
+int gsdh_rope_and_store_kv(void* stream, float* q, const float* k, const float* v,
+                           uint16_t* k_cache, uint16_t* v_cache, int layer_idx, int pos,
+                           int n_heads, int n_kv_heads, int head_dim, int max_seq_len,
+                           float rope_theta, int interleaved);
+
+/* gsd_cpu_gqa_attention (gsd_lq_cpu_engine.c:264-330): softmax(q.K/scale)V
+ * over cached positions 0..pos, split over the context (flash-decoding);
+ * head_dim must be a multiple of 8, <= 256; n_heads/n_kv_heads <= 8. */
+int gsdh_gqa_attention(void* stream, const float* q, const uint16_t* k_cache,
+                       const uint16_t* v_cache, float* attn_out, int layer_idx, int pos,
+                       int n_heads, int n_kv_heads, int head_dim, int max_seq_len, float sm_scale);
+
+/* Bit-exact unpack of codes: idx[i] = codes[i], r01[2i..2i+1] = integer
+ * lattice fields (r0, r1) of codeword idx[i] in the radius-R enumeration.
+ * Used to check the device decode path (no reference counterpart; the
+ * enumeration is gsd_lq_cpu_runtime.py:111-118). */
+int gsdh_unpack_codes(void* stream, const uint8_t* codes, int64_t n, int radius,
+                      int32_t* idx_out, int8_t* r01_out);
+
+/* ------------------------------------------------------------------------ */
+/* 2. Model context (replaces GPUMistralV2Model's device side)              */
+/* ------------------------------------------------------------------------ */
+
+typedef struct gsdh_model gsdh_model;
+
+typedef struct gsdh_model_config {
+    int n_layers, hidden, ffn, n_heads, n_kv_heads, head_dim, vocab;
+    int max_seq_len;          /* KV capacity (reference: 2048) */
+    int rope_interleaved;     /* 1 = (2i, 2i+1) pairs, 0 = (i, i+hd/2) */
+    float rms_eps, rope_theta;
+} gsdh_model_config;
+
+/* Tensor slots of a layer, in the order of run_gpu_native_chat.py:822-828. */
+enum { GSDH_Q = 0, GSDH_K, GSDH_V, GSDH_O, GSDH_GATE, GSDH_UP, GSDH_DOWN, GSDH_LM_HEAD };
+
+int gsdh_model_create(const gsdh_model_config* cfg, gsdh_model** out);
+int gsdh_model_destroy(gsdh_model* m);
+
+/* Dense tensors from host memory.  embed: fp16 bits [vocab, hidden];
+ * norms: f32 [hidden]; layer = -1 for output_norm. */
+int gsdh_model_set_embedding(gsdh_model* m, const uint16_t* embed_f16);
+int gsdh_model_set_norm(gsdh_model* m, int layer, int which /*0 attn, 1 ffn*/, const float* w);
+
+/* A packed tensor from host memory in .gsd2 layout (fields as in the file).
+ * layer is ignored for GSDH_LM_HEAD.  Validates shapes and that every code is
+ * < n_pts; transcodes into the engine's device layout. */
+int gsdh_model_set_hex(gsdh_model* m, int layer, int slot, int radius, int rows, int cols,
+                       int k_dim, const uint8_t* codes, const uint16_t* scales,
+                       const uint32_t* row_ptr, const uint16_t* kink_cols,
+                       const float* kink_deltas, int64_t nk, const uint16_t* U, const float* S,
+                       const uint16_t* Vt);
+
+/* After every tensor is set: checks completeness, builds the RoPE tables and
+ * the per-token HIP graph. */
+int gsdh_model_finalize(gsdh_model* m);
+
+/* Device bytes held by the model (weights + KV cache + activations). */
+uint64_t gsdh_model_device_bytes(gsdh_model* m);
+
+/* One token through every layer at position pos; when want_logits, copies the
+ * vocab-sized f32 logits into logits_host (may be NULL to skip the copy) and
+ * returns the greedy token (first argmax) in *argmax_out (may be NULL). */
+int gsdh_forward_token(gsdh_model* m, int token_id, int pos, int want_logits,
+                       float* logits_host, int* argmax_out);
+
+/* Prefill prompt[0..n_prompt) at positions start_pos.., then n_new greedy
+ * steps entirely on the device; writes the generated ids and the top1-top2
+ * logit margin of every step. */
+int gsdh_generate_greedy(gsdh_model* m, const int* prompt, int n_prompt, int start_pos, int n_new,
+                         int* tokens_out, float* margins_out);
+
+/* Benchmark hook: runs the model's matvec launches of `layer` (mask bit i =
+ * launch i of {qkv, o, gate+up, down}) on the model stream with the current
+ * activations, without attention or synchronisation. */
+int gsdh_model_run_linear(gsdh_model* m, int layer, int mask);
+
+/* Graph capture of an arbitrary sequence of the model's own launches on its
+ * stream, for timing: begin, issue calls, end -> replay n times. */
+int gsdh_model_capture_begin(gsdh_model* m);
+int gsdh_model_capture_end(gsdh_model* m, void** graph_exec_out);
+int gsdh_graph_launch(gsdh_model* m, void* graph_exec, int n_times);
+int gsdh_graph_destroy(void* graph_exec);
+void* gsdh_model_stream(gsdh_model* m);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GSDHIP_H */

@@ -1,0 +1,192 @@
+"""CPU tests of the host side: the .gsd2 container, the encoder, the
+synthetic generator and the C ABI surface of the engine library."""
+import ctypes
+import os
+import re
+import struct
+
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import ROOT
+
+from gsdlq import codebook, gsd2, pack, synth
+
+
+def _tiny_spec(**kw):
+    d = dict(n_layers=2, hidden=128, ffn=256, n_heads=4, n_kv_heads=2, head_dim=32, vocab=300,
+             mode="precision", kinks_per_row=2)
+    d.update(kw)
+    return synth.SynthSpec(**d)
+
+
+def test_gsd2_roundtrip_and_reference_reader(tmp_path):
+    """Writer output is read back identically by the product reader and by
+    the oracle's independent reader of the reference layout."""
+    spec = _tiny_spec()
+    path = str(tmp_path / "m.gsd2")
+    nks = synth.write_gsd2(spec, path)
+    src = synth.SynthSource(spec)
+    f = gsd2.Gsd2File(path)
+    o = O.FileSource(path)
+    assert f.config == src.config == o.config
+    assert 0 < f.header["avg_bpw"] < 8
+    for name, meta in f.tensors.items():
+        if "radius" in meta:
+            assert nks[name] == meta["kink_cols"]["nbytes"] // 2
+            for fld in gsd2.HEX_FIELDS + (gsd2.LOWRANK_FIELDS if meta["k_dim"] else ()):
+                a, b = f.hex_field(name, fld), src.hex_field(name, fld)
+                assert np.array_equal(a, b) and np.array_equal(o.hex_field(name, fld), b), (name, fld)
+        else:
+            dt = np.float16 if name == "token_embd.weight" else np.float32
+            assert np.array_equal(f.dense(name, dt), src.dense(name, dt))
+    f.close()
+
+
+def test_gsd2_bad_magic_and_truncation(tmp_path):
+    p = tmp_path / "bad.gsd2"
+    p.write_bytes(b"GSD1" + struct.pack("<Q", 2) + b"{}")
+    with pytest.raises(ValueError, match="Invalid GSD2 magic"):
+        gsd2.Gsd2File(str(p))
+    p.write_bytes(b"GSD2" + struct.pack("<Q", 100) + b"{}")
+    with pytest.raises(ValueError, match="Truncated"):
+        gsd2.Gsd2File(str(p))
+    hdr = b'{"config": {}, "tensors": {"t": {"data": {"offset": 0, "nbytes": 64}}}}'
+    p.write_bytes(b"GSD2" + struct.pack("<Q", len(hdr)) + hdr + b"\0" * 8)
+    f = gsd2.Gsd2File(str(p))
+    with pytest.raises(ValueError, match="beyond end"):
+        f.dense("t", np.float32)
+
+
+@pytest.mark.parametrize("R", [6, 8])
+def test_encoder_picks_nearest_hexagon_point(R):
+    """Every code is the nearest codebook point (brute force over all points)
+    of the pair scaled by its block scale, and the scale is the fp16 round-up
+    of max hexnorm / R."""
+    W = pack.synth_bf16(1, 2, 8 * 256).reshape(8, 256)
+    f = pack.pack_tensor(W, R)
+    xy = codebook.xy_table(R).astype(np.float64)
+    n_pts = codebook.n_points(R)
+    assert f["codes"].max() < n_pts
+    s = f["scales"].view(np.float16).astype(np.float64)
+    pairs = W.reshape(-1, 2).astype(np.float64)
+    sc = np.repeat(s, 32)
+    target = pairs / sc[:, None]
+    d = ((target[:, None, :] - xy[None, :, :]) ** 2).sum(-1)
+    best = d.min(1)
+    chosen = d[np.arange(len(d)), f["codes"].astype(int)]
+    assert np.all(chosen <= best + 1e-9)
+    b = pairs[:, 1] / (np.sqrt(3) / 2)
+    a = pairs[:, 0] - 0.5 * b
+    hn = np.maximum(np.abs(a), np.maximum(np.abs(b), np.abs(a + b))).reshape(-1, 32).max(1)
+    need = hn / R
+    assert np.all(s >= need * (1 - 1e-12))
+    below = np.nextafter(s.astype(np.float16), np.float16(0)).astype(np.float64)
+    assert np.all(below < need)
+
+
+def test_encoder_error_kinks_lowrank():
+    W = pack.synth_bf16(0, 9, 64 * 512).reshape(64, 512)
+    f0 = pack.pack_tensor(W, 8)
+    e0 = np.linalg.norm(pack.dequantize(f0) - W)
+    f1 = pack.pack_tensor(W, 8, 0, 4)
+    assert f1["nk"] == 64 * 4 and np.all(np.diff(f1["row_ptr"].astype(int)) == 4)
+    e1 = np.linalg.norm(pack.dequantize(f1) - W)
+    assert e1 < e0
+    f2 = pack.pack_tensor(W, 6, 4, 0, lr_iters=3)
+    e2a = np.linalg.norm(pack.dequantize(f2, include_lowrank=False) - W)
+    e2b = np.linalg.norm(pack.dequantize(f2) - W)
+    assert e2b < e2a
+    assert np.linalg.norm(W) * 0.2 > e0    # 4.25 bpw keeps ~10% relative error on Gaussian weights
+
+
+def test_encoder_deterministic_and_threads():
+    W = pack.synth_bf16(5, 5, 128 * 256).reshape(128, 256)
+    a = pack.pack_tensor(W, 6, 2, 2)
+    b = pack.pack_tensor(W, 6, 2, 2)
+    for k in ("codes", "scales", "row_ptr", "kink_cols", "kink_deltas", "U", "S", "Vt"):
+        assert np.array_equal(a[k], b[k])
+
+
+def test_encoder_rejects_bad_shapes():
+    with pytest.raises(ValueError, match="multiple of 64"):
+        pack.pack_tensor(np.zeros((2, 96), np.float32), 8)
+    with pytest.raises(ValueError, match="k_dim"):
+        pack.pack_tensor(np.zeros((2, 64), np.float32), 8, 17)
+
+
+def test_synth_generator_reproducible_and_gaussian():
+    a = pack.synth_bf16(0, 7, 1 << 20)
+    assert np.array_equal(a, pack.synth_bf16(0, 7, 1 << 20))
+    assert np.array_equal(a[1000:2000], pack.synth_bf16(0, 7, 1000, offset=1000))
+    assert np.all((a.view(np.uint32) & 0xFFFF) == 0)        # bf16-representable
+    assert abs(a.std() - 0.02) < 2e-4 and abs(a.mean()) < 1e-4
+    # numpy restatement of the counter-based generator (splitmix64 + Irwin-Hall(12))
+    M = np.uint64(0xFFFFFFFFFFFFFFFF)
+
+    def sm(x):
+        with np.errstate(over="ignore"):
+            x = (x + np.uint64(0x9E3779B97F4A7C15)) & M
+            x = ((x ^ (x >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)) & M
+            x = ((x ^ (x >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)) & M
+            return x ^ (x >> np.uint64(31))
+    with np.errstate(over="ignore"):
+        key = sm(np.uint64(0) ^ sm(np.uint64(7) + np.uint64(0x632BE59BD9B4E019)))
+        i = np.arange(4096, dtype=np.uint64)
+        s = np.zeros(4096, np.int64)
+        for j in range(3):
+            h = sm(key + np.uint64(3) * i + np.uint64(j))
+            for q in range(4):
+                s += ((h >> np.uint64(16 * q)) & np.uint64(0xFFFF)).astype(np.int64)
+    z = (s - 393210).astype(np.float32) * np.float32(0.02 / 65536)
+    u = z.view(np.uint32)
+    u = (u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) & np.uint32(0xFFFF0000)
+    assert np.array_equal(u.view(np.float32), a[:4096])
+
+
+def test_abi_exports_every_declared_symbol():
+    """libgsdhip.so loads without a GPU and exports every entry point that
+    include/gsdhip.h declares."""
+    from gsdlq import build
+    if not os.path.exists(build.HIP_LIB):
+        pytest.skip("libgsdhip.so not built (run __graft_entry__.build())")
+    hdr = open(os.path.join(ROOT, "include", "gsdhip.h")).read()
+    declared = set(re.findall(r"\b(gsdh_\w+)\s*\(", hdr))
+    assert len(declared) >= 25
+    lib = ctypes.CDLL(build.HIP_LIB)
+    missing = [s for s in sorted(declared) if not hasattr(lib, s)]
+    assert not missing
+    from gsdlq import hip
+    assert set(hip.SIGNATURES) | set(hip.RESTYPES) >= declared
+
+
+def test_dropin_modules_import_and_surface():
+    import gsd_lq_cpu_runtime as cpu_rt
+    import run_gpu_native_chat as chat
+    for name in ("GPUMistralV2Model", "MistralSentencePieceTokenizer", "format_mistral_prompt", "run_smoke_verify",
+                 "main", "MAX_SEQ_LEN", "ensure_model_file", "_get_turbo_codebook"):
+        assert hasattr(chat, name)
+    for name in ("build_c_library", "CPUEngine", "CPUMistralV2Model", "MAX_SEQ_LEN", "_get_turbo_codebook"):
+        assert hasattr(cpu_rt, name)
+    assert chat.MAX_SEQ_LEN == cpu_rt.MAX_SEQ_LEN == 2048
+    t, n = chat._get_turbo_codebook(8)
+    assert n == 217 and t.dtype == np.float32
+    p = chat.format_mistral_prompt([("a", "b")], "c")
+    assert p.startswith("[INST] ") and p.endswith("[INST] c [/INST]") and "</s>" in p
+
+
+def test_tokenizer_roundtrip_placeholder_vocab():
+    import run_gpu_native_chat as chat
+    toks, scores, types = synth.placeholder_vocab(600)
+    pieces = {"▁": 0.0, "h": 0.0, "e": 0.0, "l": 0.0, "o": 0.0, "▁h": 4.5, "▁he": 5.0, "ll": 4.0, "llo": 3.5,
+              "▁hello": 6.0}
+    for i, (tk, sc) in enumerate(pieces.items()):
+        toks[300 + i], scores[300 + i], types[300 + i] = tk, sc, 1
+    t = chat.MistralSentencePieceTokenizer(toks, scores, types, 1, 2)
+    ids = t.encode("hello", add_bos=True)
+    assert ids == [1, 300 + list(pieces).index("▁hello")]
+    assert t.decode(ids).strip() == "hello"
+    ids = t.encode("</s>é")
+    assert 2 in ids
+    assert t.decode(ids).strip() == "é"

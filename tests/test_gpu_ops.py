@@ -1,0 +1,160 @@
+"""Operator parity on the GPU: each C-ABI twin against the oracle on the same
+seeded inputs.  Bar: bit-exact for integer decode and for RoPE/KV append
+(whose arithmetic is fixed by the reference), 1e-3 relative L2 for matvec and
+attention (fp32 accumulation in a different order)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import rel_l2
+from gpu_util import D, E, H, banner, p
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def lib():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    from gsdlq import hip
+    return hip.lib()
+
+
+def _pack(rows, cols, R, k=0, kpr=0, seed=1):
+    from gsdlq import pack
+    W = pack.synth_bf16(seed, rows * 13 + cols, rows * cols).reshape(rows, cols)
+    return pack.pack_tensor(W, R, k, kpr)
+
+
+def _gpu_matvec(lib, f, x, tmp_k=None):
+    rows, cols, k = f["rows"], f["cols"], f["k_dim"]
+    xy, n_pts = O.codebook(f["radius"])
+    y = E(rows * 4)
+    tk = None
+    if k:
+        tk = D(np.asarray(tmp_k, np.float32))
+    bufs = {key: D(f[key]) for key in ("codes", "scales", "row_ptr", "kink_cols", "kink_deltas", "U")}
+    lib.gsdh_hex2d_matvec(None, p(D(x)), p(bufs["codes"]), p(bufs["scales"]), p(D(xy)), p(bufs["U"]) if k else None,
+                          p(tk), p(bufs["row_ptr"]), p(bufs["kink_cols"]), p(bufs["kink_deltas"]), p(y), rows, cols,
+                          k, n_pts)
+    return H(y, np.float32, rows)
+
+
+MV_CASES = [(64, 128, 8, 0, 2), (37, 192, 8, 0, 1), (1, 64, 6, 0, 0), (4096, 4096, 8, 0, 0),
+            (1024, 4096, 6, 2, 3), (4096, 14336, 8, 0, 0), (300, 1024, 6, 16, 4), (14336, 4096, 6, 2, 0)]
+
+
+@pytest.mark.parametrize("rows,cols,R,k,kpr", MV_CASES)
+def test_hex2d_matvec_vs_oracle(lib, rows, cols, R, k, kpr):
+    banner(f"matvec {rows}x{cols} R{R} k{k} kinks/row {kpr}")
+    f = _pack(rows, cols, R, k, kpr)
+    x = np.random.default_rng(rows + cols).standard_normal(cols).astype(np.float32)
+    tk = None
+    if k:
+        tk = np.zeros(16, np.float32)
+        O.load("port").gsd_cpu_lowrank_proj(O.P(x), O.P(f["Vt"]), O.P(f["S"]), O.P(tk), k, cols)
+        tk = tk[:k]
+    want = O.hex2d_matvec(x, f, tmp_k=tk)
+    got = _gpu_matvec(lib, f, x, tk)
+    assert rel_l2(got, want) < TOL
+    assert rel_l2(got, want) < 1e-5   # fp32 accumulation order only
+
+
+@pytest.mark.parametrize("tag", ["turbo", "prec"])
+def test_hex2d_matvec_golden(lib, golden, tag):
+    rows, cols, R, k = (int(v) for v in golden[f"mv_{tag}_shape"])
+    f = {key: golden[f"mv_{tag}_{key}"] for key in ("codes", "scales", "row_ptr", "kink_cols", "kink_deltas",
+                                                    "U", "S", "Vt")}
+    f.update(rows=rows, cols=cols, radius=R, k_dim=k)
+    x = golden[f"mv_{tag}_x"]
+    tk = None
+    if k:
+        tk = np.zeros(16, np.float32)
+        O.load("port").gsd_cpu_lowrank_proj(O.P(x), O.P(f["Vt"]), O.P(f["S"]), O.P(tk), k, cols)
+        tk = tk[:k]
+    assert rel_l2(_gpu_matvec(lib, f, x, tk), golden[f"mv_{tag}_y"]) < TOL
+
+
+def test_hex2d_matvec_rejects_bad_shapes(lib):
+    from gsdlq.hip import HipError
+    y = E(64)
+    with pytest.raises(HipError, match="multiple of 64"):
+        lib.gsdh_hex2d_matvec(None, p(y), p(y), p(y), p(y), None, None, p(y), p(y), p(y), p(y), 4, 96, 0, 217)
+    with pytest.raises(HipError, match="n_pts"):
+        lib.gsdh_hex2d_matvec(None, p(y), p(y), p(y), p(y), None, None, p(y), p(y), p(y), p(y), 4, 64, 0, 300)
+
+
+@pytest.mark.parametrize("R", [6, 8])
+def test_unpack_codes_bitexact(lib, R):
+    from gsdlq import codebook
+    n_pts = codebook.n_points(R)
+    codes = np.concatenate([np.arange(n_pts, dtype=np.uint8),
+                            np.random.default_rng(R).integers(0, n_pts, 100000).astype(np.uint8)])
+    idx, r01 = E(codes.size * 4), E(codes.size * 2)
+    lib.gsdh_unpack_codes(None, p(D(codes)), codes.size, R, p(idx), p(r01))
+    assert np.array_equal(H(idx, np.int32, codes.size), codes.astype(np.int32))
+    want = codebook.integer_fields(R)[codes]
+    assert np.array_equal(H(r01, np.int8, codes.size * 2).reshape(-1, 2), want)
+
+
+def test_lowrank_rmsnorm_swiglu_add(lib, golden):
+    g = golden
+    tk = E(64)
+    lib.gsdh_lowrank_proj(None, p(D(g["lr_x"])), p(D(g["lr_Vt"])), p(D(g["lr_S"])), p(tk), 4, 256)
+    assert rel_l2(H(tk, np.float32, 4), g["lr_out"]) < 1e-6
+    out = E(4096 * 4)
+    lib.gsdh_rmsnorm(None, p(D(g["rms_x"])), p(D(g["rms_w"])), p(out), 4096, 1e-5)
+    assert rel_l2(H(out, np.float32, 4096), g["rms_out"]) < 1e-6
+    out = E(4000)
+    lib.gsdh_swiglu(None, p(D(g["sw_gate"])), p(D(g["sw_up"])), p(out), 1000)
+    assert rel_l2(H(out, np.float32, 1000), g["sw_out"]) < 1e-6
+    lib.gsdh_vec_add(None, p(out), p(D(g["sw_gate"])), p(D(g["sw_up"])), 1000)
+    assert np.array_equal(H(out, np.float32, 1000), g["add_out"])
+
+
+@pytest.mark.parametrize("pos", [0, 7, 2047])
+@pytest.mark.parametrize("il", [1, 0])
+def test_rope_kv_bitexact(lib, golden, pos, il):
+    t = f"rope_p{pos}_i{il}"
+    q = D(golden[t + "_q"])
+    kc, vc = E(2048 * 8 * 128 * 2), E(2048 * 8 * 128 * 2)
+    lib.gsdh_rope_and_store_kv(None, p(q), p(D(golden[t + "_k"])), p(D(golden[t + "_v"])), p(kc), p(vc), 0, pos,
+                               32, 8, 128, 2048, 1e6, il)
+    assert np.array_equal(H(q, np.uint32), golden[t + "_qout"].view(np.uint32))
+    assert np.array_equal(H(kc, np.uint16).reshape(2048, 8, 128)[pos], golden[t + "_kc"])
+    assert np.array_equal(H(vc, np.uint16).reshape(2048, 8, 128)[pos], golden[t + "_vc"])
+
+
+@pytest.mark.parametrize("ctx", [1, 33, 512])
+def test_attention_golden(lib, golden, ctx):
+    from make_golden import attn_cache
+    kc, vc = attn_cache(ctx, "k", 512, 8, 128), attn_cache(ctx, "v", 512, 8, 128)
+    out = E(32 * 128 * 4)
+    lib.gsdh_gqa_attention(None, p(D(golden[f"attn{ctx}_q"])), p(D(kc)), p(D(vc)), p(out), 0, ctx - 1, 32, 8,
+                           128, 512, 1.0 / float(np.sqrt(128)))
+    assert rel_l2(H(out, np.float32, 32 * 128), golden[f"attn{ctx}_out"]) < TOL
+
+
+@pytest.mark.parametrize("ctx,nh,nkv,hd,layers", [(2048, 32, 8, 128, 2), (8192, 32, 8, 128, 1), (100, 8, 8, 64, 1),
+                                                  (777, 16, 2, 256, 1), (4000, 32, 8, 128, 1)])
+def test_attention_vs_oracle(lib, ctx, nh, nkv, hd, layers):
+    banner(f"attention ctx {ctx} heads {nh}/{nkv} hd {hd}")
+    from gsdlq import pack
+    ms = ctx + 5
+    kc = pack.synth_f16(21, ctx, layers * ms * nkv * hd, 1.0)
+    vc = pack.synth_f16(22, ctx, layers * ms * nkv * hd, 1.0)
+    q = np.random.default_rng(ctx).standard_normal(nh * hd).astype(np.float32)
+    want = np.zeros(nh * hd, np.float32)
+    layer = layers - 1
+    O.load("port").gsd_cpu_gqa_attention(O.P(q), O.P(kc), O.P(vc), O.P(want), layer, ctx - 1, nh, nkv, hd, ms,
+                                         1.0 / float(np.sqrt(hd)))
+    out = E(nh * hd * 4)
+    dk, dv, dq = D(kc), D(vc), D(q)
+    for _ in range(2):   # twice: the split counters must be reset by the kernel itself
+        lib.gsdh_gqa_attention(None, p(dq), p(dk), p(dv), p(out), layer, ctx - 1, nh, nkv, hd, ms,
+                               1.0 / float(np.sqrt(hd)))
+        assert rel_l2(H(out, np.float32, nh * hd), want) < TOL
