@@ -1,0 +1,253 @@
+"""Benchmark of the GSD-LQ batch-1 decode path on one MI355X.
+
+Workload (the metric's configuration): the full Mistral-7B linear set of one
+layer -- q 4096x4096, k/v 1024x4096, o 4096x4096, gate/up 14336x4096,
+down 4096x14336 -- packed in Turbo mode (radius 8, ~4.26 bpw), batch 1, fp32
+activations.  A step is one pass of the layer's fused unpack-matvec launches
+(qkv with fused RMSNorm, o + residual, gate/up with fused RMSNorm + SwiGLU,
+down + residual).  Steps rotate over `--layers` distinct packed layers
+(> 256 MB) so the Infinity Cache cannot serve the weights, and are timed with
+HIP events around a captured HIP graph on the engine's stream.
+
+value = algorithmic bytes per step / time per step (GB/s), bytes as in the
+reference format: codes + fp16 scales + row_ptr + 6 B per kink + low-rank
+factors + x (4 B/col) + y (4 B/row), each stream counted once.
+
+Also reported: the same for Precision mode (radius 6, rank 2; the file's u8
+codes), the dominant kernel's roofline (the fused gate/up launch, 2 x
+14336x4096), end-to-end greedy decode tok/s of a 32-layer 7B-shaped model,
+and the reference CPU engine timed on this host's cores on a bounded sample.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3]
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "gsd-lq_amd"))
+
+HBM_PEAK_GBS = 8000.0
+H, F, KV, V = 4096, 14336, 1024, 32768
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def layer_shapes():
+    return {"attn_q": (H, H), "attn_k": (KV, H), "attn_v": (KV, H), "attn_output": (H, H),
+            "ffn_gate": (F, H), "ffn_up": (F, H), "ffn_down": (H, F)}
+
+
+def alg_bytes(f):
+    """Algorithmic bytes of one fused matvec over packed tensor f."""
+    rows, cols, k = f["rows"], f["cols"], f["k_dim"]
+    b = f["codes"].nbytes + f["scales"].nbytes + f["row_ptr"].nbytes + 6 * f["nk"]
+    if k:
+        b += 2 * rows * k + 2 * k * cols + 4 * k
+    return b + 4 * cols + 4 * rows
+
+
+class LayerBank:
+    """Distinct packed 7B layers (each tensor packed from its own seed) plus
+    an lm_head; a `copies` option repeats the distinct layers to fill a
+    32-layer model for the end-to-end decode timing."""
+
+    def __init__(self, mode: str, n_distinct: int):
+        from gsdlq import synth
+        self.spec = synth.SynthSpec(n_layers=n_distinct, mode=mode)
+        self.mode = mode
+        self.n = n_distinct
+        self.packed = {}
+        t0 = time.time()
+        for l in range(n_distinct):
+            for t in layer_shapes():
+                self.packed[(l, t)] = synth.pack_synth(self.spec, f"blk.{l}.{t}.weight")
+            log(f"{mode}: packed layer {l + 1}/{n_distinct} ({time.time() - t0:.0f}s)")
+        self.packed["lm"] = synth.pack_synth(self.spec, "output.weight")
+        self.layer_bytes = [sum(alg_bytes(self.packed[(l, t)]) for t in layer_shapes()) for l in range(n_distinct)]
+
+
+class BankSource:
+    """Gsd2File-like source serving LayerBank tensors, layer l -> bank l % n."""
+
+    def __init__(self, bank: LayerBank, n_layers: int):
+        from gsdlq import synth
+        spec = synth.SynthSpec(n_layers=n_layers, mode=bank.mode)
+        self.src = synth.SynthSource(spec)
+        self.config = self.src.config
+        self.tensors = self.src.tensors
+        self.bank = bank
+        self.header = {"avg_bpw": None}
+
+    def dense(self, name, dtype):
+        return self.src.dense(name, dtype)
+
+    def hex_field(self, name, field):
+        if name == "output.weight":
+            return self.bank.packed["lm"][field]
+        parts = name.split(".")
+        return self.bank.packed[(int(parts[1]) % self.bank.n, parts[2])][field]
+
+
+def build_model(bank, n_layers, max_seq=256):
+    import run_gpu_native_chat as chat
+    return chat.GPUMistralV2Model(BankSource(bank, n_layers), max_seq_len=max_seq, verbose=False)
+
+
+def capture(model, fn):
+    lib = model.cl.lib
+    lib.gsdh_model_capture_begin(model._m)
+    try:
+        fn()
+    finally:
+        ge = ctypes.c_void_p()
+        lib.gsdh_model_capture_end(model._m, ctypes.byref(ge))
+    return ge
+
+
+def time_graph(model, ge, n):
+    ms = ctypes.c_float()
+    model.cl.lib.gsdh_graph_time(model._m, ge, n, ctypes.byref(ms))
+    return ms.value
+
+
+def bench_linear(bank, steps, warmup):
+    """GB/s of the layer linear set; returns (gbs, ms_per_step, roofline dict)."""
+    model = build_model(bank, bank.n)
+    lib = model.cl.lib
+    model.forward_token(1, 0)   # realistic activations in every buffer
+    L = bank.n
+    ge = capture(model, lambda: [lib.gsdh_model_run_linear(model._m, l, 15) for l in range(L)])
+    time_graph(model, ge, max(1, warmup))
+    reps = max(1, steps // L)
+    ms = time_graph(model, ge, reps)
+    n_steps = reps * L
+    ms_step = ms / n_steps
+    gbs = sum(bank.layer_bytes) * reps / (ms * 1e-3) / 1e9
+    # dominant kernel: fused gate+up (2 x 14336 x 4096), timed alone
+    gu = capture(model, lambda: [lib.gsdh_model_run_linear(model._m, l, 4) for l in range(L)])
+    time_graph(model, gu, 2)
+    gms = time_graph(model, gu, reps)
+    per_launch_ms = gms / (reps * L)
+    gu_bytes = sum(alg_bytes(bank.packed[(l, t)]) for l in range(L) for t in ("ffn_gate", "ffn_up")) / L
+    gu_bytes -= 4 * H   # gate and up read the same x once
+    ach = gu_bytes / (per_launch_ms * 1e-3) / 1e9
+    roof = {"kernel": "hexmv_kernel (fused RMSNorm + gate/up matvec + SwiGLU, 2x14336x4096)",
+            "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+            "launch_us": round(per_launch_ms * 1e3, 2), "alg_bytes_per_launch": int(gu_bytes)}
+    for g in (ge, gu):
+        lib.gsdh_graph_destroy(g)
+    model.close()
+    return gbs, ms_step, roof
+
+
+def bench_decode(bank, n_prompt=64, n_new=128):
+    """Greedy decode tok/s of a 32-layer 7B-shaped model (layers are copies of
+    the bank's distinct layers, each copy its own HBM allocation)."""
+    model = build_model(bank, 32, max_seq=n_prompt + n_new + 8)
+    prompt = np.random.default_rng(4).integers(0, V, n_prompt).tolist()
+    model.generate_greedy(prompt[:8], 4)   # warm
+    lib = model.cl.lib
+    t0 = time.time()
+    toks, _ = model.generate_greedy(prompt, n_new)
+    total = time.time() - t0
+    # decode-only rate: time n_new steps with a 1-token prefill
+    t0 = time.time()
+    model.generate_greedy(prompt[:1], n_new)
+    dec = time.time() - t0
+    model.close()
+    return {"decode_tok_s": round(n_new / dec, 1), "prompt_plus_decode_s": round(total, 3),
+            "n_prompt": n_prompt, "n_new": n_new}
+
+
+def cpu_baseline(bank, seconds=12.0):
+    """The reference CPU engine (built from its source into oracle/_ref; the
+    oracle restatement if absent) on one Turbo layer's 7 matvecs, repeated for
+    a bounded time on all host cores."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    kind = "reference" if O.have_reference() else "port"
+    x = np.random.default_rng(1).standard_normal(F).astype(np.float32)
+    fs = [bank.packed[(0, t)] for t in layer_shapes()]
+    for f in fs:   # warm
+        O.hex2d_matvec(x[:f["cols"]], f, kind=kind)
+    t0 = time.time()
+    n = 0
+    while time.time() - t0 < seconds:
+        for f in fs:
+            O.hex2d_matvec(x[:f["cols"]], f, kind=kind)
+        n += 1
+    dt = time.time() - t0
+    return {"value": round(bank.layer_bytes[0] * n / dt / 1e9, 3), "unit": "GB/s",
+            "cores": int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)), "kind": kind,
+            "sample": f"{n} passes over one Turbo 7B layer's 7 matvecs ({dt:.1f}s), gsd_cpu_hex2d_matvec "
+                      f"built with the reference flags (clang -O3 -fopenmp)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=40)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=8, help="distinct packed layers rotated (Turbo)")
+    ap.add_argument("--no-precision", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the decode path has no multi-GPU mode in this build "
+              "(sharding is design-only); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    from gsdlq import hip
+    name, total, ncu = hip.device_info()
+    log(f"device {name}, {ncu} CUs, {total / 2**30:.0f} GiB")
+
+    turbo = LayerBank("turbo", a.layers)
+    gbs, ms_step, roof = bench_linear(turbo, a.steps, a.warmup)
+    log(f"turbo layer set: {gbs:.1f} GB/s, {ms_step * 1e3:.1f} us/step; gate/up {roof['achieved']} GB/s")
+    extra = {}
+    if not a.no_precision:
+        prec = LayerBank("precision", max(3, a.layers // 2))
+        pg, pms, proof = bench_linear(prec, a.steps, a.warmup)
+        extra["precision"] = {"value": round(pg, 1), "unit": "GB/s", "us_per_step": round(pms * 1e3, 2),
+                              "frac_hbm": round(pg / HBM_PEAK_GBS, 4), "codes": "u8 (file layout)",
+                              "gate_up_GBs": proof["achieved"], "bytes_per_step": prec.layer_bytes[0]}
+        log(f"precision layer set: {pg:.1f} GB/s")
+        if not a.no_decode:
+            extra["decode_7b_precision"] = bench_decode(prec)
+            log(f"decode: {extra['decode_7b_precision']}")
+    cpu = None if a.no_cpu_baseline else cpu_baseline(turbo)
+    out = {
+        "metric": "fused unpack-matvec GB/s (% HBM peak); batch-1 decode tok/s, 7B shape",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": max(1, a.steps // a.layers) * a.layers,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded bf16 ~N(0,0.02) weights packed by this build's encoder)",
+        "config": {"workload": "Mistral-7B layer linear set q,k,v,o,gate,up,down (4096/1024/14336), Turbo R=8 "
+                               "u8 codes, batch 1, fp32 activations",
+                   "distinct_layers_rotated": a.layers, "bytes_per_step": turbo.layer_bytes[0],
+                   "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "device": name},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    out.update(extra)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

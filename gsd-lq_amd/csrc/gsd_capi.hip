@@ -184,8 +184,8 @@ int gsdh_gqa_attention(void* stream, const float* q, const uint16_t* k_cache, co
                        float* attn_out, int layer_idx, int pos, int n_heads, int n_kv_heads, int head_dim,
                        int max_seq_len, float sm_scale) {
     if (head_dim != 64 && head_dim != 128 && head_dim != 256) return fail(-1, "attention: head_dim %d not in {64,128,256}", head_dim);
-    if (n_kv_heads <= 0 || n_heads % n_kv_heads || n_heads / n_kv_heads > 8)
-        return fail(-1, "attention: n_heads %d / n_kv_heads %d", n_heads, n_kv_heads);
+    if (n_kv_heads <= 0 || n_heads % n_kv_heads || (8 % (n_heads / n_kv_heads)) != 0)
+        return fail(-1, "attention: n_heads %d / n_kv_heads %d is not a group size in {1,2,4,8}", n_heads, n_kv_heads);
     if (pos < 0 || pos >= max_seq_len) return fail(-1, "attention: pos %d outside 0..%d", pos, max_seq_len - 1);
     const int n = pos + 1, G = n_heads / n_kv_heads;
     AttnArgs a{};
@@ -255,6 +255,7 @@ struct gsdh_model {
     float2* cs = nullptr;
     float* ws = nullptr;
     unsigned* counters = nullptr;
+    float* lrbuf = nullptr;         // RMSNorm factor + tmp_k of the launch in flight
     int chunk = 64, max_splits = 1;
     StepState* st = nullptr;        // device
     StepState* st_host = nullptr;   // pinned
@@ -289,15 +290,44 @@ void fill_seg(HexSeg& s, const HexDev& t, float* const* tables, float* out) {
     s.n_pts = 3 * t.radius * t.radius + 3 * t.radius + 1;
 }
 
+// RMSNorm factor and rank-k projections of a launch's segments, computed once
+// by a small kernel (one block per segment and rank) instead of in every block
+// of the matvec; the matvec then reads them from m->lrbuf.
+int prep_lowrank(gsdh_model* m, HexArgs& a) {
+    LrPrep p{};
+    bool any = false;
+    for (int g = 0; g < a.nseg; g++) {
+        p.Vt[g] = a.seg[g].Vt; p.S[g] = a.seg[g].S; p.k[g] = a.seg[g].k;
+        any = any || a.seg[g].k > 0;
+    }
+    if (!any) return 0;
+    p.x = a.x; p.norm_w = a.norm_w; p.eps = a.eps; p.cols = a.cols; p.nseg = a.nseg; p.out = m->lrbuf;
+    HIPCHK(launch_lrprep(p, m->stream));
+    for (int g = 0; g < a.nseg; g++)
+        if (a.seg[g].k > 0) a.seg[g].tmp_k = m->lrbuf + 1 + kMaxRank * g;
+    if (a.norm_w) a.inv_dev = m->lrbuf;
+    return 0;
+}
+
 int issue_linear(gsdh_model* m, int l, int mask) {
     const auto& c = m->c;
-    if (mask & 1) {   // q, k, v with fused attention RMSNorm
+    int rc = 0;
+    if (mask & 1) {   // q, k, v: fused attention RMSNorm; interleaved RoPE + KV append in the epilogue
         HexArgs a{};
         a.nseg = 3;
         fill_seg(a.seg[0], m->slot(l, GSDH_Q), m->tables, m->q);
         fill_seg(a.seg[1], m->slot(l, GSDH_K), m->tables, m->k);
         fill_seg(a.seg[2], m->slot(l, GSDH_V), m->tables, m->v);
         a.x = m->x; a.norm_w = m->norm(l, 0); a.eps = c.rms_eps; a.cols = c.hidden; a.epilogue = kEpiStore;
+        a.scale_t = 1;
+        if (c.rope_interleaved) {
+            a.epilogue = kEpiRopeKV;
+            RopeKV& r = a.rope;
+            r.cs = m->cs; r.pos_dev = &m->st->pos; r.k_cache = m->kc; r.v_cache = m->vc; r.layer = l;
+            r.n_heads = c.n_heads; r.n_kv = c.n_kv_heads; r.hd = c.head_dim; r.max_seq = c.max_seq_len;
+            r.interleaved = 1;
+        }
+        if ((rc = prep_lowrank(m, a))) return rc;
         HIPCHK(launch_hexmv(a, m->stream));
     }
     if (mask & 2) {   // o projection + residual
@@ -305,6 +335,8 @@ int issue_linear(gsdh_model* m, int l, int mask) {
         a.nseg = 1;
         fill_seg(a.seg[0], m->slot(l, GSDH_O), m->tables, m->x);
         a.x = m->attn; a.cols = c.n_heads * c.head_dim; a.epilogue = kEpiResidual; a.resid = m->x;
+        a.scale_t = 1;
+        if ((rc = prep_lowrank(m, a))) return rc;
         HIPCHK(launch_hexmv(a, m->stream));
     }
     if (mask & 4) {   // gate + up with fused FFN RMSNorm and SwiGLU
@@ -313,6 +345,8 @@ int issue_linear(gsdh_model* m, int l, int mask) {
         fill_seg(a.seg[0], m->slot(l, GSDH_GATE), m->tables, m->h);
         fill_seg(a.seg[1], m->slot(l, GSDH_UP), m->tables, nullptr);
         a.x = m->x; a.norm_w = m->norm(l, 1); a.eps = c.rms_eps; a.cols = c.hidden; a.epilogue = kEpiSwiGLU;
+        a.scale_t = 1;
+        if ((rc = prep_lowrank(m, a))) return rc;
         HIPCHK(launch_hexmv(a, m->stream));
     }
     if (mask & 8) {   // down projection + residual
@@ -320,6 +354,8 @@ int issue_linear(gsdh_model* m, int l, int mask) {
         a.nseg = 1;
         fill_seg(a.seg[0], m->slot(l, GSDH_DOWN), m->tables, m->x);
         a.x = m->h; a.cols = c.ffn; a.epilogue = kEpiResidual; a.resid = m->x;
+        a.scale_t = 1;
+        if ((rc = prep_lowrank(m, a))) return rc;
         HIPCHK(launch_hexmv(a, m->stream));
     }
     return 0;
@@ -332,11 +368,13 @@ int issue_token(gsdh_model* m, bool with_head) {
     for (int l = 0; l < c.n_layers; l++) {
         int rc = issue_linear(m, l, 1);
         if (rc) return rc;
-        RopeKV r{};
-        r.cs = m->cs; r.pos_dev = &m->st->pos; r.k_cache = m->kc; r.v_cache = m->vc; r.layer = l;
-        r.n_heads = c.n_heads; r.n_kv = c.n_kv_heads; r.hd = c.head_dim; r.max_seq = c.max_seq_len;
-        r.interleaved = c.rope_interleaved;
-        HIPCHK(launch_rope_kv(m->q, m->k, m->v, r, nullptr, m->stream));
+        if (!c.rope_interleaved) {   // (i, i+hd/2) pairs are not adjacent rows: separate kernel
+            RopeKV r{};
+            r.cs = m->cs; r.pos_dev = &m->st->pos; r.k_cache = m->kc; r.v_cache = m->vc; r.layer = l;
+            r.n_heads = c.n_heads; r.n_kv = c.n_kv_heads; r.hd = c.head_dim; r.max_seq = c.max_seq_len;
+            r.interleaved = 0;
+            HIPCHK(launch_rope_kv(m->q, m->k, m->v, r, nullptr, m->stream));
+        }
         AttnArgs a{};
         a.q = m->q; a.k_cache = m->kc; a.v_cache = m->vc; a.out = m->attn; a.pos_dev = &m->st->pos;
         a.layer = l; a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.hd = c.head_dim; a.max_seq = c.max_seq_len;
@@ -351,6 +389,9 @@ int issue_token(gsdh_model* m, bool with_head) {
         a.nseg = 1;
         fill_seg(a.seg[0], m->slot(0, GSDH_LM_HEAD), m->tables, m->logits);
         a.x = m->x; a.norm_w = m->norm(-1, 0); a.eps = c.rms_eps; a.cols = c.hidden; a.epilogue = kEpiStore;
+        a.scale_t = 1;
+        int rc = prep_lowrank(m, a);
+        if (rc) return rc;
         HIPCHK(launch_hexmv(a, m->stream));
         HIPCHK(launch_argmax(m->logits, c.vocab, m->st, m->gen_tok, m->gen_margin, 1, m->stream));
     }
@@ -386,8 +427,8 @@ int gsdh_model_create(const gsdh_model_config* cfg, gsdh_model** out) {
         return fail(-1, "model_create: hidden %d, ffn %d and n_heads*head_dim must be multiples of 64", c.hidden, c.ffn);
     if (c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256)
         return fail(-1, "model_create: head_dim %d not in {64,128,256}", c.head_dim);
-    if (c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads || c.n_heads / c.n_kv_heads > 8)
-        return fail(-1, "model_create: n_heads %d / n_kv_heads %d", c.n_heads, c.n_kv_heads);
+    if (c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads || (8 % (c.n_heads / c.n_kv_heads)) != 0)
+        return fail(-1, "model_create: n_heads %d / n_kv_heads %d is not a group size in {1,2,4,8}", c.n_heads, c.n_kv_heads);
     if (c.hidden > 65536 || c.ffn > 65536) return fail(-1, "model_create: dimension > 65536");
     gsdh_model* m = new gsdh_model();
     m->c = c;
@@ -414,6 +455,7 @@ int gsdh_model_create(const gsdh_model_config* cfg, gsdh_model** out) {
     m->max_splits = (c.max_seq_len + m->chunk - 1) / m->chunk;
     A((void**)&m->ws, attention_ws_floats(c.n_kv_heads, m->max_splits, c.n_heads / c.n_kv_heads, c.head_dim) * 4);
     A((void**)&m->counters, (size_t)c.n_kv_heads * 4);
+    A((void**)&m->lrbuf, (size_t)(1 + kMaxRank * kMaxSeg) * 4);
     A((void**)&m->st, sizeof(StepState));
     A((void**)&m->gen_tok, (size_t)c.max_seq_len * 4);
     A((void**)&m->gen_margin, (size_t)c.max_seq_len * 4);
@@ -514,7 +556,10 @@ int gsdh_model_set_hex(gsdh_model* m, int layer, int slot, int radius, int rows,
     HexDev& t = m->slot(layer, slot);
     if (t.block) { (void)hipFree(t.block); m->dev_bytes -= t.bytes; t = HexDev(); }
     auto al = [](size_t n) { return (n + 255) / 256 * 256; };
-    const size_t o_codes = 0, o_sc = o_codes + al(ncodes), o_rp = o_sc + al((size_t)rows * cols / 64 * 2);
+    // scales are stored in groups of 4 rows: [ceil(rows/4)][cols/64][4] fp16,
+    // so one 8-byte load gives a lane the scales of 4 rows of its block
+    const size_t nsb = (size_t)cols / 64, ngrp = ((size_t)rows + 3) / 4;
+    const size_t o_codes = 0, o_sc = o_codes + al(ncodes), o_rp = o_sc + al(ngrp * nsb * 4 * 2);
     const size_t o_kc = o_rp + al((size_t)(rows + 1) * 4), o_kd = o_kc + al((size_t)nk * 2);
     const size_t o_u = o_kd + al((size_t)nk * 4), o_s = o_u + al((size_t)rows * k_dim * 2);
     const size_t o_vt = o_s + al((size_t)k_dim * 4), total = o_vt + al((size_t)k_dim * cols * 2);
@@ -526,7 +571,12 @@ int gsdh_model_set_hex(gsdh_model* m, int layer, int slot, int radius, int rows,
     t.kcols = (uint16_t*)(b + o_kc); t.kdel = (float*)(b + o_kd); t.U = (uint16_t*)(b + o_u);
     t.Sv = (float*)(b + o_s); t.Vt = (uint16_t*)(b + o_vt);
     HIPCHK(hipMemcpy(t.codes, codes, ncodes, hipMemcpyHostToDevice));
-    HIPCHK(hipMemcpy(t.scales, scales, (size_t)rows * cols / 64 * 2, hipMemcpyHostToDevice));
+    {
+        std::vector<uint16_t> st(ngrp * nsb * 4, 0);
+        for (size_t r = 0; r < (size_t)rows; r++)
+            for (size_t b = 0; b < nsb; b++) st[((r / 4) * nsb + b) * 4 + (r % 4)] = scales[r * nsb + b];
+        HIPCHK(hipMemcpy(t.scales, st.data(), st.size() * 2, hipMemcpyHostToDevice));
+    }
     HIPCHK(hipMemcpy(t.row_ptr, row_ptr, (size_t)(rows + 1) * 4, hipMemcpyHostToDevice));
     if (nk > 0) {
         HIPCHK(hipMemcpy(t.kcols, kink_cols, (size_t)nk * 2, hipMemcpyHostToDevice));
@@ -627,6 +677,24 @@ int gsdh_model_capture_end(gsdh_model* m, void** graph_exec_out) {
 
 int gsdh_graph_launch(gsdh_model* m, void* ge, int n) {
     for (int i = 0; i < n; i++) HIPCHK(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(ge), m->stream));
+    return 0;
+}
+
+int gsdh_graph_time(gsdh_model* m, void* ge, int n, float* ms_out) {
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    HIPCHK(hipEventCreate(&e0));
+    hipError_t e = hipEventCreate(&e1);
+    if (e != hipSuccess) { (void)hipEventDestroy(e0); return fail((int)e, "hipEventCreate: %s", hipGetErrorString(e)); }
+    e = hipEventRecord(e0, m->stream);
+    for (int i = 0; i < n && e == hipSuccess; i++) e = hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(ge), m->stream);
+    if (e == hipSuccess) e = hipEventRecord(e1, m->stream);
+    if (e == hipSuccess) e = hipEventSynchronize(e1);
+    float ms = 0.f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (e != hipSuccess) return fail((int)e, "graph_time: %s", hipGetErrorString(e));
+    *ms_out = ms;
     return 0;
 }
 

@@ -55,8 +55,27 @@ struct HexArgs {
     int cols;
     int nbatch;            // row batches in total
     int epilogue;
-    RopeKV rope;
+    int scale_t;           // scales layout: 0 = row-major [rows][cols/64] (file),
+                           // 1 = [ceil(rows/4)][cols/64][4] (4 rows per 8-byte load)
+    const float* inv_dev;  // non-null with norm_w: RMSNorm factor computed by launch_lrprep
+    RopeKV rope;           // kEpiRopeKV: interleaved RoPE of q/k rows, fp16 K/V append
 };
+
+// Low-rank / RMSNorm preparation for one fused matvec launch:
+// out[0] = 1/sqrtf(mean(x^2)+eps) (1 when norm_w is null),
+// out[1 + 16*g + j] = S_g[j] * sum_c x'[c] * Vt_g[j,c] with x' the (normed) input.
+struct LrPrep {
+    const float* x;
+    const float* norm_w;
+    float eps;
+    int cols;
+    int nseg;
+    const uint16_t* Vt[kMaxSeg];
+    const float* S[kMaxSeg];
+    int k[kMaxSeg];
+    float* out;
+};
+hipError_t launch_lrprep(const LrPrep& p, hipStream_t stream);
 
 // Launches (all asynchronous on `stream`).
 hipError_t launch_hexmv(const HexArgs& a, hipStream_t stream);

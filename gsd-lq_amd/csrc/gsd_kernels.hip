@@ -18,6 +18,8 @@
 //     tmp_k = S * (Vt x) are recomputed per block from the register slice;
 //   * epilogue fusions: kinks and the U tmp_k term, then store / residual add /
 //     SwiGLU of paired gate-up rows.
+#include <cstdlib>
+
 #include "gsd_internal.h"
 
 namespace gsd {
@@ -65,10 +67,49 @@ __device__ __forceinline__ float dot16(const uint4 c, const float2* __restrict__
     return p;
 }
 
-template <int SPT, int MAXT, int RB>
-__global__ void __launch_bounds__(MAXT) hexmv_kernel(const HexArgs a) {
+// Cross-lane reduction of 8 per-lane partial sums (one per row of a batch)
+// with VALU permutes only: two swap-and-add rounds (v_permlane32_swap,
+// v_permlane16_swap) halve the values per lane while doubling their span,
+// then DPP adds finish each 16-lane row.  On return, lane 16q holds the
+// wave totals of rows 2q (u0) and 2q+1 (u1), q = 0..3.
+__device__ __forceinline__ float swap_add32(float a, float b, bool upper) {
+    // lanes 0-31 get a(lo)+a(hi), lanes 32-63 get b(lo)+b(hi)
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    (void)upper;
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float swap_add16(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+    v += __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+    v += __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x141, 0xF, 0xF, false));  // row_half_mirror
+    v += __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x140, 0xF, 0xF, false));  // row_mirror
+    return v;
+}
+__device__ __forceinline__ void reduce8(const float (&acc)[8], float& u0, float& u1) {
+    const float t0 = swap_add32(acc[0], acc[4], false);   // rows 0 | 4
+    const float t1 = swap_add32(acc[1], acc[5], false);   // rows 1 | 5
+    const float t2 = swap_add32(acc[2], acc[6], false);   // rows 2 | 6
+    const float t3 = swap_add32(acc[3], acc[7], false);   // rows 3 | 7
+    u0 = row16_sum(swap_add16(t0, t2));                   // rows 0 | 2 | 4 | 6 per 16 lanes
+    u1 = row16_sum(swap_add16(t1, t3));                   // rows 1 | 3 | 5 | 7
+}
+
+// Rows of batch b.  Unpaired: RB consecutive rows of one segment.  Paired
+// (gate/up + SwiGLU): rows 0-3 of the batch are gate rows r0..r0+3, rows 4-7
+// the same rows of up.
+struct BatchRows {
+    int g0, r0;
+};
+
+template <int SPT, int NWM, bool ST>
+__global__ void __launch_bounds__(NWM * 64) hexmv_kernel(const HexArgs a) {
+    constexpr int RB = 8;
     __shared__ float2 tbl[kMaxSeg][kTableSlots];
-    __shared__ float red[MAXT / 64][RB];
+    __shared__ float red[2][NWM][RB];
     __shared__ float fin[RB];
     __shared__ float tkl[kMaxSeg][kMaxRank];
     __shared__ float scratch[16];
@@ -79,6 +120,57 @@ __global__ void __launch_bounds__(MAXT) hexmv_kernel(const HexArgs a) {
     const int S = a.cols >> 5;
     const int nsb = a.cols >> 6;
     const size_t rowbytes = (size_t)(a.cols >> 1);
+    const bool paired = a.epilogue == kEpiSwiGLU;
+
+    auto rows_of = [&](int b) {
+        BatchRows br;
+        if (paired) {
+            br.g0 = 0;
+            br.r0 = b * (RB / 2);
+        } else {
+            int g = 0;
+            while (g + 1 < a.nseg && b >= a.seg[g + 1].batch0) g++;
+            br.g0 = g;
+            br.r0 = (b - a.seg[g].batch0) * RB;
+        }
+        return br;
+    };
+
+    uint4 cw[SPT][RB];
+    uint32_t sv[SPT][RB];
+    // Issue every load of batch b: RB x SPT 16-byte code loads and the
+    // matching scales, rows and slots clamped in range (results of padding
+    // rows/slots are discarded later), no branches between the loads.
+    auto issue = [&](int b) {
+        const BatchRows br = rows_of(b);
+#pragma unroll
+        for (int j = 0; j < SPT; j++) {
+            const int s = min(tid + j * NT, S - 1);
+#pragma unroll
+            for (int rr = 0; rr < RB; rr++) {
+                const int g = paired ? (rr >> 2) : br.g0;
+                const int row = min(br.r0 + (paired ? (rr & 3) : rr), a.seg[g].rows - 1);
+                cw[j][rr] = *reinterpret_cast<const uint4*>(a.seg[g].codes + (size_t)row * rowbytes + (size_t)s * 16);
+                if (!ST) sv[j][rr] = a.seg[g].scales[(size_t)row * nsb + (s >> 1)];
+            }
+            if (ST) {
+#pragma unroll
+                for (int grp = 0; grp < 2; grp++) {
+                    const int g = paired ? grp : br.g0;
+                    const int ngrp = (a.seg[g].rows + 3) >> 2;
+                    const int rg = min((br.r0 >> 2) + (paired ? 0 : grp), ngrp - 1);
+                    const uint2 w = *reinterpret_cast<const uint2*>(a.seg[g].scales + ((size_t)rg * nsb + (s >> 1)) * 4);
+                    sv[j][4 * grp + 0] = w.x & 0xFFFFu;
+                    sv[j][4 * grp + 1] = w.x >> 16;
+                    sv[j][4 * grp + 2] = w.y & 0xFFFFu;
+                    sv[j][4 * grp + 3] = w.y >> 16;
+                }
+            }
+        }
+    };
+
+    int b = blockIdx.x;
+    if (b < a.nbatch) issue(b);   // in flight while the prologue runs
 
     for (int g = 0; g < a.nseg; g++) {
         const float2* tg = reinterpret_cast<const float2*>(a.seg[g].table);
@@ -106,13 +198,17 @@ __global__ void __launch_bounds__(MAXT) hexmv_kernel(const HexArgs a) {
     // fused RMSNorm (gsd_lq_cpu_engine.c:66-82): x' = (x * inv) * w
     float inv = 1.f;
     if (a.norm_w) {
-        float ss = 0.f;
+        if (a.inv_dev) {
+            inv = *a.inv_dev;
+        } else {
+            float ss = 0.f;
 #pragma unroll
-        for (int j = 0; j < SPT; j++)
+            for (int j = 0; j < SPT; j++)
 #pragma unroll
-            for (int q = 0; q < 32; q++) ss = fmaf(xr[j][q], xr[j][q], ss);
-        ss = block_sum(ss, scratch);
-        inv = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
+                for (int q = 0; q < 32; q++) ss = fmaf(xr[j][q], xr[j][q], ss);
+            ss = block_sum(ss, scratch);
+            inv = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
+        }
 #pragma unroll
         for (int j = 0; j < SPT; j++) {
             const int s = tid + j * NT;
@@ -140,7 +236,7 @@ __global__ void __launch_bounds__(MAXT) hexmv_kernel(const HexArgs a) {
             continue;
         }
         for (int jj = 0; jj < sg.k; jj++) {
-            float p = 0.f;
+            float pp = 0.f;
 #pragma unroll
             for (int j = 0; j < SPT; j++) {
                 const int s = tid + j * NT;
@@ -152,69 +248,51 @@ __global__ void __launch_bounds__(MAXT) hexmv_kernel(const HexArgs a) {
                         const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
                         for (int e = 0; e < 4; e++) {
-                            p = fmaf(xr[j][8 * q + 2 * e], h2f((uint16_t)(w[e] & 0xFFFFu)), p);
-                            p = fmaf(xr[j][8 * q + 2 * e + 1], h2f((uint16_t)(w[e] >> 16)), p);
+                            pp = fmaf(xr[j][8 * q + 2 * e], h2f((uint16_t)(w[e] & 0xFFFFu)), pp);
+                            pp = fmaf(xr[j][8 * q + 2 * e + 1], h2f((uint16_t)(w[e] >> 16)), pp);
                         }
                     }
                 }
             }
-            p = block_sum(p, scratch);
-            if (tid == 0) tkl[g][jj] = p * sg.S[jj];
+            pp = block_sum(pp, scratch);
+            if (tid == 0) tkl[g][jj] = pp * sg.S[jj];
         }
     }
     __syncthreads();
 
-    const bool paired = a.epilogue == kEpiSwiGLU;
-    for (int b = blockIdx.x; b < a.nbatch; b += gridDim.x) {
-        // rows of this batch: paired -> RB/2 rows of seg0 and the same of seg1
-        int gsel = 0, r0 = 0;
-        if (paired) {
-            r0 = b * (RB / 2);
-        } else {
-            while (gsel + 1 < a.nseg && b >= a.seg[gsel + 1].batch0) gsel++;
-            r0 = (b - a.seg[gsel].batch0) * RB;
-        }
+    int buf = 0;
+    for (; b < a.nbatch; b += gridDim.x) {
+        const BatchRows br = rows_of(b);
         float acc[RB];
 #pragma unroll
         for (int rr = 0; rr < RB; rr++) acc[rr] = 0.f;
-
 #pragma unroll
         for (int j = 0; j < SPT; j++) {
-            const int s = tid + j * NT;
-            if (s >= S) continue;
-            uint4 cw[RB];
-            uint16_t sc[RB];
+            if (tid + j * NT < S) {
 #pragma unroll
-            for (int rr = 0; rr < RB; rr++) {
-                const int g = paired ? (rr >= RB / 2) : gsel;
-                const int row = paired ? r0 + (rr % (RB / 2)) : r0 + rr;
-                if (row < a.seg[g].rows) {
-                    cw[rr] = *reinterpret_cast<const uint4*>(a.seg[g].codes + (size_t)row * rowbytes + (size_t)s * 16);
-                    sc[rr] = a.seg[g].scales[(size_t)row * nsb + (s >> 1)];
-                } else {
-                    cw[rr] = make_uint4(0, 0, 0, 0);
-                    sc[rr] = 0;
+                for (int rr = 0; rr < RB; rr++) {
+                    const int g = paired ? (rr >> 2) : br.g0;
+                    acc[rr] = fmaf(dot16(cw[j][rr], tbl[g], xr[j]), h2f((uint16_t)sv[j][rr]), acc[rr]);
                 }
             }
-#pragma unroll
-            for (int rr = 0; rr < RB; rr++) {
-                const int g = paired ? (rr >= RB / 2) : gsel;
-                acc[rr] = fmaf(dot16(cw[rr], tbl[g], xr[j]), h2f(sc[rr]), acc[rr]);
-            }
         }
-#pragma unroll
-        for (int rr = 0; rr < RB; rr++) {
-            const float v = wave_sum(acc[rr]);
-            if (lane == 0) red[wid][rr] = v;
+        // next batch's loads fly during the reduction and the epilogue
+        if (b + (int)gridDim.x < a.nbatch) issue(b + gridDim.x);
+
+        float u0, u1;
+        reduce8(acc, u0, u1);
+        if ((lane & 15) == 0) {
+            red[buf][wid][2 * (lane >> 4)] = u0;
+            red[buf][wid][2 * (lane >> 4) + 1] = u1;
         }
         __syncthreads();
         if (tid < RB) {
             const int rr = tid;
-            const int g = paired ? (rr >= RB / 2) : gsel;
-            const int row = paired ? r0 + (rr % (RB / 2)) : r0 + rr;
+            const int g = paired ? (rr >> 2) : br.g0;
+            const int row = br.r0 + (paired ? (rr & 3) : rr);
             const HexSeg& sg = a.seg[g];
             float t = 0.f;
-            for (int w = 0; w < NW; w++) t += red[w][rr];
+            for (int w = 0; w < NW; w++) t += red[buf][w][rr];
             if (row < sg.rows) {
                 if (sg.row_ptr) {
                     const uint32_t e = sg.row_ptr[row + 1];
@@ -230,25 +308,56 @@ __global__ void __launch_bounds__(MAXT) hexmv_kernel(const HexArgs a) {
             }
             fin[rr] = t;
         }
+        if (a.epilogue == kEpiRopeKV) {
+            // segments q, k, v; rows 2i, 2i+1 of a head are one rotation pair
+            // (interleaved RoPE, gsd_lq_cpu_engine.c:213-256), evaluated without
+            // contraction like the reference; k', v stored as fp16 at pos
+            __syncthreads();
+            if (tid < RB / 2) {
+#pragma clang fp contract(off)
+                const RopeKV& r = a.rope;
+                const int row = br.r0 + 2 * tid;
+                const HexSeg& sg = a.seg[br.g0];
+                if (row + 1 < sg.rows) {
+                    const int pos = r.pos_dev ? *r.pos_dev : r.pos;
+                    const float x0 = fin[2 * tid], x1 = fin[2 * tid + 1];
+                    const size_t base = ((size_t)r.layer * r.max_seq + (size_t)pos) * (size_t)r.n_kv * r.hd;
+                    if (br.g0 == 2) {
+                        r.v_cache[base + row] = f2h(x0);
+                        r.v_cache[base + row + 1] = f2h(x1);
+                    } else {
+                        const float2 cs = r.cs[(size_t)pos * (r.hd >> 1) + ((row % r.hd) >> 1)];
+                        const float y0 = x0 * cs.x - x1 * cs.y;
+                        const float y1 = x0 * cs.y + x1 * cs.x;
+                        if (br.g0 == 0) {
+                            sg.out[row] = y0;
+                            sg.out[row + 1] = y1;
+                        } else {
+                            r.k_cache[base + row] = f2h(y0);
+                            r.k_cache[base + row + 1] = f2h(y1);
+                        }
+                    }
+                }
+            }
+        }
         if (paired) {
             __syncthreads();
             if (tid < RB / 2) {
-                const int row = r0 + tid;
+                const int row = br.r0 + tid;
                 if (row < a.seg[0].rows) {
                     const float gt = fin[tid], up = fin[tid + RB / 2];
                     a.seg[0].out[row] = (gt / (1.0f + expf(-gt))) * up;
                 }
             }
         }
-        __syncthreads();
+        buf ^= 1;
     }
 }
 
-template <int SPT, int MAXT>
+template <int SPT, int NWM, bool ST>
 hipError_t launch_hexmv_t(const HexArgs& a, hipStream_t st, int nt) {
     constexpr int RB = 8;
     HexArgs b = a;
-    // batches: per segment ceil(rows/RB), or ceil(rows/(RB/2)) paired
     if (b.epilogue == kEpiSwiGLU) {
         b.nbatch = (b.seg[0].rows + RB / 2 - 1) / (RB / 2);
     } else {
@@ -260,8 +369,18 @@ hipError_t launch_hexmv_t(const HexArgs& a, hipStream_t st, int nt) {
         b.nbatch = nb;
     }
     if (b.nbatch == 0) return hipSuccess;
-    const int grid = b.nbatch < 4096 ? b.nbatch : 4096;
-    hipLaunchKernelGGL((hexmv_kernel<SPT, MAXT, RB>), dim3(grid), dim3(nt), 0, st, b);
+    // persistent grid: as many blocks as are resident on the chip at once
+    static int per_cu = 0;
+    if (per_cu == 0) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, hexmv_kernel<SPT, NWM, ST>, nt, 0) != hipSuccess || n < 1)
+            n = 1;
+        per_cu = n;
+    }
+    const int ncu = device_cu_count() > 0 ? device_cu_count() : 256;
+    int grid = ncu * per_cu;
+    if (grid > b.nbatch) grid = b.nbatch;
+    hipLaunchKernelGGL((hexmv_kernel<SPT, NWM, ST>), dim3(grid), dim3(nt), 0, st, b);
     return hipGetLastError();
 }
 
@@ -340,124 +459,168 @@ __global__ void rope_kv_kernel(float* q, const float* k, const float* v, const R
 
 // ------------------------------------------------------------------------
 // GQA decode attention, split over the context (flash-decoding).
-// grid = (n_kv, max_splits); a block handles one KV head, all `group` query
-// heads that share it (K/V read once per group, not once per query head),
-// and `chunk` (<= 256) positions.  The last block of a KV head to finish
-// merges the per-split (max, sum, o) partials.
+// grid = (n_kv, max_splits); a block owns one KV head, all G query heads
+// that share it (K/V read once per group, not once per query head) and
+// `chunk` (<= 256) positions.  LPP = HD/8 lanes hold one position: each lane
+// loads 16 bytes (8 fp16 dims) of K or V, so a wave reads 64/LPP whole rows
+// per 16-byte load.  Dot products finish with DPP row reductions; every
+// reduction stays in VALU (DPP, permlane swaps) except the final cross-wave
+// one.  The last block of a KV head to finish merges the per-split
+// (max, sum, o) partials.
 // ------------------------------------------------------------------------
-template <int HD>
+__device__ __forceinline__ float dpp_sum8(float v) {    // sum within 8-lane half-rows
+    v += __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0xB1, 0xF, 0xF, false));
+    v += __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x4E, 0xF, 0xF, false));
+    v += __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x141, 0xF, 0xF, false));
+    return v;
+}
+template <int LPP>
+__device__ __forceinline__ float lane_group_sum(float v) {   // sum over LPP consecutive lanes
+    if (LPP == 8) return dpp_sum8(v);
+    v = row16_sum(v);
+    if (LPP == 32) v = swap_add16(v, v);
+    return v;
+}
+__device__ __forceinline__ float wave_allsum(float v) {
+    v = row16_sum(v);
+    v = swap_add16(v, v);
+    return swap_add32(v, v, false);
+}
+__device__ __forceinline__ float wave_allmax(float v) {
+    v = fmaxf(v, __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0xB1, 0xF, 0xF, false)));
+    v = fmaxf(v, __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x4E, 0xF, 0xF, false)));
+    v = fmaxf(v, __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x141, 0xF, 0xF, false)));
+    v = fmaxf(v, __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x140, 0xF, 0xF, false)));
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// sum over the position slots of a wave (lanes with equal lane % LPP)
+template <int LPP>
+__device__ __forceinline__ float slot_sum(float v) {
+    if (LPP == 8) v += __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x128, 0xF, 0xF, false));  // row_ror:8
+    if (LPP <= 16) v = swap_add16(v, v);
+    return swap_add32(v, v, false);
+}
+__device__ __forceinline__ void unpack8(const uint4 w, float (&f)[8]) {
+    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int e = 0; e < 8; e++) f[e] = h2f((uint16_t)(u[e >> 1] >> (16 * (e & 1))));
+}
+
+template <int HD, int G>
 __global__ void __launch_bounds__(256) attn_kernel(const AttnArgs a) {
-    constexpr int DG = HD / 8;          // 8-dim groups (16-byte loads)
-    constexpr int PL = 256 / DG;        // position lanes in phase C
-    constexpr int MAXG = 8;
-    __shared__ float qs[MAXG][HD];
-    __shared__ float sc[MAXG][256];
-    __shared__ float part[4][MAXG][HD];
-    __shared__ float mred[4][MAXG];
-    __shared__ float ml[2][MAXG];
+    constexpr int LPP = HD / 8;          // lanes per position
+    constexpr int PPW = 64 / LPP;        // positions per wave per step
+    constexpr int PPB = 4 * PPW;         // positions per block per step
+    constexpr int UNR = 4;               // steps whose loads are issued together
+    __shared__ float sc[G][256];
+    __shared__ float part[4][G][HD];
+    __shared__ float ml[2][G];
     __shared__ int s_last;
 
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int sub = lane % LPP, prow = lane / LPP;
     const int pos = a.pos_dev ? *a.pos_dev : a.pos;
     const int n = pos + 1;
     const int nsplit = (n + a.chunk - 1) / a.chunk;
     const int split = blockIdx.y;
     if (split >= nsplit) return;
     const int kvh = blockIdx.x;
-    const int G = a.n_heads / a.n_kv;
     const int t0 = split * a.chunk;
     const int t1 = min(n, t0 + a.chunk);
-    const size_t rowstride = (size_t)a.n_kv * HD;
-    const size_t lbase = (size_t)a.layer * a.max_seq * rowstride + (size_t)kvh * HD;
-
-    for (int i = tid; i < G * HD; i += 256) qs[i / HD][i % HD] = a.q[(size_t)(kvh * G) * HD + i];
-    __syncthreads();
-
-    // phase A: scores, one position per thread, dot in the reference order
-    {
-        const int t = t0 + tid;
-        if (t < t1) {
-            float dot[MAXG];
-#pragma unroll
-            for (int g = 0; g < MAXG; g++) dot[g] = 0.f;
-            const uint4* kp = reinterpret_cast<const uint4*>(a.k_cache + lbase + (size_t)t * rowstride);
-            for (int d8 = 0; d8 < DG; d8++) {
-                const uint4 kv = kp[d8];
-                const uint32_t w[4] = {kv.x, kv.y, kv.z, kv.w};
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const float kf = h2f((uint16_t)(w[e >> 1] >> (16 * (e & 1))));
-#pragma unroll
-                    for (int g = 0; g < MAXG; g++) {
-                        if (g < G) {
-#pragma clang fp contract(off)
-                            dot[g] = dot[g] + qs[g][d8 * 8 + e] * kf;
-                        }
-                    }
-                }
-            }
-#pragma unroll
-            for (int g = 0; g < MAXG; g++)
-                if (g < G) sc[g][tid] = dot[g] * a.sm_scale;
-        }
-    }
-    __syncthreads();
-    // phase B: per-head max and exp-sum over this chunk
     const int cn = t1 - t0;
+    const size_t rowstride = (size_t)a.n_kv * HD;
+    const uint16_t* kb = a.k_cache + (size_t)a.layer * a.max_seq * rowstride + (size_t)kvh * HD + sub * 8;
+    const uint16_t* vb = a.v_cache + (size_t)a.layer * a.max_seq * rowstride + (size_t)kvh * HD + sub * 8;
+
+    float qv[G][8];
+#pragma unroll
     for (int g = 0; g < G; g++) {
-        float m = tid < cn ? sc[g][tid] : -INFINITY;
-        m = wave_max(m);
-        if (lane == 0) mred[wid][g] = m;
+        const float4* qp = reinterpret_cast<const float4*>(a.q + (size_t)(kvh * G + g) * HD + sub * 8);
+        const float4 q0 = qp[0], q1 = qp[1];
+        qv[g][0] = q0.x; qv[g][1] = q0.y; qv[g][2] = q0.z; qv[g][3] = q0.w;
+        qv[g][4] = q1.x; qv[g][5] = q1.y; qv[g][6] = q1.z; qv[g][7] = q1.w;
     }
-    __syncthreads();
-    if (tid < G) ml[0][tid] = fmaxf(fmaxf(mred[0][tid], mred[1][tid]), fmaxf(mred[2][tid], mred[3][tid]));
-    __syncthreads();
-    for (int g = 0; g < G; g++) {
-        float e = 0.f;
-        if (tid < cn) {
-            e = expf(sc[g][tid] - ml[0][g]);
-            sc[g][tid] = e;
+
+    // phase A: scores s[g][t] = (q_g . K_t) * sm_scale
+    const int nsteps = (cn + PPB - 1) / PPB;
+    for (int s0 = 0; s0 < nsteps; s0 += UNR) {
+        uint4 kw[UNR];
+#pragma unroll
+        for (int u = 0; u < UNR; u++) {
+            const int t = min(t0 + (s0 + u) * PPB + wid * PPW + prow, t1 - 1);
+            kw[u] = *reinterpret_cast<const uint4*>(kb + (size_t)t * rowstride);
         }
-        e = wave_sum(e);
-        if (lane == 0) mred[wid][g] = e;
+#pragma unroll
+        for (int u = 0; u < UNR; u++) {
+            const int tl = (s0 + u) * PPB + wid * PPW + prow;
+            float kf[8];
+            unpack8(kw[u], kf);
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                float d = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) d = fmaf(qv[g][e], kf[e], d);
+                d = lane_group_sum<LPP>(d);
+                if (sub == 0 && tl < cn) sc[g][tl] = d * a.sm_scale;
+            }
+        }
     }
     __syncthreads();
-    if (tid < G) ml[1][tid] = (mred[0][tid] + mred[1][tid]) + (mred[2][tid] + mred[3][tid]);
+    // phase B: per head max and exp-sum over the chunk (wave w: heads w, w+4)
+    for (int g = wid; g < G; g += 4) {
+        float m = -INFINITY;
+        for (int i = lane; i < cn; i += 64) m = fmaxf(m, sc[g][i]);
+        m = wave_allmax(m);
+        float l = 0.f;
+        for (int i = lane; i < cn; i += 64) {
+            const float e = expf(sc[g][i] - m);
+            sc[g][i] = e;
+            l += e;
+        }
+        l = wave_allsum(l);
+        if (lane == 0) { ml[0][g] = m; ml[1][g] = l; }
+    }
+    __syncthreads();
     // phase C: o[g][d] = sum_t p[g][t] V_t[d]
-    {
-        const int dg = tid % DG, pl = tid / DG;
-        float acc[MAXG][8];
+    float acc[G][8];
 #pragma unroll
-        for (int g = 0; g < MAXG; g++)
+    for (int g = 0; g < G; g++)
 #pragma unroll
-            for (int e = 0; e < 8; e++) acc[g][e] = 0.f;
-        for (int t = t0 + pl; t < t1; t += PL) {
-            const uint4 vv = *reinterpret_cast<const uint4*>(a.v_cache + lbase + (size_t)t * rowstride + dg * 8);
-            const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
-            float vf[8];
+        for (int e = 0; e < 8; e++) acc[g][e] = 0.f;
+    for (int s0 = 0; s0 < nsteps; s0 += UNR) {
+        uint4 vw[UNR];
 #pragma unroll
-            for (int e = 0; e < 8; e++) vf[e] = h2f((uint16_t)(w[e >> 1] >> (16 * (e & 1))));
+        for (int u = 0; u < UNR; u++) {
+            const int t = min(t0 + (s0 + u) * PPB + wid * PPW + prow, t1 - 1);
+            vw[u] = *reinterpret_cast<const uint4*>(vb + (size_t)t * rowstride);
+        }
 #pragma unroll
-            for (int g = 0; g < MAXG; g++) {
-                if (g < G) {
-                    const float p = sc[g][t - t0];
+        for (int u = 0; u < UNR; u++) {
+            const int tl = (s0 + u) * PPB + wid * PPW + prow;
+            if (tl < cn) {
+                float vf[8];
+                unpack8(vw[u], vf);
+#pragma unroll
+                for (int g = 0; g < G; g++) {
+                    const float p = sc[g][tl];
 #pragma unroll
                     for (int e = 0; e < 8; e++) acc[g][e] = fmaf(p, vf[e], acc[g][e]);
                 }
             }
         }
-        // reduce over position lanes inside the wave (lanes dg + DG*k)
+    }
 #pragma unroll
-        for (int o = DG; o < 64; o <<= 1)
+    for (int g = 0; g < G; g++)
 #pragma unroll
-            for (int g = 0; g < MAXG; g++)
+        for (int e = 0; e < 8; e++) acc[g][e] = slot_sum<LPP>(acc[g][e]);
+    if (prow == 0) {
 #pragma unroll
-                for (int e = 0; e < 8; e++) acc[g][e] += __shfl_xor(acc[g][e], o, 64);
-        if (lane < DG) {
-            for (int g = 0; g < G; g++)
+        for (int g = 0; g < G; g++)
 #pragma unroll
-                for (int e = 0; e < 8; e++) part[wid][g][dg * 8 + e] = acc[g][e];
-        }
+            for (int e = 0; e < 8; e++) part[wid][g][sub * 8 + e] = acc[g][e];
     }
     __syncthreads();
     const int group_base = kvh * G;
@@ -469,7 +632,7 @@ __global__ void __launch_bounds__(256) attn_kernel(const AttnArgs a) {
         }
         return;
     }
-    // write partials [kvh][split][g][2+HD]
+    // partials [kvh][split][g][2+HD], merged by the last block of this KV head
     float* wsb = a.ws + ((size_t)kvh * a.max_splits + split) * G * (2 + HD);
     for (int i = tid; i < G * HD; i += 256) {
         const int g = i / HD, d = i % HD;
@@ -505,6 +668,42 @@ __global__ void __launch_bounds__(256) attn_kernel(const AttnArgs a) {
     if (tid == 0) a.counters[kvh] = 0u;
 }
 
+// One block per (segment, j): RMSNorm factor and tmp_k of one launch.
+__global__ void __launch_bounds__(256) lrprep_kernel(const LrPrep p) {
+    __shared__ float scratch[16];
+    const int g = blockIdx.x / kMaxRank, j = blockIdx.x % kMaxRank;
+    if (g >= p.nseg || j >= (p.k[g] > 0 ? p.k[g] : (g == 0 && j == 0 ? 1 : 0))) return;
+    float inv = 1.f;
+    if (p.norm_w) {
+        float ss = 0.f;
+        for (int c = threadIdx.x * 4; c < p.cols; c += 1024) {
+            const float4 v = *reinterpret_cast<const float4*>(p.x + c);
+            ss = fmaf(v.x, v.x, ss); ss = fmaf(v.y, v.y, ss); ss = fmaf(v.z, v.z, ss); ss = fmaf(v.w, v.w, ss);
+        }
+        ss = block_sum(ss, scratch);
+        inv = 1.0f / sqrtf(ss / (float)p.cols + p.eps);
+    }
+    if (g == 0 && j == 0 && threadIdx.x == 0) p.out[0] = inv;
+    if (p.k[g] <= 0) return;
+    const uint16_t* vt = p.Vt[g] + (size_t)j * p.cols;
+    float d = 0.f;
+    for (int c = threadIdx.x * 4; c < p.cols; c += 1024) {
+        const float4 v = *reinterpret_cast<const float4*>(p.x + c);
+        const uint2 h = *reinterpret_cast<const uint2*>(vt + c);
+        float4 w = make_float4(1.f, 1.f, 1.f, 1.f);
+        if (p.norm_w) w = *reinterpret_cast<const float4*>(p.norm_w + c);
+        const float xs[4] = {v.x, v.y, v.z, v.w}, ws[4] = {w.x, w.y, w.z, w.w};
+        const uint16_t hv[4] = {(uint16_t)(h.x & 0xFFFF), (uint16_t)(h.x >> 16), (uint16_t)(h.y & 0xFFFF), (uint16_t)(h.y >> 16)};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float xe = p.norm_w ? (xs[e] * inv) * ws[e] : xs[e];
+            d = fmaf(xe, h2f(hv[e]), d);
+        }
+    }
+    d = block_sum(d, scratch);
+    if (threadIdx.x == 0) p.out[1 + kMaxRank * g + j] = d * p.S[g][j];
+}
+
 __global__ void embed_kernel(const uint16_t* embed, const int* token, float* x, int hidden) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < hidden) x[i] = h2f(embed[(size_t)(*token) * hidden + i]);
@@ -518,39 +717,55 @@ __device__ __forceinline__ float clean(float v) {
     return v;
 }
 
+// (value, index, runner-up) merge: higher value wins, lower index on ties
+struct Top2 {
+    float v1, v2;
+    int i1;
+};
+__device__ __forceinline__ Top2 merge(Top2 a, Top2 b) {
+    Top2 r;
+    if (b.v1 > a.v1 || (b.v1 == a.v1 && b.i1 < a.i1)) {
+        r.v1 = b.v1; r.i1 = b.i1; r.v2 = fmaxf(a.v1, b.v2);
+    } else {
+        r.v1 = a.v1; r.i1 = a.i1; r.v2 = fmaxf(a.v2, b.v1);
+    }
+    return r;
+}
+
 __global__ void __launch_bounds__(1024) argmax_kernel(const float* logits, int n, StepState* st, int* gen_tok,
                                                       float* gen_margin, int advance) {
-    __shared__ float sv1[1024], sv2[1024];
-    __shared__ int si1[1024];
-    const int tid = threadIdx.x;
-    float v1 = -INFINITY, v2 = -INFINITY;
-    int i1 = 0x7FFFFFFF;
-    for (int i = tid; i < n; i += blockDim.x) {
-        const float v = clean(logits[i]);
-        if (v > v1) { v2 = v1; v1 = v; i1 = i; }
-        else if (v > v2) v2 = v;
-    }
-    sv1[tid] = v1; sv2[tid] = v2; si1[tid] = i1;
-    __syncthreads();
-    for (int s = blockDim.x >> 1; s > 0; s >>= 1) {
-        if (tid < s) {
-            const float a1 = sv1[tid], a2 = sv2[tid], b1 = sv1[tid + s], b2 = sv2[tid + s];
-            const int ai = si1[tid], bi = si1[tid + s];
-            if (b1 > a1 || (b1 == a1 && bi < ai)) {
-                sv1[tid] = b1; si1[tid] = bi; sv2[tid] = fmaxf(a1, b2);
-            } else {
-                sv2[tid] = fmaxf(a2, b1);
-            }
+    __shared__ Top2 sw[16];
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    Top2 t{-INFINITY, -INFINITY, 0x7FFFFFFF};
+    // 16 independent coalesced loads per thread per round
+    for (int base = tid; base < n; base += 1024 * 16) {
+        float v[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const int i = base + u * 1024;
+            v[u] = i < n ? logits[i] : -INFINITY;
         }
-        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const int i = base + u * 1024;
+            if (i < n) t = merge(t, Top2{clean(v[u]), -INFINITY, i});
+        }
     }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        Top2 u{__shfl_xor(t.v1, o, 64), __shfl_xor(t.v2, o, 64), __shfl_xor(t.i1, o, 64)};
+        t = merge(t, u);
+    }
+    if (lane == 0) sw[wid] = t;
+    __syncthreads();
     if (tid == 0) {
-        const int tok = si1[0];
-        const float margin = sv1[0] - sv2[0];
-        st->token = tok;
+        Top2 r = sw[0];
+        for (int w = 1; w < (int)(blockDim.x >> 6); w++) r = merge(r, sw[w]);
+        const float margin = r.v1 - r.v2;
+        st->token = r.i1;
         if (gen_tok) {
             const int c = st->gen_count;
-            gen_tok[c] = tok;
+            gen_tok[c] = r.i1;
             gen_margin[c] = margin;
             st->gen_count = c + 1;
         }
@@ -588,19 +803,31 @@ __global__ void unpack_kernel(const uint8_t* codes, int64_t n, int R, int32_t* i
 // ------------------------------------------------------------------------
 hipError_t launch_hexmv(const HexArgs& a, hipStream_t st) {
     const int S = a.cols >> 5;
-    const int spt = (S % 128 == 0) ? 2 : 1;
+    // slots per thread: 2 halves the threads per row (one wave covers 4096
+    // columns) at the price of more VGPRs; GSD_HEXMV_SPT=1|2 overrides
+    static const int force_spt = getenv("GSD_HEXMV_SPT") ? atoi(getenv("GSD_HEXMV_SPT")) : 0;
+    int spt = (S % 128 == 0) ? 2 : 1;
+    if (force_spt == 1 || (force_spt == 2 && S % 128 == 0)) spt = force_spt;
     const int nt = ((S + spt - 1) / spt + 63) / 64 * 64;
     if (nt > 1024) return hipErrorInvalidValue;
-    if (spt == 2) {
-        if (nt <= 64) return launch_hexmv_t<2, 64>(a, st, nt);
-        if (nt <= 256) return launch_hexmv_t<2, 256>(a, st, nt);
-        if (nt <= 512) return launch_hexmv_t<2, 512>(a, st, nt);
-        return launch_hexmv_t<2, 1024>(a, st, nt);
+    const bool st_layout = a.scale_t != 0;
+#define GSD_HEXMV_DISPATCH(ST)                                                      \
+    if (spt == 2) {                                                                 \
+        if (nt <= 64) return launch_hexmv_t<2, 1, ST>(a, st, nt);                    \
+        if (nt <= 256) return launch_hexmv_t<2, 4, ST>(a, st, nt);                   \
+        if (nt <= 512) return launch_hexmv_t<2, 8, ST>(a, st, nt);                   \
+        return launch_hexmv_t<2, 16, ST>(a, st, nt);                                 \
+    }                                                                               \
+    if (nt <= 64) return launch_hexmv_t<1, 1, ST>(a, st, nt);                        \
+    if (nt <= 256) return launch_hexmv_t<1, 4, ST>(a, st, nt);                       \
+    if (nt <= 512) return launch_hexmv_t<1, 8, ST>(a, st, nt);                       \
+    return launch_hexmv_t<1, 16, ST>(a, st, nt);
+    if (st_layout) {
+        GSD_HEXMV_DISPATCH(true)
+    } else {
+        GSD_HEXMV_DISPATCH(false)
     }
-    if (nt <= 64) return launch_hexmv_t<1, 64>(a, st, nt);
-    if (nt <= 256) return launch_hexmv_t<1, 256>(a, st, nt);
-    if (nt <= 512) return launch_hexmv_t<1, 512>(a, st, nt);
-    return launch_hexmv_t<1, 1024>(a, st, nt);
+#undef GSD_HEXMV_DISPATCH
 }
 
 hipError_t launch_lowrank(const float* x, const uint16_t* Vt, const float* S, float* tmp_k, int k, int cols,
@@ -647,12 +874,28 @@ size_t attention_ws_floats(int n_kv, int max_splits, int group, int hd) {
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
     const dim3 grid(a.n_kv, a.max_splits);
+    const int G = a.n_heads / a.n_kv;
+#define GSD_ATTN_G(HD)                                                                          \
+    switch (G) {                                                                                \
+        case 1: hipLaunchKernelGGL((attn_kernel<HD, 1>), grid, dim3(256), 0, st, a); break;     \
+        case 2: hipLaunchKernelGGL((attn_kernel<HD, 2>), grid, dim3(256), 0, st, a); break;     \
+        case 4: hipLaunchKernelGGL((attn_kernel<HD, 4>), grid, dim3(256), 0, st, a); break;     \
+        case 8: hipLaunchKernelGGL((attn_kernel<HD, 8>), grid, dim3(256), 0, st, a); break;     \
+        default: return hipErrorInvalidValue;                                                   \
+    }
     switch (a.hd) {
-        case 64: hipLaunchKernelGGL(attn_kernel<64>, grid, dim3(256), 0, st, a); break;
-        case 128: hipLaunchKernelGGL(attn_kernel<128>, grid, dim3(256), 0, st, a); break;
-        case 256: hipLaunchKernelGGL(attn_kernel<256>, grid, dim3(256), 0, st, a); break;
+        case 64: GSD_ATTN_G(64) break;
+        case 128: GSD_ATTN_G(128) break;
+        case 256: GSD_ATTN_G(256) break;
         default: return hipErrorInvalidValue;
     }
+#undef GSD_ATTN_G
+    return hipGetLastError();
+}
+
+hipError_t launch_lrprep(const LrPrep& p, hipStream_t st) {
+    if (p.cols % 4) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(lrprep_kernel, dim3(p.nseg * kMaxRank), dim3(256), 0, st, p);
     return hipGetLastError();
 }
 

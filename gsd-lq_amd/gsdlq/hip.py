@@ -44,6 +44,7 @@ SIGNATURES = {
     "gsdh_model_capture_end": [vp, ctypes.POINTER(vp)],
     "gsdh_graph_launch": [vp, vp, i32],
     "gsdh_graph_destroy": [vp],
+    "gsdh_graph_time": [vp, vp, i32, ctypes.POINTER(f32)],
 }
 RESTYPES = {"gsdh_model_device_bytes": (u64, [vp]), "gsdh_model_stream": (vp, [vp]),
             "gsdh_last_error": (ctypes.c_char_p, [])}

@@ -86,7 +86,7 @@ int gsdh_rope_and_store_kv(void* stream, float* q, const float* k, const float* 
 
 /* gsd_cpu_gqa_attention (gsd_lq_cpu_engine.c:264-330): softmax(q.K/scale)V
  * over cached positions 0..pos, split over the context (flash-decoding);
- * head_dim must be a multiple of 8, <= 256; n_heads/n_kv_heads <= 8. */
+ * head_dim must be 64, 128 or 256; n_heads/n_kv_heads must be 1, 2, 4 or 8. */
 int gsdh_gqa_attention(void* stream, const float* q, const uint16_t* k_cache,
                        const uint16_t* v_cache, float* attn_out, int layer_idx, int pos,
                        int n_heads, int n_kv_heads, int head_dim, int max_seq_len, float sm_scale);
@@ -161,6 +161,9 @@ int gsdh_model_capture_begin(gsdh_model* m);
 int gsdh_model_capture_end(gsdh_model* m, void** graph_exec_out);
 int gsdh_graph_launch(gsdh_model* m, void* graph_exec, int n_times);
 int gsdh_graph_destroy(void* graph_exec);
+/* n_times launches of graph_exec on the model stream bracketed by HIP events;
+ * *ms_out = elapsed milliseconds between the two events. */
+int gsdh_graph_time(gsdh_model* m, void* graph_exec, int n_times, float* ms_out);
 void* gsdh_model_stream(gsdh_model* m);
 
 #ifdef __cplusplus

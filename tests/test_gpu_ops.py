@@ -18,9 +18,9 @@ TOL = 1e-3
 
 @pytest.fixture(scope="module")
 def lib():
-    import torch
-    assert torch.cuda.is_available(), "GPU tests need a GPU"
     from gsdlq import hip
+    name, total, ncu = hip.device_info()     # raises when no GPU is visible
+    assert ncu > 0, name
     return hip.lib()
 
 
@@ -38,7 +38,8 @@ def _gpu_matvec(lib, f, x, tmp_k=None):
     if k:
         tk = D(np.asarray(tmp_k, np.float32))
     bufs = {key: D(f[key]) for key in ("codes", "scales", "row_ptr", "kink_cols", "kink_deltas", "U")}
-    lib.gsdh_hex2d_matvec(None, p(D(x)), p(bufs["codes"]), p(bufs["scales"]), p(D(xy)), p(bufs["U"]) if k else None,
+    dx, dxy = D(x), D(xy)    # hold every buffer until the result is read back
+    lib.gsdh_hex2d_matvec(None, p(dx), p(bufs["codes"]), p(bufs["scales"]), p(dxy), p(bufs["U"]) if k else None,
                           p(tk), p(bufs["row_ptr"]), p(bufs["kink_cols"]), p(bufs["kink_deltas"]), p(y), rows, cols,
                           k, n_pts)
     return H(y, np.float32, rows)
@@ -94,8 +95,8 @@ def test_unpack_codes_bitexact(lib, R):
     n_pts = codebook.n_points(R)
     codes = np.concatenate([np.arange(n_pts, dtype=np.uint8),
                             np.random.default_rng(R).integers(0, n_pts, 100000).astype(np.uint8)])
-    idx, r01 = E(codes.size * 4), E(codes.size * 2)
-    lib.gsdh_unpack_codes(None, p(D(codes)), codes.size, R, p(idx), p(r01))
+    idx, r01, dc = E(codes.size * 4), E(codes.size * 2), D(codes)
+    lib.gsdh_unpack_codes(None, p(dc), codes.size, R, p(idx), p(r01))
     assert np.array_equal(H(idx, np.int32, codes.size), codes.astype(np.int32))
     want = codebook.integer_fields(R)[codes]
     assert np.array_equal(H(r01, np.int8, codes.size * 2).reshape(-1, 2), want)
@@ -103,16 +104,17 @@ def test_unpack_codes_bitexact(lib, R):
 
 def test_lowrank_rmsnorm_swiglu_add(lib, golden):
     g = golden
+    d = {k: D(g[k]) for k in ("lr_x", "lr_Vt", "lr_S", "rms_x", "rms_w", "sw_gate", "sw_up")}
     tk = E(64)
-    lib.gsdh_lowrank_proj(None, p(D(g["lr_x"])), p(D(g["lr_Vt"])), p(D(g["lr_S"])), p(tk), 4, 256)
+    lib.gsdh_lowrank_proj(None, p(d["lr_x"]), p(d["lr_Vt"]), p(d["lr_S"]), p(tk), 4, 256)
     assert rel_l2(H(tk, np.float32, 4), g["lr_out"]) < 1e-6
     out = E(4096 * 4)
-    lib.gsdh_rmsnorm(None, p(D(g["rms_x"])), p(D(g["rms_w"])), p(out), 4096, 1e-5)
+    lib.gsdh_rmsnorm(None, p(d["rms_x"]), p(d["rms_w"]), p(out), 4096, 1e-5)
     assert rel_l2(H(out, np.float32, 4096), g["rms_out"]) < 1e-6
     out = E(4000)
-    lib.gsdh_swiglu(None, p(D(g["sw_gate"])), p(D(g["sw_up"])), p(out), 1000)
+    lib.gsdh_swiglu(None, p(d["sw_gate"]), p(d["sw_up"]), p(out), 1000)
     assert rel_l2(H(out, np.float32, 1000), g["sw_out"]) < 1e-6
-    lib.gsdh_vec_add(None, p(out), p(D(g["sw_gate"])), p(D(g["sw_up"])), 1000)
+    lib.gsdh_vec_add(None, p(out), p(d["sw_gate"]), p(d["sw_up"]), 1000)
     assert np.array_equal(H(out, np.float32, 1000), g["add_out"])
 
 
@@ -120,21 +122,21 @@ def test_lowrank_rmsnorm_swiglu_add(lib, golden):
 @pytest.mark.parametrize("il", [1, 0])
 def test_rope_kv_bitexact(lib, golden, pos, il):
     t = f"rope_p{pos}_i{il}"
-    q = D(golden[t + "_q"])
+    q, dk, dv = D(golden[t + "_q"]), D(golden[t + "_k"]), D(golden[t + "_v"])
     kc, vc = E(2048 * 8 * 128 * 2), E(2048 * 8 * 128 * 2)
-    lib.gsdh_rope_and_store_kv(None, p(q), p(D(golden[t + "_k"])), p(D(golden[t + "_v"])), p(kc), p(vc), 0, pos,
+    lib.gsdh_rope_and_store_kv(None, p(q), p(dk), p(dv), p(kc), p(vc), 0, pos,
                                32, 8, 128, 2048, 1e6, il)
-    assert np.array_equal(H(q, np.uint32), golden[t + "_qout"].view(np.uint32))
-    assert np.array_equal(H(kc, np.uint16).reshape(2048, 8, 128)[pos], golden[t + "_kc"])
-    assert np.array_equal(H(vc, np.uint16).reshape(2048, 8, 128)[pos], golden[t + "_vc"])
+    assert np.array_equal(H(q, np.uint32, 32 * 128), golden[t + "_qout"].view(np.uint32))
+    assert np.array_equal(H(kc, np.uint16, 2048 * 8 * 128).reshape(2048, 8, 128)[pos], golden[t + "_kc"])
+    assert np.array_equal(H(vc, np.uint16, 2048 * 8 * 128).reshape(2048, 8, 128)[pos], golden[t + "_vc"])
 
 
 @pytest.mark.parametrize("ctx", [1, 33, 512])
 def test_attention_golden(lib, golden, ctx):
     from make_golden import attn_cache
     kc, vc = attn_cache(ctx, "k", 512, 8, 128), attn_cache(ctx, "v", 512, 8, 128)
-    out = E(32 * 128 * 4)
-    lib.gsdh_gqa_attention(None, p(D(golden[f"attn{ctx}_q"])), p(D(kc)), p(D(vc)), p(out), 0, ctx - 1, 32, 8,
+    out, dq, dk, dv = E(32 * 128 * 4), D(golden[f"attn{ctx}_q"]), D(kc), D(vc)
+    lib.gsdh_gqa_attention(None, p(dq), p(dk), p(dv), p(out), 0, ctx - 1, 32, 8,
                            128, 512, 1.0 / float(np.sqrt(128)))
     assert rel_l2(H(out, np.float32, 32 * 128), golden[f"attn{ctx}_out"]) < TOL
 
