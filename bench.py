@@ -141,7 +141,7 @@ def bench_linear(bank, steps, warmup):
     ach = gu_bytes / (per_launch_ms * 1e-3) / 1e9
     roof = {"kernel": "hexmv_kernel (fused RMSNorm + gate/up matvec + SwiGLU, 2x14336x4096)",
             "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(),
             "launch_us": round(per_launch_ms * 1e3, 2), "alg_bytes_per_launch": int(gu_bytes)}
     for g in (ge, gu):
         lib.gsdh_graph_destroy(g)
@@ -192,6 +192,56 @@ def cpu_baseline(bank, seconds=12.0):
                       f"built with the reference flags (clang -O3 -fopenmp)"}
 
 
+def probe(kind: str, n: int):
+    """Launch one kernel repeatedly for counter collection under rocprofv3:
+    'gateup' = the fused gate/up matvec over 8 rotated Turbo layers,
+    'copy' = a 256 MiB device copy (the calibration of FETCH/WRITE_SIZE)."""
+    from gsdlq import hip
+    lib = hip.lib()
+    if kind == "copy":
+        nbytes = 256 << 20
+        a, b = ctypes.c_void_p(), ctypes.c_void_p()
+        lib.gsdh_malloc(ctypes.byref(a), nbytes)
+        lib.gsdh_malloc(ctypes.byref(b), nbytes)
+        for _ in range(n):
+            lib.gsdh_stream_copy(None, b, a, nbytes)
+        lib.gsdh_stream_sync(None)
+        lib.gsdh_free(a)
+        lib.gsdh_free(b)
+        print(f"[probe] copy {nbytes} bytes x {n}", flush=True)
+        return
+    bank = LayerBank("turbo", 8)
+    model = build_model(bank, bank.n)
+    model.forward_token(1, 0)
+    for i in range(n):
+        lib.gsdh_model_run_linear(model._m, i % bank.n, 4)
+    lib.gsdh_stream_sync(lib.gsdh_model_stream(model._m))
+    gu = sum(alg_bytes(bank.packed[(0, t)]) for t in ("ffn_gate", "ffn_up")) - 4 * H
+    print(f"[probe] gate/up launches {n}, algorithmic bytes per launch {gu}", flush=True)
+    model.close()
+
+
+def traffic_from_profile():
+    """HBM bytes per gate/up launch from the committed counter summary
+    (profiles/hexmv_gateup_traffic.txt: FETCH_SIZE and WRITE_SIZE per
+    dispatch of the kernel and of a 256 MiB copy), or None."""
+    path = os.path.join(ROOT, "profiles", "hexmv_gateup_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    kv = {}
+    for line in open(path):
+        if "=" in line and not line.lstrip().startswith("#"):
+            k, v = line.split("=", 1)
+            kv[k.strip()] = v.strip().split()[0]
+    try:
+        copy_bytes = float(kv["copy_bytes"])
+        f_scale = copy_bytes / float(kv["copy_fetch_kib"])
+        w_scale = copy_bytes / float(kv["copy_write_kib"])
+        return int(float(kv["gateup_fetch_kib"]) * f_scale + float(kv["gateup_write_kib"]) * w_scale)
+    except (KeyError, ValueError, ZeroDivisionError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -201,7 +251,11 @@ def main():
     ap.add_argument("--no-precision", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--probe", choices=["gateup", "copy"], help="run one kernel for rocprofv3 counters")
     a = ap.parse_args()
+    if a.probe:
+        probe(a.probe, max(a.steps, 1))
+        return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the decode path has no multi-GPU mode in this build "
               "(sharding is design-only); run with --gpus 1", file=sys.stderr)

@@ -70,9 +70,12 @@ struct AttnScratch {
     size_t n_counters = 0;
 } g_attn;
 
+// Positions per attention split: enough splits to spread long contexts over
+// the chip (n_kv * splits ~ 256 blocks), at least 64 and at most 256
+// positions each (256 is the kernel's LDS score buffer).
 int choose_chunk(int n_ctx, int n_kv) {
-    int c = (n_ctx * n_kv + 511) / 512;
-    c = (c + 31) / 32 * 32;
+    int c = (n_ctx * n_kv + 255) / 256;
+    c = (c + 63) / 64 * 64;
     if (c < 64) c = 64;
     if (c > 256) c = 256;
     return c;
@@ -111,6 +114,10 @@ int gsdh_memcpy_h2d(void* dst, const void* src, uint64_t n, void* stream) {
 }
 int gsdh_memcpy_d2h(void* dst, const void* src, uint64_t n, void* stream) {
     HIPCHK(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, S(stream)));
+    return 0;
+}
+int gsdh_stream_copy(void* stream, void* dst, const void* src, uint64_t nbytes) {
+    HIPCHK(launch_copy(src, dst, nbytes, S(stream)));
     return 0;
 }
 int gsdh_stream_sync(void* stream) {

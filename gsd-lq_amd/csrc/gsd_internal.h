@@ -124,6 +124,8 @@ hipError_t launch_fill_u32(unsigned* p, unsigned v, size_t n, hipStream_t stream
 hipError_t launch_unpack(const uint8_t* codes, int64_t n, int radius, int32_t* idx,
                          int8_t* r01, hipStream_t stream);
 
+hipError_t launch_copy(const void* src, void* dst, size_t nbytes, hipStream_t stream);
+
 int device_cu_count();
 
 }  // namespace gsd

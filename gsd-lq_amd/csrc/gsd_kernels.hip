@@ -138,6 +138,7 @@ __global__ void __launch_bounds__(NWM * 64) hexmv_kernel(const HexArgs a) {
 
     uint4 cw[SPT][RB];
     uint32_t sv[SPT][RB];
+    uint4 uw[2];   // epilogue threads: U row (k <= 16 fp16) of their row, fetched with the batch
     // Issue every load of batch b: RB x SPT 16-byte code loads and the
     // matching scales, rows and slots clamped in range (results of padding
     // rows/slots are discarded later), no branches between the loads.
@@ -152,6 +153,22 @@ __global__ void __launch_bounds__(NWM * 64) hexmv_kernel(const HexArgs a) {
                 const int row = min(br.r0 + (paired ? (rr & 3) : rr), a.seg[g].rows - 1);
                 cw[j][rr] = *reinterpret_cast<const uint4*>(a.seg[g].codes + (size_t)row * rowbytes + (size_t)s * 16);
                 if (!ST) sv[j][rr] = a.seg[g].scales[(size_t)row * nsb + (s >> 1)];
+            }
+            if (j == 0 && tid < RB) {
+                const int g = paired ? (tid >> 2) : br.g0;
+                const int kk = a.seg[g].k;
+                if (kk > 0) {
+                    const int row = min(br.r0 + (paired ? (tid & 3) : tid), a.seg[g].rows - 1);
+                    const uint16_t* up = a.seg[g].U + (size_t)row * kk;
+                    // U rows are 2*k bytes: fetch as 16-bit loads into the two vectors
+                    uint16_t tmp[16];
+#pragma unroll
+                    for (int q = 0; q < 16; q++) tmp[q] = q < kk ? up[q] : (uint16_t)0;
+                    uw[0] = make_uint4(tmp[0] | (uint32_t)tmp[1] << 16, tmp[2] | (uint32_t)tmp[3] << 16,
+                                       tmp[4] | (uint32_t)tmp[5] << 16, tmp[6] | (uint32_t)tmp[7] << 16);
+                    uw[1] = make_uint4(tmp[8] | (uint32_t)tmp[9] << 16, tmp[10] | (uint32_t)tmp[11] << 16,
+                                       tmp[12] | (uint32_t)tmp[13] << 16, tmp[14] | (uint32_t)tmp[15] << 16);
+                }
             }
             if (ST) {
 #pragma unroll
@@ -276,6 +293,7 @@ __global__ void __launch_bounds__(NWM * 64) hexmv_kernel(const HexArgs a) {
                 }
             }
         }
+        const uint4 uw_cur[2] = {uw[0], uw[1]};
         // next batch's loads fly during the reduction and the epilogue
         if (b + (int)gridDim.x < a.nbatch) issue(b + gridDim.x);
 
@@ -302,7 +320,9 @@ __global__ void __launch_bounds__(NWM * 64) hexmv_kernel(const HexArgs a) {
                         t += sg.kdel[i] * xc;
                     }
                 }
-                for (int jj = 0; jj < sg.k; jj++) t += h2f(sg.U[(size_t)row * sg.k + jj]) * tkl[g][jj];
+                const uint32_t uu[8] = {uw_cur[0].x, uw_cur[0].y, uw_cur[0].z, uw_cur[0].w,
+                                        uw_cur[1].x, uw_cur[1].y, uw_cur[1].z, uw_cur[1].w};
+                for (int jj = 0; jj < sg.k; jj++) t += h2f((uint16_t)(uu[jj >> 1] >> (16 * (jj & 1)))) * tkl[g][jj];
                 if (a.epilogue == kEpiStore) sg.out[row] = t;
                 else if (a.epilogue == kEpiResidual) a.resid[row] = a.resid[row] + t;
             }
@@ -377,8 +397,12 @@ hipError_t launch_hexmv_t(const HexArgs& a, hipStream_t st, int nt) {
             n = 1;
         per_cu = n;
     }
+    // persistent grid (as many blocks as are resident, each looping over
+    // batches with the next batch's loads in flight); GSD_HEXMV_PERSIST=0
+    // launches one block per batch instead
+    static const int persist = getenv("GSD_HEXMV_PERSIST") ? atoi(getenv("GSD_HEXMV_PERSIST")) : 1;
     const int ncu = device_cu_count() > 0 ? device_cu_count() : 256;
-    int grid = ncu * per_cu;
+    int grid = persist ? ncu * per_cu : b.nbatch;
     if (grid > b.nbatch) grid = b.nbatch;
     hipLaunchKernelGGL((hexmv_kernel<SPT, NWM, ST>), dim3(grid), dim3(nt), 0, st, b);
     return hipGetLastError();
@@ -518,7 +542,6 @@ __global__ void __launch_bounds__(256) attn_kernel(const AttnArgs a) {
     __shared__ float sc[G][256];
     __shared__ float part[4][G][HD];
     __shared__ float ml[2][G];
-    __shared__ int s_last;
 
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int sub = lane % LPP, prow = lane / LPP;
@@ -632,7 +655,7 @@ __global__ void __launch_bounds__(256) attn_kernel(const AttnArgs a) {
         }
         return;
     }
-    // partials [kvh][split][g][2+HD], merged by the last block of this KV head
+    // partials [kvh][split][g][2+HD]; attn_merge_kernel combines them
     float* wsb = a.ws + ((size_t)kvh * a.max_splits + split) * G * (2 + HD);
     for (int i = tid; i < G * HD; i += 256) {
         const int g = i / HD, d = i % HD;
@@ -642,66 +665,79 @@ __global__ void __launch_bounds__(256) attn_kernel(const AttnArgs a) {
         wsb[tid * (2 + HD)] = ml[0][tid];
         wsb[tid * (2 + HD) + 1] = ml[1][tid];
     }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned prev = atomicAdd(&a.counters[kvh], 1u);
-        s_last = (prev == (unsigned)(nsplit - 1));
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    const float* base = a.ws + (size_t)kvh * a.max_splits * G * (2 + HD);
-    for (int i = tid; i < G * HD; i += 256) {
-        const int g = i / HD, d = i % HD;
-        float M = -INFINITY;
-        for (int sp = 0; sp < nsplit; sp++) M = fmaxf(M, __builtin_nontemporal_load(base + ((size_t)sp * G + g) * (2 + HD)));
-        float L = 0.f, O = 0.f;
-        for (int sp = 0; sp < nsplit; sp++) {
-            const float* pp = base + ((size_t)sp * G + g) * (2 + HD);
-            const float f = expf(__builtin_nontemporal_load(pp) - M);
-            L = fmaf(__builtin_nontemporal_load(pp + 1), f, L);
-            O = fmaf(__builtin_nontemporal_load(pp + 2 + d), f, O);
-        }
-        a.out[(size_t)(group_base + g) * HD + d] = O / L;
-    }
-    if (tid == 0) a.counters[kvh] = 0u;
 }
 
-// One block per (segment, j): RMSNorm factor and tmp_k of one launch.
+// Merge of the per-split softmax partials (stream order after attn_kernel
+// makes them visible); a no-op when the context fits one split, in which
+// case attn_kernel wrote the output itself.  grid = n_heads blocks of HD.
+__global__ void attn_merge_kernel(const AttnArgs a) {
+    const int pos = a.pos_dev ? *a.pos_dev : a.pos;
+    const int nsplit = (pos + 1 + a.chunk - 1) / a.chunk;
+    if (nsplit <= 1) return;
+    const int G = a.n_heads / a.n_kv;
+    const int h = blockIdx.x, kvh = h / G, g = h % G, d = threadIdx.x;
+    const int HD = a.hd;
+    const float* base = a.ws + (size_t)kvh * a.max_splits * G * (2 + HD) + (size_t)g * (2 + HD);
+    const size_t sstride = (size_t)G * (2 + HD);
+    float M = -INFINITY;
+    for (int sp = 0; sp < nsplit; sp++) M = fmaxf(M, base[sp * sstride]);
+    float L = 0.f, O = 0.f;
+    for (int sp = 0; sp < nsplit; sp++) {
+        const float* pp = base + sp * sstride;
+        const float f = expf(pp[0] - M);
+        L = fmaf(pp[1], f, L);
+        O = fmaf(pp[2 + d], f, O);
+    }
+    a.out[(size_t)h * HD + d] = O / L;
+}
+
+// One block per (segment, j): RMSNorm factor and tmp_k of one launch.  Each
+// thread owns up to 64 columns; all of its loads are issued before any use.
 __global__ void __launch_bounds__(256) lrprep_kernel(const LrPrep p) {
     __shared__ float scratch[16];
     const int g = blockIdx.x / kMaxRank, j = blockIdx.x % kMaxRank;
     if (g >= p.nseg || j >= (p.k[g] > 0 ? p.k[g] : (g == 0 && j == 0 ? 1 : 0))) return;
+    constexpr int Q = 16;   // float4 groups per thread: 256 * 16 * 4 = 16384 columns per pass
+    const bool lr = p.k[g] > 0;
+    const uint16_t* vt = lr ? p.Vt[g] + (size_t)j * p.cols : nullptr;
+    float ss = 0.f, d = 0.f;
+    for (int c0 = 0; c0 < p.cols; c0 += 256 * Q * 4) {
+        float4 xv[Q], wv[Q];
+        uint2 hv[Q];
+#pragma unroll
+        for (int q = 0; q < Q; q++) {
+            const int c = c0 + (q * 256 + (int)threadIdx.x) * 4;
+            const bool in = c < p.cols;
+            xv[q] = in ? *reinterpret_cast<const float4*>(p.x + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+            wv[q] = (in && p.norm_w) ? *reinterpret_cast<const float4*>(p.norm_w + c) : make_float4(1.f, 1.f, 1.f, 1.f);
+            hv[q] = (in && lr) ? *reinterpret_cast<const uint2*>(vt + c) : make_uint2(0u, 0u);
+        }
+#pragma unroll
+        for (int q = 0; q < Q; q++) {
+            ss = fmaf(xv[q].x, xv[q].x, ss); ss = fmaf(xv[q].y, xv[q].y, ss);
+            ss = fmaf(xv[q].z, xv[q].z, ss); ss = fmaf(xv[q].w, xv[q].w, ss);
+        }
+        if (lr) {
+            // held until the norm factor is known: x' = (x * inv) * w
+            // (accumulated as x * w * Vt, times inv afterwards)
+#pragma unroll
+            for (int q = 0; q < Q; q++) {
+                d = fmaf(xv[q].x * wv[q].x, h2f((uint16_t)(hv[q].x & 0xFFFFu)), d);
+                d = fmaf(xv[q].y * wv[q].y, h2f((uint16_t)(hv[q].x >> 16)), d);
+                d = fmaf(xv[q].z * wv[q].z, h2f((uint16_t)(hv[q].y & 0xFFFFu)), d);
+                d = fmaf(xv[q].w * wv[q].w, h2f((uint16_t)(hv[q].y >> 16)), d);
+            }
+        }
+    }
     float inv = 1.f;
     if (p.norm_w) {
-        float ss = 0.f;
-        for (int c = threadIdx.x * 4; c < p.cols; c += 1024) {
-            const float4 v = *reinterpret_cast<const float4*>(p.x + c);
-            ss = fmaf(v.x, v.x, ss); ss = fmaf(v.y, v.y, ss); ss = fmaf(v.z, v.z, ss); ss = fmaf(v.w, v.w, ss);
-        }
         ss = block_sum(ss, scratch);
         inv = 1.0f / sqrtf(ss / (float)p.cols + p.eps);
     }
     if (g == 0 && j == 0 && threadIdx.x == 0) p.out[0] = inv;
-    if (p.k[g] <= 0) return;
-    const uint16_t* vt = p.Vt[g] + (size_t)j * p.cols;
-    float d = 0.f;
-    for (int c = threadIdx.x * 4; c < p.cols; c += 1024) {
-        const float4 v = *reinterpret_cast<const float4*>(p.x + c);
-        const uint2 h = *reinterpret_cast<const uint2*>(vt + c);
-        float4 w = make_float4(1.f, 1.f, 1.f, 1.f);
-        if (p.norm_w) w = *reinterpret_cast<const float4*>(p.norm_w + c);
-        const float xs[4] = {v.x, v.y, v.z, v.w}, ws[4] = {w.x, w.y, w.z, w.w};
-        const uint16_t hv[4] = {(uint16_t)(h.x & 0xFFFF), (uint16_t)(h.x >> 16), (uint16_t)(h.y & 0xFFFF), (uint16_t)(h.y >> 16)};
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const float xe = p.norm_w ? (xs[e] * inv) * ws[e] : xs[e];
-            d = fmaf(xe, h2f(hv[e]), d);
-        }
-    }
+    if (!lr) return;
     d = block_sum(d, scratch);
-    if (threadIdx.x == 0) p.out[1 + kMaxRank * g + j] = d * p.S[g][j];
+    if (threadIdx.x == 0) p.out[1 + kMaxRank * g + j] = (d * inv) * p.S[g][j];
 }
 
 __global__ void embed_kernel(const uint16_t* embed, const int* token, float* x, int hidden) {
@@ -774,6 +810,12 @@ __global__ void __launch_bounds__(1024) argmax_kernel(const float* logits, int n
     }
 }
 
+// Plain 16-byte streaming copy (HBM calibration: its FETCH_SIZE/WRITE_SIZE per
+// dispatch against its known size gives the counter scale).
+__global__ void __launch_bounds__(256) copy_kernel(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) dst[i] = src[i];
+}
+
 __global__ void fill_u32_kernel(unsigned* p, unsigned v, size_t n) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = v;
@@ -803,11 +845,11 @@ __global__ void unpack_kernel(const uint8_t* codes, int64_t n, int R, int32_t* i
 // ------------------------------------------------------------------------
 hipError_t launch_hexmv(const HexArgs& a, hipStream_t st) {
     const int S = a.cols >> 5;
-    // slots per thread: 2 halves the threads per row (one wave covers 4096
-    // columns) at the price of more VGPRs; GSD_HEXMV_SPT=1|2 overrides
+    // slots per thread: 1 (measured fastest: fewer VGPRs, more waves per CU);
+    // GSD_HEXMV_SPT=2 halves the threads per row for experiments
     static const int force_spt = getenv("GSD_HEXMV_SPT") ? atoi(getenv("GSD_HEXMV_SPT")) : 0;
-    int spt = (S % 128 == 0) ? 2 : 1;
-    if (force_spt == 1 || (force_spt == 2 && S % 128 == 0)) spt = force_spt;
+    int spt = 1;
+    if (force_spt == 2 && S % 128 == 0) spt = 2;
     const int nt = ((S + spt - 1) / spt + 63) / 64 * 64;
     if (nt > 1024) return hipErrorInvalidValue;
     const bool st_layout = a.scale_t != 0;
@@ -890,6 +932,9 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
         default: return hipErrorInvalidValue;
     }
 #undef GSD_ATTN_G
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(a.n_heads), dim3(a.hd), 0, st, a);
     return hipGetLastError();
 }
 
@@ -919,6 +964,17 @@ hipError_t launch_fill_u32(unsigned* p, unsigned v, size_t n, hipStream_t st) {
 hipError_t launch_unpack(const uint8_t* codes, int64_t n, int radius, int32_t* idx, int8_t* r01, hipStream_t st) {
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(unpack_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, codes, n, radius, idx, r01);
+    return hipGetLastError();
+}
+
+hipError_t launch_copy(const void* src, void* dst, size_t nbytes, hipStream_t st) {
+    if (nbytes % 16) return hipErrorInvalidValue;
+    const size_t n = nbytes / 16;
+    if (n == 0) return hipSuccess;
+    size_t grid = (n + 255) / 256;
+    if (grid > 4096) grid = 4096;
+    hipLaunchKernelGGL(copy_kernel, dim3((unsigned)grid), dim3(256), 0, st, reinterpret_cast<const uint4*>(src),
+                       reinterpret_cast<uint4*>(dst), n);
     return hipGetLastError();
 }
 

@@ -23,6 +23,7 @@ SIGNATURES = {
     "gsdh_memcpy_h2d": [vp, vp, u64, vp],
     "gsdh_memcpy_d2h": [vp, vp, u64, vp],
     "gsdh_stream_sync": [vp],
+    "gsdh_stream_copy": [vp, vp, vp, u64],
     "gsdh_rmsnorm": [vp, vp, vp, vp, i32, f32],
     "gsdh_vec_add": [vp, vp, vp, vp, i32],
     "gsdh_swiglu": [vp, vp, vp, vp, i32],

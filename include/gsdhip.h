@@ -46,6 +46,9 @@ int gsdh_free(void* ptr);
 int gsdh_memcpy_h2d(void* dst, const void* src, uint64_t nbytes, void* stream);
 int gsdh_memcpy_d2h(void* dst, const void* src, uint64_t nbytes, void* stream);
 int gsdh_stream_sync(void* stream);
+/* Plain device-to-device copy by a 16-byte streaming kernel (nbytes % 16 == 0);
+ * used to calibrate HBM traffic counters against a known byte count. */
+int gsdh_stream_copy(void* stream, void* dst, const void* src, uint64_t nbytes);
 
 /* ------------------------------------------------------------------------ */
 /* 1. Operator twins of gsd_lq_cpu_engine.c                                  */
