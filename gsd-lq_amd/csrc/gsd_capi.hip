@@ -49,6 +49,27 @@ std::vector<float> host_table(int R) {
     return t;
 }
 
+// Integer fields (r0, r1) of the radius-R codewords in enumeration order, as
+// fp16 pairs (low half r0): the lattice form of the same table.
+uint16_t half_of_small_int(int n) {
+    if (n == 0) return 0;
+    const uint16_t sign = n < 0 ? 0x8000u : 0u;
+    unsigned a = (unsigned)(n < 0 ? -n : n), e = 0;
+    while ((a >> (e + 1)) != 0) e++;
+    const unsigned mant = (a << (10 - e)) & 0x3FFu;
+    return (uint16_t)(sign | ((e + 15u) << 10) | mant);
+}
+
+std::vector<uint32_t> host_fields(int R) {
+    std::vector<uint32_t> t;
+    for (int a = -R; a <= R; a++)
+        for (int b = -R; b <= R; b++) {
+            if (std::abs(a + b) > R) continue;
+            t.push_back((uint32_t)half_of_small_int(a) | ((uint32_t)half_of_small_int(b) << 16));
+        }
+    return t;
+}
+
 // RoPE angles exactly as gsd_lq_cpu_engine.c:213-218 evaluates them (C library
 // powf/cosf/sinf in float), so the device rotation sees identical cos/sin.
 __attribute__((noinline)) void rope_cs(float theta, int hd, int pos, float* out /* 2*hd/2 */) {
@@ -253,7 +274,8 @@ struct HexDev {
 struct gsdh_model {
     gsdh_model_config c{};
     hipStream_t stream = nullptr;
-    float* tables[9] = {};          // by radius
+    float* tables[9] = {};          // by radius: codeword points
+    uint32_t* fields[9] = {};       // by radius: (r0, r1) fp16 pairs
     uint16_t* embed = nullptr;
     float* norms = nullptr;         // [n_layers][2][hidden] + output [hidden]
     std::vector<HexDev> hex;        // n_layers * 7 + 1
@@ -262,7 +284,8 @@ struct gsdh_model {
     float2* cs = nullptr;
     float* ws = nullptr;
     unsigned* counters = nullptr;
-    float* lrbuf = nullptr;         // RMSNorm factor + tmp_k of the launch in flight
+    unsigned long long* pub = nullptr;   // rank-k publication words, one range per matvec launch
+    int pub_words = 0, pub_next = 0;
     int chunk = 64, max_splits = 1;
     StepState* st = nullptr;        // device
     StepState* st_host = nullptr;   // pinned
@@ -290,29 +313,25 @@ int dalloc(gsdh_model* m, void** p, size_t n) {
     return 0;
 }
 
-void fill_seg(HexSeg& s, const HexDev& t, float* const* tables, float* out) {
+void fill_seg(HexSeg& s, const HexDev& t, const gsdh_model* m, float* out) {
     s.codes = t.codes; s.scales = t.scales; s.row_ptr = t.nk ? t.row_ptr : nullptr;
     s.kcols = t.kcols; s.kdel = t.kdel; s.U = t.U; s.Vt = t.Vt; s.S = t.Sv; s.tmp_k = nullptr;
-    s.table = tables[t.radius]; s.out = out; s.rows = t.rows; s.k = t.k;
+    s.table = m->tables[t.radius]; s.fields = m->fields[t.radius]; s.out = out; s.rows = t.rows; s.k = t.k;
     s.n_pts = 3 * t.radius * t.radius + 3 * t.radius + 1;
 }
 
-// RMSNorm factor and rank-k projections of a launch's segments, computed once
-// by a small kernel (one block per segment and rank) instead of in every block
-// of the matvec; the matvec then reads them from m->lrbuf.
+// Rank-k segments publish their projections inside the matvec launch (blocks
+// 0..sum(k)-1): give the launch the next sum(k) publication words of the
+// sequence (zeroed at its start) and the error word.
 int prep_lowrank(gsdh_model* m, HexArgs& a) {
-    LrPrep p{};
-    bool any = false;
-    for (int g = 0; g < a.nseg; g++) {
-        p.Vt[g] = a.seg[g].Vt; p.S[g] = a.seg[g].S; p.k[g] = a.seg[g].k;
-        any = any || a.seg[g].k > 0;
-    }
-    if (!any) return 0;
-    p.x = a.x; p.norm_w = a.norm_w; p.eps = a.eps; p.cols = a.cols; p.nseg = a.nseg; p.out = m->lrbuf;
-    HIPCHK(launch_lrprep(p, m->stream));
-    for (int g = 0; g < a.nseg; g++)
-        if (a.seg[g].k > 0) a.seg[g].tmp_k = m->lrbuf + 1 + kMaxRank * g;
-    if (a.norm_w) a.inv_dev = m->lrbuf;
+    int nlead = 0;
+    for (int g = 0; g < a.nseg; g++) nlead += a.seg[g].k;
+    if (nlead == 0) return 0;
+    if (m->pub_next + nlead > m->pub_words)
+        return fail(-1, "rank-k publication words exhausted (%d + %d > %d)", m->pub_next, nlead, m->pub_words);
+    a.pub = m->pub + m->pub_next;
+    a.err = &m->st->err;
+    m->pub_next += nlead;
     return 0;
 }
 
@@ -322,9 +341,9 @@ int issue_linear(gsdh_model* m, int l, int mask) {
     if (mask & 1) {   // q, k, v: fused attention RMSNorm; interleaved RoPE + KV append in the epilogue
         HexArgs a{};
         a.nseg = 3;
-        fill_seg(a.seg[0], m->slot(l, GSDH_Q), m->tables, m->q);
-        fill_seg(a.seg[1], m->slot(l, GSDH_K), m->tables, m->k);
-        fill_seg(a.seg[2], m->slot(l, GSDH_V), m->tables, m->v);
+        fill_seg(a.seg[0], m->slot(l, GSDH_Q), m, m->q);
+        fill_seg(a.seg[1], m->slot(l, GSDH_K), m, m->k);
+        fill_seg(a.seg[2], m->slot(l, GSDH_V), m, m->v);
         a.x = m->x; a.norm_w = m->norm(l, 0); a.eps = c.rms_eps; a.cols = c.hidden; a.epilogue = kEpiStore;
         a.scale_t = 1;
         if (c.rope_interleaved) {
@@ -340,7 +359,7 @@ int issue_linear(gsdh_model* m, int l, int mask) {
     if (mask & 2) {   // o projection + residual
         HexArgs a{};
         a.nseg = 1;
-        fill_seg(a.seg[0], m->slot(l, GSDH_O), m->tables, m->x);
+        fill_seg(a.seg[0], m->slot(l, GSDH_O), m, m->x);
         a.x = m->attn; a.cols = c.n_heads * c.head_dim; a.epilogue = kEpiResidual; a.resid = m->x;
         a.scale_t = 1;
         if ((rc = prep_lowrank(m, a))) return rc;
@@ -349,8 +368,8 @@ int issue_linear(gsdh_model* m, int l, int mask) {
     if (mask & 4) {   // gate + up with fused FFN RMSNorm and SwiGLU
         HexArgs a{};
         a.nseg = 2;
-        fill_seg(a.seg[0], m->slot(l, GSDH_GATE), m->tables, m->h);
-        fill_seg(a.seg[1], m->slot(l, GSDH_UP), m->tables, nullptr);
+        fill_seg(a.seg[0], m->slot(l, GSDH_GATE), m, m->h);
+        fill_seg(a.seg[1], m->slot(l, GSDH_UP), m, nullptr);
         a.x = m->x; a.norm_w = m->norm(l, 1); a.eps = c.rms_eps; a.cols = c.hidden; a.epilogue = kEpiSwiGLU;
         a.scale_t = 1;
         if ((rc = prep_lowrank(m, a))) return rc;
@@ -359,7 +378,7 @@ int issue_linear(gsdh_model* m, int l, int mask) {
     if (mask & 8) {   // down projection + residual
         HexArgs a{};
         a.nseg = 1;
-        fill_seg(a.seg[0], m->slot(l, GSDH_DOWN), m->tables, m->x);
+        fill_seg(a.seg[0], m->slot(l, GSDH_DOWN), m, m->x);
         a.x = m->h; a.cols = c.ffn; a.epilogue = kEpiResidual; a.resid = m->x;
         a.scale_t = 1;
         if ((rc = prep_lowrank(m, a))) return rc;
@@ -371,7 +390,8 @@ int issue_linear(gsdh_model* m, int l, int mask) {
 // The per-token launch sequence (run_gpu_native_chat.py:892-969, fused).
 int issue_token(gsdh_model* m, bool with_head) {
     const auto& c = m->c;
-    HIPCHK(launch_embed(m->embed, &m->st->token, m->x, c.hidden, m->stream));
+    m->pub_next = 0;
+    HIPCHK(launch_embed(m->embed, &m->st->token, m->x, c.hidden, m->pub, m->pub_words, m->stream));
     for (int l = 0; l < c.n_layers; l++) {
         int rc = issue_linear(m, l, 1);
         if (rc) return rc;
@@ -394,7 +414,7 @@ int issue_token(gsdh_model* m, bool with_head) {
     if (with_head) {
         HexArgs a{};
         a.nseg = 1;
-        fill_seg(a.seg[0], m->slot(0, GSDH_LM_HEAD), m->tables, m->logits);
+        fill_seg(a.seg[0], m->slot(0, GSDH_LM_HEAD), m, m->logits);
         a.x = m->x; a.norm_w = m->norm(-1, 0); a.eps = c.rms_eps; a.cols = c.hidden; a.epilogue = kEpiStore;
         a.scale_t = 1;
         int rc = prep_lowrank(m, a);
@@ -462,7 +482,8 @@ int gsdh_model_create(const gsdh_model_config* cfg, gsdh_model** out) {
     m->max_splits = (c.max_seq_len + m->chunk - 1) / m->chunk;
     A((void**)&m->ws, attention_ws_floats(c.n_kv_heads, m->max_splits, c.n_heads / c.n_kv_heads, c.head_dim) * 4);
     A((void**)&m->counters, (size_t)c.n_kv_heads * 4);
-    A((void**)&m->lrbuf, (size_t)(1 + kMaxRank * kMaxSeg) * 4);
+    m->pub_words = (4 * c.n_layers + 1) * kLeadMax;
+    A((void**)&m->pub, (size_t)m->pub_words * 8);
     A((void**)&m->st, sizeof(StepState));
     A((void**)&m->gen_tok, (size_t)c.max_seq_len * 4);
     A((void**)&m->gen_margin, (size_t)c.max_seq_len * 4);
@@ -473,6 +494,12 @@ int gsdh_model_create(const gsdh_model_config* cfg, gsdh_model** out) {
             e = hipMemcpy(m->tables[R], t.data(), t.size() * 4, hipMemcpyHostToDevice);
             if (e != hipSuccess) rc = fail((int)e, "hipMemcpy table: %s", hipGetErrorString(e));
         }
+        std::vector<uint32_t> f = host_fields(R);
+        A((void**)&m->fields[R], f.size() * 4);
+        if (!rc) {
+            e = hipMemcpy(m->fields[R], f.data(), f.size() * 4, hipMemcpyHostToDevice);
+            if (e != hipSuccess) rc = fail((int)e, "hipMemcpy fields: %s", hipGetErrorString(e));
+        }
     }
     if (!rc) {
         e = hipHostMalloc((void**)&m->st_host, sizeof(StepState) * 2, 0);
@@ -481,6 +508,7 @@ int gsdh_model_create(const gsdh_model_config* cfg, gsdh_model** out) {
     if (!rc) {
         // zero the KV cache and counters with kernels (no memset nodes anywhere)
         e = launch_fill_u32(m->counters, 0u, (size_t)c.n_kv_heads, m->stream);
+        if (e == hipSuccess) e = launch_fill_u32((unsigned*)m->pub, 0u, 2 * (size_t)m->pub_words, m->stream);
         if (e == hipSuccess) e = launch_fill_u32((unsigned*)m->kc, 0u, kvn / 2, m->stream);
         if (e == hipSuccess) e = launch_fill_u32((unsigned*)m->vc, 0u, kvn / 2, m->stream);
         if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
@@ -617,14 +645,15 @@ int gsdh_forward_token(gsdh_model* m, int token_id, int pos, int want_logits, fl
     if (token_id < 0 || token_id >= m->c.vocab) return fail(-1, "forward_token: token %d outside vocab %d", token_id, m->c.vocab);
     if (pos < 0 || pos >= m->c.max_seq_len) return fail(-1, "forward_token: pos %d outside 0..%d", pos, m->c.max_seq_len - 1);
     StepState* h = m->st_host;
-    h->token = token_id; h->pos = pos; h->gen_count = 0; h->pad = 0;
+    *h = StepState{};
+    h->token = token_id; h->pos = pos;
     HIPCHK(hipMemcpyAsync(m->st, h, sizeof(StepState), hipMemcpyHostToDevice, m->stream));
     HIPCHK(hipGraphLaunch(want_logits ? m->g_full : m->g_prefill, m->stream));
-    if (want_logits) {
-        if (logits_host) HIPCHK(hipMemcpyAsync(logits_host, m->logits, (size_t)m->c.vocab * 4, hipMemcpyDeviceToHost, m->stream));
-        HIPCHK(hipMemcpyAsync(m->st_host + 1, m->st, sizeof(StepState), hipMemcpyDeviceToHost, m->stream));
-    }
+    if (want_logits && logits_host)
+        HIPCHK(hipMemcpyAsync(logits_host, m->logits, (size_t)m->c.vocab * 4, hipMemcpyDeviceToHost, m->stream));
+    HIPCHK(hipMemcpyAsync(m->st_host + 1, m->st, sizeof(StepState), hipMemcpyDeviceToHost, m->stream));
     HIPCHK(hipStreamSynchronize(m->stream));
+    if (m->st_host[1].err) return fail(-2, "forward_token: a rank-k publication wait timed out");
     if (want_logits && argmax_out) *argmax_out = m->st_host[1].token;
     return 0;
 }
@@ -641,7 +670,8 @@ int gsdh_generate_greedy(gsdh_model* m, const int* prompt, int n_prompt, int sta
     HIPCHK(hipHostMalloc((void**)&ring, sizeof(StepState) * (size_t)n_prompt, 0));
     int rc = 0;
     for (int i = 0; i < n_prompt && !rc; i++) {
-        ring[i].token = prompt[i]; ring[i].pos = start_pos + i; ring[i].gen_count = 0; ring[i].pad = 0;
+        ring[i] = StepState{};
+        ring[i].token = prompt[i]; ring[i].pos = start_pos + i;
         hipError_t e = hipMemcpyAsync(m->st, &ring[i], sizeof(StepState), hipMemcpyHostToDevice, m->stream);
         if (e == hipSuccess) e = hipGraphLaunch(i == n_prompt - 1 ? m->g_full : m->g_prefill, m->stream);
         if (e != hipSuccess) rc = fail((int)e, "generate prefill: %s", hipGetErrorString(e));
@@ -653,8 +683,10 @@ int gsdh_generate_greedy(gsdh_model* m, const int* prompt, int n_prompt, int sta
     if (!rc) {
         hipError_t e = hipMemcpyAsync(tokens_out, m->gen_tok, (size_t)n_new * 4, hipMemcpyDeviceToHost, m->stream);
         if (e == hipSuccess && margins_out) e = hipMemcpyAsync(margins_out, m->gen_margin, (size_t)n_new * 4, hipMemcpyDeviceToHost, m->stream);
+        if (e == hipSuccess) e = hipMemcpyAsync(m->st_host + 1, m->st, sizeof(StepState), hipMemcpyDeviceToHost, m->stream);
         if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
         if (e != hipSuccess) rc = fail((int)e, "generate readback: %s", hipGetErrorString(e));
+        else if (m->st_host[1].err) rc = fail(-2, "generate: a rank-k publication wait timed out");
     }
     (void)hipStreamSynchronize(m->stream);
     (void)hipHostFree(ring);
@@ -663,6 +695,14 @@ int gsdh_generate_greedy(gsdh_model* m, const int* prompt, int n_prompt, int sta
 
 int gsdh_model_run_linear(gsdh_model* m, int layer, int mask) {
     if (layer < 0 || layer >= m->c.n_layers) return fail(-1, "run_linear: layer %d", layer);
+    // a sequence of its own: its publication words (if any) start at zero
+    static const int slots[4][2] = {{GSDH_Q, GSDH_V}, {GSDH_O, GSDH_O}, {GSDH_GATE, GSDH_UP}, {GSDH_DOWN, GSDH_DOWN}};
+    bool lowrank = false;
+    for (int i = 0; i < 4; i++)
+        if (mask & (1 << i))
+            for (int s = slots[i][0]; s <= slots[i][1]; s++) lowrank = lowrank || m->slot(layer, s).k > 0;
+    m->pub_next = 0;
+    if (lowrank) HIPCHK(launch_fill_u32((unsigned*)m->pub, 0u, 2 * (size_t)4 * kLeadMax, m->stream));
     return issue_linear(m, layer, mask);
 }
 

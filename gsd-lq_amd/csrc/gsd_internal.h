@@ -23,7 +23,11 @@ struct HexSeg {
     const uint16_t* Vt;        // k > 0 and tmp_k == null: computed in-kernel
     const float* S;
     const float* tmp_k;        // k > 0: precomputed low-rank projection, or null
-    const float* table;        // float2 [n_pts]
+    const float* table;        // float2 [n_pts]: codeword points (generic path)
+    // half2 [n_pts] integer fields (r0, r1) of the A2 codewords, whose points
+    // are (r0 + r1/2, r1*sqrt(3)/2); non-null in every segment selects the
+    // lattice path (requires scale_t = 1)
+    const uint32_t* fields;
     float* out;
     int rows, k, n_pts, batch0;
 };
@@ -57,25 +61,18 @@ struct HexArgs {
     int epilogue;
     int scale_t;           // scales layout: 0 = row-major [rows][cols/64] (file),
                            // 1 = [ceil(rows/4)][cols/64][4] (4 rows per 8-byte load)
-    const float* inv_dev;  // non-null with norm_w: RMSNorm factor computed by launch_lrprep
     RopeKV rope;           // kEpiRopeKV: interleaved RoPE of q/k rows, fp16 K/V append
+    // In-launch rank-k projection (segments with k > 0 and tmp_k == null):
+    // block b < sum(k) computes one tmp_k value and publishes it as one 64-bit
+    // word pub[b] = 1 << 32 | float bits (a single atomic store, so a reader
+    // sees 0 or the whole value, and no fence is needed).  Every block with
+    // rows to do polls the words before its first epilogue.  The words must
+    // be zero when the launch starts (each launch of a sequence has its own).
+    unsigned long long* pub;
+    unsigned* err;             // set to 1 when the wait exceeds its bound
 };
 
-// Low-rank / RMSNorm preparation for one fused matvec launch:
-// out[0] = 1/sqrtf(mean(x^2)+eps) (1 when norm_w is null),
-// out[1 + 16*g + j] = S_g[j] * sum_c x'[c] * Vt_g[j,c] with x' the (normed) input.
-struct LrPrep {
-    const float* x;
-    const float* norm_w;
-    float eps;
-    int cols;
-    int nseg;
-    const uint16_t* Vt[kMaxSeg];
-    const float* S[kMaxSeg];
-    int k[kMaxSeg];
-    float* out;
-};
-hipError_t launch_lrprep(const LrPrep& p, hipStream_t stream);
+constexpr int kLeadMax = kMaxSeg * kMaxRank;   // publishing blocks per launch
 
 // Launches (all asynchronous on `stream`).
 hipError_t launch_hexmv(const HexArgs& a, hipStream_t stream);
@@ -105,8 +102,10 @@ struct AttnArgs {
 hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
 size_t attention_ws_floats(int n_kv, int max_splits, int group, int hd);
 
+// embedding row of *token_dev to fp32 x; also zeroes clear[0..nclear) (the
+// rank-k publication words of the token's matvec launches)
 hipError_t launch_embed(const uint16_t* embed, const int* token_dev, float* x, int hidden,
-                        hipStream_t stream);
+                        unsigned long long* clear, int nclear, hipStream_t stream);
 
 // Greedy argmax with the reference's nan_to_num (gsd_lq_cpu_runtime.py:423);
 // writes token to *tok_out, margin top1-top2 to *margin_out and, when
@@ -116,7 +115,9 @@ struct StepState {
     int token;
     int pos;
     int gen_count;
-    int pad;
+    int margin_bits;    // top1 - top2 of the last argmax (float bits)
+    unsigned err;       // nonzero: a bounded in-kernel wait timed out
+    int pad[3];
 };
 hipError_t launch_argmax(const float* logits, int n, StepState* st, int* gen_tokens,
                          float* gen_margins, int advance, hipStream_t stream);

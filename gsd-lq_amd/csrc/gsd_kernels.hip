@@ -14,8 +14,9 @@
 //     16 pairs by the fp16 block scale;
 //   * RB rows are in flight per thread (RB independent 16-byte loads and FMA
 //     chains), reduced across the block with cross-lane shuffles + LDS;
-//   * prologue fusions: RMSNorm of the input and the rank-k projection
-//     tmp_k = S * (Vt x) are recomputed per block from the register slice;
+//   * prologue fusions: RMSNorm of the input (each block, from its register
+//     slice); the rank-k projection tmp_k = S * (Vt x) is computed once, by
+//     blocks 0..sum(k)-1, and published to the others through flags;
 //   * epilogue fusions: kinks and the U tmp_k term, then store / residual add /
 //     SwiGLU of paired gate-up rows.
 #include <cstdlib>
@@ -67,6 +68,29 @@ __device__ __forceinline__ float dot16(const uint4 c, const float2* __restrict__
     return p;
 }
 
+// Lattice form of dot16: with codeword (r0 + r1/2, r1*s), s = sqrt(3)/2, a pair
+// contributes xa*(r0 + r1/2) + xb*r1*s = u*r0 + v*r1 with u = xa and
+// v = xa/2 + s*xb precomputed per column pair (uv holds u, v interleaved).
+// The table entry is (r0, r1) as two fp16 (exact integers), so each pair is
+// one byte-select address (v_lshlrev_b32 SDWA), one 4-byte LDS read and two
+// mixed-precision FMAs (v_fma_mix_f32), all arithmetic in fp32.
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot16_lat(const uint4 c, const half2v* __restrict__ T, const float* uv) {
+    float p0 = 0.f, p1 = 0.f;   // r0 and r1 terms: two independent FMA chains
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const half2v t = T[(w[d] >> (8 * b)) & 0xFFu];
+            p0 = fmaf((float)t.x, uv[8 * d + 2 * b], p0);
+            p1 = fmaf((float)t.y, uv[8 * d + 2 * b + 1], p1);
+        }
+    }
+    return p0 + p1;
+}
+
 // Cross-lane reduction of 8 per-lane partial sums (one per row of a batch)
 // with VALU permutes only: two swap-and-add rounds (v_permlane32_swap,
 // v_permlane16_swap) halve the values per lane while doubling their span,
@@ -105,10 +129,82 @@ struct BatchRows {
     int g0, r0;
 };
 
-template <int SPT, int NWM, bool ST>
+// Rank-k value `lead` of a launch (segments in order, tmp_k == null ones only):
+// tmp_k[j] = S[j] * sum_c ((x[c] * inv) * w[c]) * Vt[j][c]
+// (gsd_lq_cpu_engine.c:66-82 then :110-127), published as one 64-bit word.
+// All loads of a thread (x, norm weights, Vt) are issued before any is used.
+template <int SPT>
+__device__ void lowrank_publish(const HexArgs& a, int lead, float* scratch) {
+    int g = 0, jj = lead;
+    for (; g < a.nseg; g++) {
+        const int k = a.seg[g].tmp_k ? 0 : a.seg[g].k;
+        if (jj < k) break;
+        jj -= k > 0 ? k : 0;
+    }
+    const HexSeg& sg = a.seg[g];
+    const int tid = threadIdx.x, NT = blockDim.x, S = a.cols >> 5;
+    float ss = 0.f, d = 0.f;
+    float4 xv[SPT][8], wv[SPT][8];
+    uint4 vv[SPT][4];
+#pragma unroll
+    for (int j = 0; j < SPT; j++) {
+        const int s = min(tid + j * NT, S - 1);
+        const float4* xp = reinterpret_cast<const float4*>(a.x + (size_t)s * 32);
+        const float4* wp = reinterpret_cast<const float4*>(a.norm_w ? a.norm_w + (size_t)s * 32 : a.x);
+        const uint4* vp = reinterpret_cast<const uint4*>(sg.Vt + (size_t)jj * a.cols + (size_t)s * 32);
+#pragma unroll
+        for (int q = 0; q < 8; q++) xv[j][q] = xp[q];
+        if (a.norm_w) {
+#pragma unroll
+            for (int q = 0; q < 8; q++) wv[j][q] = wp[q];
+        }
+#pragma unroll
+        for (int q = 0; q < 4; q++) vv[j][q] = vp[q];
+    }
+#pragma unroll
+    for (int j = 0; j < SPT; j++) {
+        if (tid + j * NT >= S) continue;
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            ss = fmaf(xv[j][q].x, xv[j][q].x, ss); ss = fmaf(xv[j][q].y, xv[j][q].y, ss);
+            ss = fmaf(xv[j][q].z, xv[j][q].z, ss); ss = fmaf(xv[j][q].w, xv[j][q].w, ss);
+        }
+    }
+    float inv = 1.f;
+    if (a.norm_w) {
+        ss = block_sum(ss, scratch);
+        inv = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
+    }
+#pragma unroll
+    for (int j = 0; j < SPT; j++) {
+        if (tid + j * NT >= S) continue;
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            float xe[4] = {xv[j][q].x, xv[j][q].y, xv[j][q].z, xv[j][q].w};
+            if (a.norm_w) {
+                const float we[4] = {wv[j][q].x, wv[j][q].y, wv[j][q].z, wv[j][q].w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) xe[e] = (xe[e] * inv) * we[e];
+            }
+            const uint32_t h0 = (&vv[j][q >> 1].x)[2 * (q & 1)], h1 = (&vv[j][q >> 1].x)[2 * (q & 1) + 1];
+            d = fmaf(xe[0], h2f((uint16_t)(h0 & 0xFFFFu)), d);
+            d = fmaf(xe[1], h2f((uint16_t)(h0 >> 16)), d);
+            d = fmaf(xe[2], h2f((uint16_t)(h1 & 0xFFFFu)), d);
+            d = fmaf(xe[3], h2f((uint16_t)(h1 >> 16)), d);
+        }
+    }
+    d = block_sum(d, scratch);
+    if (tid == 0)
+        __hip_atomic_store(&a.pub[lead], (1ull << 32) | __float_as_uint(d * sg.S[jj]), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// TM: 0 = generic float2 codeword tables (one per segment), 1 = lattice
+// fields, one table shared by all segments, 2 = lattice fields per segment.
+template <int SPT, int NWM, bool ST, int TM>
 __global__ void __launch_bounds__(NWM * 64) hexmv_kernel(const HexArgs a) {
     constexpr int RB = 8;
-    __shared__ float2 tbl[kMaxSeg][kTableSlots];
+    __shared__ float2 tbl[kMaxSeg][kTableSlots];   // TM > 0: half2 entries, 256 per segment
     __shared__ float red[2][NWM][RB];
     __shared__ float fin[RB];
     __shared__ float tkl[kMaxSeg][kMaxRank];
@@ -186,12 +282,33 @@ __global__ void __launch_bounds__(NWM * 64) hexmv_kernel(const HexArgs a) {
         }
     };
 
-    int b = blockIdx.x;
+    // blocks 0..nlead-1 compute the rank-k projections and exit; the matvec
+    // blocks follow them
+    int nlead = 0;
+    for (int g = 0; g < a.nseg; g++)
+        if (!a.seg[g].tmp_k) nlead += a.seg[g].k > 0 ? a.seg[g].k : 0;
+    if ((int)blockIdx.x < nlead) {
+        lowrank_publish<SPT>(a, (int)blockIdx.x, scratch);
+        return;
+    }
+    const int nblk = (int)gridDim.x - nlead;
+    int b = (int)blockIdx.x - nlead;
     if (b < a.nbatch) issue(b);   // in flight while the prologue runs
 
-    for (int g = 0; g < a.nseg; g++) {
-        const float2* tg = reinterpret_cast<const float2*>(a.seg[g].table);
-        for (int i = tid; i < kTableSlots; i += NT) tbl[g][i] = i < a.seg[g].n_pts ? tg[i] : make_float2(0.f, 0.f);
+    half2v* ltab = reinterpret_cast<half2v*>(&tbl[0][0]);
+    if (TM == 0) {
+        for (int g = 0; g < a.nseg; g++) {
+            const float2* tg = reinterpret_cast<const float2*>(a.seg[g].table);
+            for (int i = tid; i < kTableSlots; i += NT) tbl[g][i] = i < a.seg[g].n_pts ? tg[i] : make_float2(0.f, 0.f);
+        }
+    } else {
+        for (int g = 0; g < (TM == 1 ? 1 : a.nseg); g++) {
+            const half2v* fg = reinterpret_cast<const half2v*>(a.seg[g].fields);
+            for (int i = tid; i < kTableSlots; i += NT) {
+                half2v z; z.x = (_Float16)0.f; z.y = (_Float16)0.f;
+                ltab[g * kTableSlots + i] = i < a.seg[g].n_pts ? fg[i] : z;
+            }
+        }
     }
 
     // input slice: slot s = tid + j*NT covers columns [32s, 32s+32)
@@ -215,17 +332,13 @@ __global__ void __launch_bounds__(NWM * 64) hexmv_kernel(const HexArgs a) {
     // fused RMSNorm (gsd_lq_cpu_engine.c:66-82): x' = (x * inv) * w
     float inv = 1.f;
     if (a.norm_w) {
-        if (a.inv_dev) {
-            inv = *a.inv_dev;
-        } else {
-            float ss = 0.f;
+        float ss = 0.f;
 #pragma unroll
-            for (int j = 0; j < SPT; j++)
+        for (int j = 0; j < SPT; j++)
 #pragma unroll
-                for (int q = 0; q < 32; q++) ss = fmaf(xr[j][q], xr[j][q], ss);
-            ss = block_sum(ss, scratch);
-            inv = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
-        }
+            for (int q = 0; q < 32; q++) ss = fmaf(xr[j][q], xr[j][q], ss);
+        ss = block_sum(ss, scratch);
+        inv = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
 #pragma unroll
         for (int j = 0; j < SPT; j++) {
             const int s = tid + j * NT;
@@ -243,42 +356,29 @@ __global__ void __launch_bounds__(NWM * 64) hexmv_kernel(const HexArgs a) {
         }
     }
     if (tid == 0) s_inv = inv;
+    if (TM != 0) {
+        // lattice path: (xa, xb) -> (u, v) = (xa, xa/2 + xb*sqrt(3)/2)
+        constexpr float kS32 = 0.866025403784438646763723170752936183f;
+#pragma unroll
+        for (int j = 0; j < SPT; j++)
+#pragma unroll
+            for (int q = 0; q < 16; q++) xr[j][2 * q + 1] = fmaf(kS32, xr[j][2 * q + 1], 0.5f * xr[j][2 * q]);
+    }
 
-    // fused rank-k projection (gsd_lq_cpu_engine.c:110-127)
+    // rank-k values: given (tmp_k, copied here) or published by the
+    // projection blocks (fetched by each epilogue lane when it first needs a
+    // segment's values; bit g of `have` marks segment g as fetched)
+    unsigned have = 0;
     for (int g = 0; g < a.nseg; g++) {
-        const HexSeg& sg = a.seg[g];
-        if (sg.k <= 0) continue;
-        if (sg.tmp_k) {
-            if (tid < sg.k) tkl[g][tid] = sg.tmp_k[tid];
-            continue;
-        }
-        for (int jj = 0; jj < sg.k; jj++) {
-            float pp = 0.f;
-#pragma unroll
-            for (int j = 0; j < SPT; j++) {
-                const int s = tid + j * NT;
-                if (s < S) {
-                    const uint4* vp = reinterpret_cast<const uint4*>(sg.Vt + (size_t)jj * a.cols + (size_t)s * 32);
-#pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        const uint4 v = vp[q];
-                        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                        for (int e = 0; e < 4; e++) {
-                            pp = fmaf(xr[j][8 * q + 2 * e], h2f((uint16_t)(w[e] & 0xFFFFu)), pp);
-                            pp = fmaf(xr[j][8 * q + 2 * e + 1], h2f((uint16_t)(w[e] >> 16)), pp);
-                        }
-                    }
-                }
-            }
-            pp = block_sum(pp, scratch);
-            if (tid == 0) tkl[g][jj] = pp * sg.S[jj];
+        if (a.seg[g].k > 0 && a.seg[g].tmp_k) {
+            if (tid < a.seg[g].k) tkl[g][tid] = a.seg[g].tmp_k[tid];
+            have |= 1u << g;
         }
     }
     __syncthreads();
 
     int buf = 0;
-    for (; b < a.nbatch; b += gridDim.x) {
+    for (; b < a.nbatch; b += nblk) {
         const BatchRows br = rows_of(b);
         float acc[RB];
 #pragma unroll
@@ -289,13 +389,16 @@ __global__ void __launch_bounds__(NWM * 64) hexmv_kernel(const HexArgs a) {
 #pragma unroll
                 for (int rr = 0; rr < RB; rr++) {
                     const int g = paired ? (rr >> 2) : br.g0;
-                    acc[rr] = fmaf(dot16(cw[j][rr], tbl[g], xr[j]), h2f((uint16_t)sv[j][rr]), acc[rr]);
+                    float d;
+                    if (TM == 0) d = dot16(cw[j][rr], tbl[g], xr[j]);
+                    else d = dot16_lat(cw[j][rr], ltab + (TM == 1 ? 0 : g * kTableSlots), xr[j]);
+                    acc[rr] = fmaf(d, h2f((uint16_t)sv[j][rr]), acc[rr]);
                 }
             }
         }
         const uint4 uw_cur[2] = {uw[0], uw[1]};
         // next batch's loads fly during the reduction and the epilogue
-        if (b + (int)gridDim.x < a.nbatch) issue(b + gridDim.x);
+        if (b + nblk < a.nbatch) issue(b + nblk);
 
         float u0, u1;
         reduce8(acc, u0, u1);
@@ -319,6 +422,25 @@ __global__ void __launch_bounds__(NWM * 64) hexmv_kernel(const HexArgs a) {
                         const float xc = a.norm_w ? (a.x[c] * s_inv) * a.norm_w[c] : a.x[c];
                         t += sg.kdel[i] * xc;
                     }
+                }
+                if (sg.k > 0 && !((have >> g) & 1u)) {
+                    // this segment's published words (segments without tmp_k
+                    // in order); a bounded wait, normally already satisfied:
+                    // after 2^20 polls the error word is set
+                    int off = 0;
+                    for (int g2 = 0; g2 < g; g2++)
+                        if (!a.seg[g2].tmp_k && a.seg[g2].k > 0) off += a.seg[g2].k;
+                    int spins = 0;
+                    for (int jj = 0; jj < sg.k; jj++) {
+                        unsigned long long w;
+                        while (((w = __hip_atomic_load(&a.pub[off + jj], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) >> 32) == 0 &&
+                               spins < (1 << 20)) {
+                            if (++spins == (1 << 20)) *a.err = 1u;
+                            __builtin_amdgcn_s_sleep(1);
+                        }
+                        tkl[g][jj] = __uint_as_float((unsigned)w);
+                    }
+                    have |= 1u << g;
                 }
                 const uint32_t uu[8] = {uw_cur[0].x, uw_cur[0].y, uw_cur[0].z, uw_cur[0].w,
                                         uw_cur[1].x, uw_cur[1].y, uw_cur[1].z, uw_cur[1].w};
@@ -374,7 +496,7 @@ __global__ void __launch_bounds__(NWM * 64) hexmv_kernel(const HexArgs a) {
     }
 }
 
-template <int SPT, int NWM, bool ST>
+template <int SPT, int NWM, bool ST, int TM>
 hipError_t launch_hexmv_t(const HexArgs& a, hipStream_t st, int nt) {
     constexpr int RB = 8;
     HexArgs b = a;
@@ -393,7 +515,7 @@ hipError_t launch_hexmv_t(const HexArgs& a, hipStream_t st, int nt) {
     static int per_cu = 0;
     if (per_cu == 0) {
         int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, hexmv_kernel<SPT, NWM, ST>, nt, 0) != hipSuccess || n < 1)
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, hexmv_kernel<SPT, NWM, ST, TM>, nt, 0) != hipSuccess || n < 1)
             n = 1;
         per_cu = n;
     }
@@ -402,9 +524,17 @@ hipError_t launch_hexmv_t(const HexArgs& a, hipStream_t st, int nt) {
     // launches one block per batch instead
     static const int persist = getenv("GSD_HEXMV_PERSIST") ? atoi(getenv("GSD_HEXMV_PERSIST")) : 1;
     const int ncu = device_cu_count() > 0 ? device_cu_count() : 256;
+    // blocks 0..nlead-1 publish the rank-k values and exit after one short
+    // pass; the matvec blocks follow them (dispatched in order, so a matvec
+    // block never waits on a publishing block that is not yet resident)
+    int nlead = 0;
+    for (int g = 0; g < b.nseg; g++)
+        if (!b.seg[g].tmp_k && b.seg[g].k > 0) nlead += b.seg[g].k;
+    if (nlead > 0 && (!b.pub || !b.err)) return hipErrorInvalidValue;
     int grid = persist ? ncu * per_cu : b.nbatch;
     if (grid > b.nbatch) grid = b.nbatch;
-    hipLaunchKernelGGL((hexmv_kernel<SPT, NWM, ST>), dim3(grid), dim3(nt), 0, st, b);
+    grid += nlead;
+    hipLaunchKernelGGL((hexmv_kernel<SPT, NWM, ST, TM>), dim3(grid), dim3(nt), 0, st, b);
     return hipGetLastError();
 }
 
@@ -691,58 +821,11 @@ __global__ void attn_merge_kernel(const AttnArgs a) {
     a.out[(size_t)h * HD + d] = O / L;
 }
 
-// One block per (segment, j): RMSNorm factor and tmp_k of one launch.  Each
-// thread owns up to 64 columns; all of its loads are issued before any use.
-__global__ void __launch_bounds__(256) lrprep_kernel(const LrPrep p) {
-    __shared__ float scratch[16];
-    const int g = blockIdx.x / kMaxRank, j = blockIdx.x % kMaxRank;
-    if (g >= p.nseg || j >= (p.k[g] > 0 ? p.k[g] : (g == 0 && j == 0 ? 1 : 0))) return;
-    constexpr int Q = 16;   // float4 groups per thread: 256 * 16 * 4 = 16384 columns per pass
-    const bool lr = p.k[g] > 0;
-    const uint16_t* vt = lr ? p.Vt[g] + (size_t)j * p.cols : nullptr;
-    float ss = 0.f, d = 0.f;
-    for (int c0 = 0; c0 < p.cols; c0 += 256 * Q * 4) {
-        float4 xv[Q], wv[Q];
-        uint2 hv[Q];
-#pragma unroll
-        for (int q = 0; q < Q; q++) {
-            const int c = c0 + (q * 256 + (int)threadIdx.x) * 4;
-            const bool in = c < p.cols;
-            xv[q] = in ? *reinterpret_cast<const float4*>(p.x + c) : make_float4(0.f, 0.f, 0.f, 0.f);
-            wv[q] = (in && p.norm_w) ? *reinterpret_cast<const float4*>(p.norm_w + c) : make_float4(1.f, 1.f, 1.f, 1.f);
-            hv[q] = (in && lr) ? *reinterpret_cast<const uint2*>(vt + c) : make_uint2(0u, 0u);
-        }
-#pragma unroll
-        for (int q = 0; q < Q; q++) {
-            ss = fmaf(xv[q].x, xv[q].x, ss); ss = fmaf(xv[q].y, xv[q].y, ss);
-            ss = fmaf(xv[q].z, xv[q].z, ss); ss = fmaf(xv[q].w, xv[q].w, ss);
-        }
-        if (lr) {
-            // held until the norm factor is known: x' = (x * inv) * w
-            // (accumulated as x * w * Vt, times inv afterwards)
-#pragma unroll
-            for (int q = 0; q < Q; q++) {
-                d = fmaf(xv[q].x * wv[q].x, h2f((uint16_t)(hv[q].x & 0xFFFFu)), d);
-                d = fmaf(xv[q].y * wv[q].y, h2f((uint16_t)(hv[q].x >> 16)), d);
-                d = fmaf(xv[q].z * wv[q].z, h2f((uint16_t)(hv[q].y & 0xFFFFu)), d);
-                d = fmaf(xv[q].w * wv[q].w, h2f((uint16_t)(hv[q].y >> 16)), d);
-            }
-        }
-    }
-    float inv = 1.f;
-    if (p.norm_w) {
-        ss = block_sum(ss, scratch);
-        inv = 1.0f / sqrtf(ss / (float)p.cols + p.eps);
-    }
-    if (g == 0 && j == 0 && threadIdx.x == 0) p.out[0] = inv;
-    if (!lr) return;
-    d = block_sum(d, scratch);
-    if (threadIdx.x == 0) p.out[1 + kMaxRank * g + j] = (d * inv) * p.S[g][j];
-}
-
-__global__ void embed_kernel(const uint16_t* embed, const int* token, float* x, int hidden) {
+__global__ void embed_kernel(const uint16_t* embed, const int* token, float* x, int hidden,
+                             unsigned long long* clear, int nclear) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < hidden) x[i] = h2f(embed[(size_t)(*token) * hidden + i]);
+    if (i < nclear) clear[i] = 0ull;
 }
 
 // greedy argmax: nan -> -1e4, +inf -> 100, -inf -> -1e4, first index wins
@@ -806,7 +889,7 @@ __global__ void __launch_bounds__(1024) argmax_kernel(const float* logits, int n
             st->gen_count = c + 1;
         }
         if (advance) st->pos = st->pos + 1;
-        st->pad = __float_as_int(margin);
+        st->margin_bits = __float_as_int(margin);
     }
 }
 
@@ -845,29 +928,36 @@ __global__ void unpack_kernel(const uint8_t* codes, int64_t n, int R, int32_t* i
 // ------------------------------------------------------------------------
 hipError_t launch_hexmv(const HexArgs& a, hipStream_t st) {
     const int S = a.cols >> 5;
-    // slots per thread: 1 (measured fastest: fewer VGPRs, more waves per CU);
-    // GSD_HEXMV_SPT=2 halves the threads per row for experiments
-    static const int force_spt = getenv("GSD_HEXMV_SPT") ? atoi(getenv("GSD_HEXMV_SPT")) : 0;
-    int spt = 1;
-    if (force_spt == 2 && S % 128 == 0) spt = 2;
+    // one 32-column slot per thread (fewest VGPRs, most waves per CU); two
+    // when the row has more than 1024 slots
+    const int spt = S <= 1024 ? 1 : 2;
     const int nt = ((S + spt - 1) / spt + 63) / 64 * 64;
     if (nt > 1024) return hipErrorInvalidValue;
-    const bool st_layout = a.scale_t != 0;
-#define GSD_HEXMV_DISPATCH(ST)                                                      \
+    bool lattice = a.nseg > 0, shared = true;
+    for (int g = 0; g < a.nseg; g++) {
+        lattice = lattice && a.seg[g].fields != nullptr;
+        shared = shared && a.seg[g].fields == a.seg[0].fields && a.seg[g].n_pts == a.seg[0].n_pts;
+    }
+    // lattice fields come with the 4-row scale groups; the generic path
+    // reads the file's row-major scales
+    if (lattice != (a.scale_t != 0)) return hipErrorInvalidValue;
+#define GSD_HEXMV_DISPATCH(ST, TM)                                                  \
     if (spt == 2) {                                                                 \
-        if (nt <= 64) return launch_hexmv_t<2, 1, ST>(a, st, nt);                    \
-        if (nt <= 256) return launch_hexmv_t<2, 4, ST>(a, st, nt);                   \
-        if (nt <= 512) return launch_hexmv_t<2, 8, ST>(a, st, nt);                   \
-        return launch_hexmv_t<2, 16, ST>(a, st, nt);                                 \
+        if (nt <= 64) return launch_hexmv_t<2, 1, ST, TM>(a, st, nt);                \
+        if (nt <= 256) return launch_hexmv_t<2, 4, ST, TM>(a, st, nt);               \
+        if (nt <= 512) return launch_hexmv_t<2, 8, ST, TM>(a, st, nt);               \
+        return launch_hexmv_t<2, 16, ST, TM>(a, st, nt);                             \
     }                                                                               \
-    if (nt <= 64) return launch_hexmv_t<1, 1, ST>(a, st, nt);                        \
-    if (nt <= 256) return launch_hexmv_t<1, 4, ST>(a, st, nt);                       \
-    if (nt <= 512) return launch_hexmv_t<1, 8, ST>(a, st, nt);                       \
-    return launch_hexmv_t<1, 16, ST>(a, st, nt);
-    if (st_layout) {
-        GSD_HEXMV_DISPATCH(true)
+    if (nt <= 64) return launch_hexmv_t<1, 1, ST, TM>(a, st, nt);                    \
+    if (nt <= 256) return launch_hexmv_t<1, 4, ST, TM>(a, st, nt);                   \
+    if (nt <= 512) return launch_hexmv_t<1, 8, ST, TM>(a, st, nt);                   \
+    return launch_hexmv_t<1, 16, ST, TM>(a, st, nt);
+    if (!lattice) {
+        GSD_HEXMV_DISPATCH(false, 0)
+    } else if (shared) {
+        GSD_HEXMV_DISPATCH(true, 1)
     } else {
-        GSD_HEXMV_DISPATCH(false)
+        GSD_HEXMV_DISPATCH(true, 2)
     }
 #undef GSD_HEXMV_DISPATCH
 }
@@ -938,14 +1028,11 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
-hipError_t launch_lrprep(const LrPrep& p, hipStream_t st) {
-    if (p.cols % 4) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(lrprep_kernel, dim3(p.nseg * kMaxRank), dim3(256), 0, st, p);
-    return hipGetLastError();
-}
-
-hipError_t launch_embed(const uint16_t* embed, const int* token_dev, float* x, int hidden, hipStream_t st) {
-    hipLaunchKernelGGL(embed_kernel, dim3((hidden + 255) / 256), dim3(256), 0, st, embed, token_dev, x, hidden);
+hipError_t launch_embed(const uint16_t* embed, const int* token_dev, float* x, int hidden,
+                        unsigned long long* clear, int nclear, hipStream_t st) {
+    const int n = hidden > nclear ? hidden : nclear;
+    hipLaunchKernelGGL(embed_kernel, dim3((n + 255) / 256), dim3(256), 0, st, embed, token_dev, x, hidden, clear,
+                       nclear);
     return hipGetLastError();
 }
 
