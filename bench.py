@@ -139,7 +139,7 @@ def bench_linear(bank, steps, warmup):
     gu_bytes = sum(alg_bytes(bank.packed[(l, t)]) for l in range(L) for t in ("ffn_gate", "ffn_up")) / L
     gu_bytes -= 4 * H   # gate and up read the same x once
     ach = gu_bytes / (per_launch_ms * 1e-3) / 1e9
-    roof = {"kernel": "hexmv_kernel (fused RMSNorm + gate/up matvec + SwiGLU, 2x14336x4096)",
+    roof = {"kernel": "hexmv4_kernel (MFMA fused RMSNorm + gate/up matvec + SwiGLU, 2x14336x4096)",
             "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(),
             "launch_us": round(per_launch_ms * 1e3, 2), "alg_bytes_per_launch": int(gu_bytes)}

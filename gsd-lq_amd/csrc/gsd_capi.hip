@@ -259,8 +259,8 @@ int gsdh_unpack_codes(void* stream, const uint8_t* codes, int64_t n, int radius,
 struct HexDev {
     int set = 0, radius = 0, rows = 0, cols = 0, k = 0;
     int64_t nk = 0;
-    uint8_t* codes = nullptr;
-    uint16_t* scales = nullptr;
+    uint4* codes_t = nullptr;      // tiled layout (HexSeg::codes_t)
+    uint32_t* scales_t = nullptr;  // tiled layout (HexSeg::scales_t)
     uint32_t* row_ptr = nullptr;
     uint16_t* kcols = nullptr;
     float* kdel = nullptr;
@@ -314,7 +314,7 @@ int dalloc(gsdh_model* m, void** p, size_t n) {
 }
 
 void fill_seg(HexSeg& s, const HexDev& t, const gsdh_model* m, float* out) {
-    s.codes = t.codes; s.scales = t.scales; s.row_ptr = t.nk ? t.row_ptr : nullptr;
+    s.codes_t = t.codes_t; s.scales_t = t.scales_t; s.row_ptr = t.nk ? t.row_ptr : nullptr;
     s.kcols = t.kcols; s.kdel = t.kdel; s.U = t.U; s.Vt = t.Vt; s.S = t.Sv; s.tmp_k = nullptr;
     s.table = m->tables[t.radius]; s.fields = m->fields[t.radius]; s.out = out; s.rows = t.rows; s.k = t.k;
     s.n_pts = 3 * t.radius * t.radius + 3 * t.radius + 1;
@@ -354,7 +354,7 @@ int issue_linear(gsdh_model* m, int l, int mask) {
             r.interleaved = 1;
         }
         if ((rc = prep_lowrank(m, a))) return rc;
-        HIPCHK(launch_hexmv(a, m->stream));
+        HIPCHK(launch_hexmv4(a, m->stream));
     }
     if (mask & 2) {   // o projection + residual
         HexArgs a{};
@@ -363,7 +363,7 @@ int issue_linear(gsdh_model* m, int l, int mask) {
         a.x = m->attn; a.cols = c.n_heads * c.head_dim; a.epilogue = kEpiResidual; a.resid = m->x;
         a.scale_t = 1;
         if ((rc = prep_lowrank(m, a))) return rc;
-        HIPCHK(launch_hexmv(a, m->stream));
+        HIPCHK(launch_hexmv4(a, m->stream));
     }
     if (mask & 4) {   // gate + up with fused FFN RMSNorm and SwiGLU
         HexArgs a{};
@@ -373,7 +373,7 @@ int issue_linear(gsdh_model* m, int l, int mask) {
         a.x = m->x; a.norm_w = m->norm(l, 1); a.eps = c.rms_eps; a.cols = c.hidden; a.epilogue = kEpiSwiGLU;
         a.scale_t = 1;
         if ((rc = prep_lowrank(m, a))) return rc;
-        HIPCHK(launch_hexmv(a, m->stream));
+        HIPCHK(launch_hexmv4(a, m->stream));
     }
     if (mask & 8) {   // down projection + residual
         HexArgs a{};
@@ -382,7 +382,7 @@ int issue_linear(gsdh_model* m, int l, int mask) {
         a.x = m->h; a.cols = c.ffn; a.epilogue = kEpiResidual; a.resid = m->x;
         a.scale_t = 1;
         if ((rc = prep_lowrank(m, a))) return rc;
-        HIPCHK(launch_hexmv(a, m->stream));
+        HIPCHK(launch_hexmv4(a, m->stream));
     }
     return 0;
 }
@@ -419,7 +419,7 @@ int issue_token(gsdh_model* m, bool with_head) {
         a.scale_t = 1;
         int rc = prep_lowrank(m, a);
         if (rc) return rc;
-        HIPCHK(launch_hexmv(a, m->stream));
+        HIPCHK(launch_hexmv4(a, m->stream));
         HIPCHK(launch_argmax(m->logits, c.vocab, m->st, m->gen_tok, m->gen_margin, 1, m->stream));
     }
     return 0;
@@ -495,6 +495,7 @@ int gsdh_model_create(const gsdh_model_config* cfg, gsdh_model** out) {
             if (e != hipSuccess) rc = fail((int)e, "hipMemcpy table: %s", hipGetErrorString(e));
         }
         std::vector<uint32_t> f = host_fields(R);
+        f.resize(kTableSlots, 0u);   // padded: the matvec reads 16-entry slices
         A((void**)&m->fields[R], f.size() * 4);
         if (!rc) {
             e = hipMemcpy(m->fields[R], f.data(), f.size() * 4, hipMemcpyHostToDevice);
@@ -591,10 +592,13 @@ int gsdh_model_set_hex(gsdh_model* m, int layer, int slot, int radius, int rows,
     HexDev& t = m->slot(layer, slot);
     if (t.block) { (void)hipFree(t.block); m->dev_bytes -= t.bytes; t = HexDev(); }
     auto al = [](size_t n) { return (n + 255) / 256 * 256; };
-    // scales are stored in groups of 4 rows: [ceil(rows/4)][cols/64][4] fp16,
-    // so one 8-byte load gives a lane the scales of 4 rows of its block
-    const size_t nsb = (size_t)cols / 64, ngrp = ((size_t)rows + 3) / 4;
-    const size_t o_codes = 0, o_sc = o_codes + al(ncodes), o_rp = o_sc + al(ngrp * nsb * 4 * 2);
+    // tiled layout of the MFMA matvec: codes [nrb][nc][64 lanes][16 B] with
+    // lane l = row 16rb + (l & 15), bytes j = pairs 64c + 8(l >> 4) + j (j < 8)
+    // and 64c + 32 + 8(l >> 4) + j - 8 (j >= 8); scales [nrb][nc][16] as the
+    // fp16 pair of the chunk's two 64-weight blocks.  Padding: code 0, scale 0.
+    const size_t nrb = ((size_t)rows + 15) / 16, nc = ((size_t)cols + 127) / 128, nsb = (size_t)cols / 64;
+    const size_t half = (size_t)cols / 2;
+    const size_t o_codes = 0, o_sc = o_codes + al(nrb * nc * 1024), o_rp = o_sc + al(nrb * nc * 64);
     const size_t o_kc = o_rp + al((size_t)(rows + 1) * 4), o_kd = o_kc + al((size_t)nk * 2);
     const size_t o_u = o_kd + al((size_t)nk * 4), o_s = o_u + al((size_t)rows * k_dim * 2);
     const size_t o_vt = o_s + al((size_t)k_dim * 4), total = o_vt + al((size_t)k_dim * cols * 2);
@@ -602,15 +606,34 @@ int gsdh_model_set_hex(gsdh_model* m, int layer, int slot, int radius, int rows,
     HIPCHK(hipMalloc(&blk, total));
     char* b = static_cast<char*>(blk);
     t.block = blk; t.bytes = total; m->dev_bytes += total;
-    t.codes = (uint8_t*)(b + o_codes); t.scales = (uint16_t*)(b + o_sc); t.row_ptr = (uint32_t*)(b + o_rp);
+    t.codes_t = (uint4*)(b + o_codes); t.scales_t = (uint32_t*)(b + o_sc); t.row_ptr = (uint32_t*)(b + o_rp);
     t.kcols = (uint16_t*)(b + o_kc); t.kdel = (float*)(b + o_kd); t.U = (uint16_t*)(b + o_u);
     t.Sv = (float*)(b + o_s); t.Vt = (uint16_t*)(b + o_vt);
-    HIPCHK(hipMemcpy(t.codes, codes, ncodes, hipMemcpyHostToDevice));
     {
-        std::vector<uint16_t> st(ngrp * nsb * 4, 0);
-        for (size_t r = 0; r < (size_t)rows; r++)
-            for (size_t b = 0; b < nsb; b++) st[((r / 4) * nsb + b) * 4 + (r % 4)] = scales[r * nsb + b];
-        HIPCHK(hipMemcpy(t.scales, st.data(), st.size() * 2, hipMemcpyHostToDevice));
+        std::vector<uint8_t> ct(nrb * nc * 1024, 0);
+        std::vector<uint32_t> stl(nrb * nc * 16, 0);
+        for (size_t rb = 0; rb < nrb; rb++)
+            for (size_t c = 0; c < nc; c++) {
+                uint8_t* dst = ct.data() + (rb * nc + c) * 1024;
+                for (int l = 0; l < 64; l++) {
+                    const size_t row = rb * 16 + (size_t)(l & 15);
+                    if (row >= (size_t)rows) continue;
+                    const uint8_t* src = codes + row * half;
+                    for (int j = 0; j < 16; j++) {
+                        const size_t p = 64 * c + (j < 8 ? 8 * (size_t)(l >> 4) + j : 32 + 8 * (size_t)(l >> 4) + (j - 8));
+                        if (p < half) dst[l * 16 + j] = src[p];
+                    }
+                }
+                for (int n = 0; n < 16; n++) {
+                    const size_t row = rb * 16 + (size_t)n;
+                    if (row >= (size_t)rows) continue;
+                    const uint32_t s0 = scales[row * nsb + 2 * c];
+                    const uint32_t s1 = 2 * c + 1 < nsb ? scales[row * nsb + 2 * c + 1] : 0u;
+                    stl[(rb * nc + c) * 16 + n] = s0 | (s1 << 16);
+                }
+            }
+        HIPCHK(hipMemcpy(t.codes_t, ct.data(), ct.size(), hipMemcpyHostToDevice));
+        HIPCHK(hipMemcpy(t.scales_t, stl.data(), stl.size() * 4, hipMemcpyHostToDevice));
     }
     HIPCHK(hipMemcpy(t.row_ptr, row_ptr, (size_t)(rows + 1) * 4, hipMemcpyHostToDevice));
     if (nk > 0) {

@@ -28,6 +28,15 @@ struct HexSeg {
     // are (r0 + r1/2, r1*sqrt(3)/2); non-null in every segment selects the
     // lattice path (requires scale_t = 1)
     const uint32_t* fields;
+    // tiled device layout of the MFMA path (hexmv4):
+    //   codes_t  [ceil(rows/16)][ceil(cols/128)][64 lanes][16 B]
+    //   scales_t [ceil(rows/16)][ceil(cols/128)][16 rows] fp16 pairs
+    // lane l holds row 16*rb + (l & 15); its byte j is pair 64c + 8(l >> 4) + j
+    // (j < 8) or 64c + 32 + 8(l >> 4) + j - 8 (j >= 8) of that row; the scale
+    // pair holds the two 64-weight blocks of the chunk.  Padding is code 0 /
+    // scale 0.
+    const uint4* codes_t;
+    const uint32_t* scales_t;
     float* out;
     int rows, k, n_pts, batch0;
 };
@@ -76,6 +85,9 @@ constexpr int kLeadMax = kMaxSeg * kMaxRank;   // publishing blocks per launch
 
 // Launches (all asynchronous on `stream`).
 hipError_t launch_hexmv(const HexArgs& a, hipStream_t stream);
+// MFMA matvec over the tiled layout (codes_t / scales_t / fields of every
+// segment); same epilogues, norm and rank-k handling as launch_hexmv.
+hipError_t launch_hexmv4(const HexArgs& a, hipStream_t stream);
 hipError_t launch_lowrank(const float* x, const uint16_t* Vt, const float* S, float* tmp_k,
                           int k, int cols, hipStream_t stream);
 hipError_t launch_rmsnorm(const float* x, const float* w, float* out, int dim, float eps,

@@ -921,6 +921,441 @@ __global__ void unpack_kernel(const uint8_t* codes, int64_t n, int R, int32_t* i
     r01[2 * i + 1] = (int8_t)(lo + rem);
 }
 
+// ------------------------------------------------------------------------
+// hexmv4: the fused unpack + dequant matvec on the matrix cores.
+//
+// Per 64-weight block the reference computes scale * sum_p xy[code_p] . x_p
+// (gsd_lq_cpu_engine.c:129-183).  In lattice form a pair contributes
+// u*r0 + v*r1 with (u, v) = (xa, xa/2 + xb*sqrt(3)/2) and (r0, r1) the
+// codeword's integer fields, which fp16 holds exactly.  One
+// v_mfma_f32_16x16x32_f16 then evaluates 16 rows x 16 pairs:
+//   B[k][n] = fields of row n (lane n & 15, 4 pairs per lane from the 16-byte
+//             code word of the tiled layout, one LDS lookup each),
+//   A[m][k] = x side: row m = 0 the fp16 high part of (u, v) * 2^e, row 1 the
+//             fp16 low part (x = hi + lo to 2^-22); rows 2..15 repeat them
+//             and feed only rows of D that are never read,
+//   D[m][n] lands in lane n: element 0 + element 1 = the 16-pair dot product
+//             (fp16 x fp16 products are exact, accumulation fp32).
+// The per-row fp16 scale is applied after each 32-pair block.  VALU work per
+// pair is one v_perm_b32 (LDS address of the lane's own copy of the codebook:
+// code << 8 | lane * 4, so the 64 lanes never share a bank).
+//
+// Work split: a block of W waves takes row-blocks (16 rows) in turn; its waves
+// split the 128-column chunks of a row-block (double-buffered 16-byte code
+// loads, one chunk in flight while the other is computed) and reduce through
+// LDS; wave 0's lanes 0-15 run the epilogue.  For the paired gate/up launch
+// the waves form two groups (gate row-block, up row-block of the same rows).
+// ------------------------------------------------------------------------
+typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+constexpr int kMv4MaxWaves = 16;
+
+// x'[c] of the launch (RMSNorm applied when norm_w is set), as the reference
+// forms it: (x * inv) * w.
+__device__ __forceinline__ float xnorm(const HexArgs& a, int c, float inv) {
+    return a.norm_w ? (a.x[c] * inv) * a.norm_w[c] : a.x[c];
+}
+
+// Rank-k value `lead` of a launch (segments without tmp_k, in order):
+// S[j] * sum_c x'[c] * Vt[j][c] (gsd_lq_cpu_engine.c:110-127), published as
+// one 64-bit word 1 << 32 | float bits.
+__device__ void mv4_publish(const HexArgs& a, int lead, float* scratch) {
+    int g = 0, jj = lead;
+    for (; g < a.nseg; g++) {
+        const int k = a.seg[g].tmp_k ? 0 : a.seg[g].k;
+        if (jj < k) break;
+        jj -= k > 0 ? k : 0;
+    }
+    const HexSeg& sg = a.seg[g];
+    float inv = 1.f;
+    if (a.norm_w) {
+        float ss = 0.f;
+        for (int c = threadIdx.x; c < a.cols; c += blockDim.x) ss = fmaf(a.x[c], a.x[c], ss);
+        ss = block_sum(ss, scratch);
+        inv = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
+    }
+    float d = 0.f;
+    const uint16_t* vt = sg.Vt + (size_t)jj * a.cols;
+    for (int c = threadIdx.x; c < a.cols; c += blockDim.x) d = fmaf(xnorm(a, c, inv), h2f(vt[c]), d);
+    d = block_sum(d, scratch);
+    if (threadIdx.x == 0)
+        __hip_atomic_store(&a.pub[lead], (1ull << 32) | __float_as_uint(d * sg.S[jj]), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Workgroup barrier for LDS traffic only.  __syncthreads() is a workgroup
+// fence plus s_barrier, and on this target the fence waits for every
+// outstanding vector memory operation of the wave (vmcnt(0)), which would
+// drain the prefetched code loads at each barrier.  Here each wave waits for
+// its own LDS operations (lgkmcnt(0); vmcnt and expcnt left at their maxima:
+// 0xC07F) and then meets the others; the empty asm statements keep the
+// compiler from moving memory accesses across.
+__device__ __forceinline__ void lds_barrier() {
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+}
+
+// TB > 0: every segment uses the same codebook of TB points, held at a
+// static LDS address; TB == 0: per-segment codebooks in dynamic LDS.
+template <int TB>
+__global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(8))) hexmv4_kernel(const HexArgs a) {
+    __shared__ __attribute__((aligned(16))) uint32_t stab[TB > 0 ? TB * 64 : 1];
+    __shared__ float red[2][kMv4MaxWaves][16];
+    __shared__ float tkl[kMaxSeg][kMaxRank];
+    __shared__ float scratch[32];
+    extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
+
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, NW = (int)(blockDim.x >> 6);
+    const int nc = (a.cols + 127) >> 7;
+    const bool paired = a.epilogue == kEpiSwiGLU;
+    const int G = paired ? 2 : 1, WR = NW / G, grp = wid / WR, wr = wid - grp * WR;
+
+    // rank-k publishing blocks first
+    int nlead = 0;
+    for (int g = 0; g < a.nseg; g++)
+        if (!a.seg[g].tmp_k && a.seg[g].k > 0) nlead += a.seg[g].k;
+    if ((int)blockIdx.x < nlead) {
+        mv4_publish(a, (int)blockIdx.x, scratch);
+        return;
+    }
+    const int nblk = (int)gridDim.x - nlead;
+
+    // units: paired -> row-block rb of gate and up; else the row-blocks of
+    // the segments in order
+    // unit boundaries of the segments (scalars: no indexed private arrays)
+    const int nrb0 = (a.seg[0].rows + 15) >> 4;
+    const int ub1 = nrb0, ub2 = ub1 + (a.nseg > 1 ? (a.seg[1].rows + 15) >> 4 : 0);
+    const int ub3 = ub2 + (a.nseg > 2 ? (a.seg[2].rows + 15) >> 4 : 0);
+    const int nunits = paired ? nrb0 : ub3;
+    auto seg_of = [&](int u) {   // segment of a unit for this wave
+        if (paired) return grp;
+        return u >= ub2 ? 2 : (u >= ub1 ? 1 : 0);
+    };
+    auto ubase = [&](int g) { return g == 0 ? 0 : (g == 1 ? ub1 : ub2); };
+    const int toff1 = TB == 0 ? a.seg[0].n_pts * 256 : 0;
+    const int toff2 = TB == 0 && a.nseg > 1 ? toff1 + a.seg[1].n_pts * 256 : toff1;
+    const int tab_bytes = TB == 0 && a.nseg > 2 ? toff2 + a.seg[2].n_pts * 256 : toff2;
+    auto toff = [&](int g) { return g == 0 ? 0 : (g == 1 ? toff1 : toff2); };
+    uint4* X = reinterpret_cast<uint4*>(dyn + tab_bytes);
+
+    // this wave's steps: P chunks (wr, wr + WR, ...) of each of the block's
+    // units in turn (units u0, u0 + nblk, ...); P is the same for every wave
+    // (WR divides nc), so unit ends, and their barriers, fall on the same step
+    // in all waves.  The load cursor runs two steps ahead of the compute
+    // cursor; both advance by compare-and-reset, and per-unit base pointers
+    // are recomputed only when a unit starts.  Past the last unit the load
+    // cursor stays on the last unit (valid addresses, unused data).
+    const int P = nc / WR;   // >= 1
+    const int u0 = (int)blockIdx.x - nlead;
+    const int my_units = u0 < nunits ? (nunits - 1 - u0) / nblk + 1 : 0;
+    const int nsteps = P * my_units;
+    int lk = 0, lj = 0;
+    const uint4* lcb = nullptr;
+    const uint32_t* lsb = nullptr;
+    auto lset = [&](int k) {
+        const int uu = min(u0 + k * nblk, nunits - 1);
+        const int g = seg_of(uu);
+        const int rb = paired ? uu : uu - ubase(g);
+        const HexSeg& sg = g == 0 ? a.seg[0] : (g == 1 ? a.seg[1] : a.seg[2]);
+        lcb = sg.codes_t + (size_t)rb * nc * 64;
+        lsb = sg.scales_t + (size_t)rb * nc * 16;
+    };
+    auto lissue = [&](uint4& cw, uint32_t& sw) {
+        const int c = wr + lj * WR;
+        cw = lcb[c * 64 + lane];
+        sw = lsb[c * 16 + (lane & 15)];
+        if (++lj == P) {
+            lj = 0;
+            lset(++lk);
+        }
+    };
+
+    // prologue loads in the order they are needed: x (and the norm
+    // weights) first, then the first chunk of codes (HBM), so waiting for x
+    // never waits behind the codes
+    constexpr int XPT = 4, WPT = 1;   // float4 of x / norm weights held in registers
+    const int nq = a.cols >> 2;
+    float4 xq[XPT], wq[WPT];
+#pragma unroll
+    for (int i = 0; i < XPT; i++) {
+        const int q = tid + i * (int)blockDim.x;
+        xq[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (i < WPT) wq[i] = make_float4(1.f, 1.f, 1.f, 1.f);
+        if (q < nq) {
+            xq[i] = reinterpret_cast<const float4*>(a.x)[q];
+            if (i < WPT && a.norm_w) wq[i] = reinterpret_cast<const float4*>(a.norm_w)[q];
+        }
+    }
+    auto xw = [&](int i, int q, float4& xv, float4& wv) {   // x and w of float4 q = tid + i * blockDim
+        xv = i < XPT ? xq[i] : reinterpret_cast<const float4*>(a.x)[q];
+        if (i < WPT) wv = wq[i];
+        else wv = a.norm_w ? reinterpret_cast<const float4*>(a.norm_w)[q] : make_float4(1.f, 1.f, 1.f, 1.f);
+    };
+    // codebook copies: entry e of lane l at byte e * 256 + l * 4.  Wave w
+    // writes entries 16w .. 16w + 15 (waves 16 apart when fewer than 16
+    // waves cover the table); their fields come in one 64-byte scalar read
+    // (the field tables are padded to 256 entries)
+    uint32_t fv[16];
+    const int wid_u = __builtin_amdgcn_readfirstlane(wid);
+    if (TB > 0 && wid_u * 16 < TB) {
+        const uint32_t* fp = a.seg[0].fields + wid_u * 16;
+#pragma unroll
+        for (int j = 0; j < 16; j++) fv[j] = fp[j];
+    }
+    uint4 cA, cB;
+    uint32_t sA, sB;
+    if (TB > 0) {
+        if (wid_u * 16 < TB) {
+#pragma unroll
+            for (int j = 0; j < 16; j++)
+                if (wid_u * 16 + j < TB) stab[(wid_u * 16 + j) * 64 + lane] = fv[j];
+        }
+        // fewer than TB / 16 waves: the remaining slices, one entry at a time
+        const uint32_t* f = a.seg[0].fields;
+        for (int e = NW * 16 + wid; e < TB; e += NW) stab[e * 64 + lane] = f[e];
+    } else {
+        for (int g = 0; g < a.nseg; g++) {
+            uint32_t* t = reinterpret_cast<uint32_t*>(dyn + toff(g));
+            const uint32_t* f = a.seg[g].fields;
+            for (int e = wid; e < a.seg[g].n_pts; e += NW) t[e * 64 + lane] = f[e];
+        }
+    }
+
+    // x' = (x * inv) * w (gsd_lq_cpu_engine.c:66-82), then (u, v) * 2^e as
+    // fp16 hi / lo in the A-operand order X[c][h][t][g][m].  One pass gives
+    // sum x^2 and max |x w|, |x_a w_a / 2 + s x_b w_b| (times inv: the
+    // largest |u|, |v| up to rounding), reduced together.
+    constexpr float kS32 = 0.866025403784438646763723170752936183f;
+    float ss = 0.f, mx = 0.f;
+    for (int i = 0; i < (nq + (int)blockDim.x - 1) / (int)blockDim.x; i++) {
+        const int q = tid + i * (int)blockDim.x;
+        if (q >= nq) break;
+        float4 xv, wv;
+        xw(i, q, xv, wv);
+        ss = fmaf(xv.x, xv.x, ss); ss = fmaf(xv.y, xv.y, ss); ss = fmaf(xv.z, xv.z, ss); ss = fmaf(xv.w, xv.w, ss);
+        const float p0 = xv.x * wv.x, p1 = xv.y * wv.y, p2 = xv.z * wv.z, p3 = xv.w * wv.w;
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(p0), fabsf(fmaf(kS32, p1, 0.5f * p0))),
+                             fmaxf(fabsf(p2), fabsf(fmaf(kS32, p3, 0.5f * p2)))));
+    }
+    // this wave's first two steps (see the main loop) go out once its x and
+    // codebook reads are back: x was written by the previous launch, possibly
+    // on another XCD, and its reads share the fabric with the code stream
+    lset(0);
+    lissue(cA, sA);
+    lissue(cB, sB);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        ss += __shfl_xor(ss, o, 64);
+        mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    }
+    if (lane == 0) {
+        scratch[wid] = ss;
+        scratch[16 + wid] = mx;
+    }
+    lds_barrier();
+    ss = 0.f;
+    mx = 0.f;
+    for (int w = 0; w < NW; w++) {
+        ss += scratch[w];
+        mx = fmaxf(mx, scratch[16 + w]);
+    }
+    const float inv = a.norm_w ? 1.0f / sqrtf(ss / (float)a.cols + a.eps) : 1.f;
+    mx *= inv;
+    // power-of-two scale putting the largest |u|, |v| near [2^13, 2^14)
+    int ex = 0;
+    if (mx > 0.f && mx < INFINITY) (void)frexpf(mx, &ex);
+    const float up = ldexpf(1.f, 14 - ex), down = ldexpf(1.f, ex - 14);
+    uint32_t* X32 = reinterpret_cast<uint32_t*>(X);
+    auto put = [&](int p, float xa, float xb) {   // pair p of the padded row
+        const float uu = xa * up, vv = fmaf(kS32, xb, 0.5f * xa) * up;
+        const _Float16 uh = (_Float16)uu, vh = (_Float16)vv;
+        const _Float16 ul = (_Float16)(uu - (float)uh), vl = (_Float16)(vv - (float)vh);
+        const int c = p >> 6, h = (p >> 5) & 1, g = (p >> 3) & 3, t = (p >> 2) & 1, e = p & 3;
+        const int base = ((((c * 2 + h) * 2 + t) * 4 + g) * 2) * 4 + e;
+        X32[base] = (uint32_t)__builtin_bit_cast(uint16_t, uh) | ((uint32_t)__builtin_bit_cast(uint16_t, vh) << 16);
+        X32[base + 4] = (uint32_t)__builtin_bit_cast(uint16_t, ul) | ((uint32_t)__builtin_bit_cast(uint16_t, vl) << 16);
+    };
+    for (int i = 0; i < (nq + (int)blockDim.x - 1) / (int)blockDim.x; i++) {
+        const int q = tid + i * (int)blockDim.x;
+        if (q >= nq) break;
+        float4 xv, wv;
+        xw(i, q, xv, wv);
+        if (a.norm_w) {
+            xv.x = (xv.x * inv) * wv.x; xv.y = (xv.y * inv) * wv.y;
+            xv.z = (xv.z * inv) * wv.z; xv.w = (xv.w * inv) * wv.w;
+        }
+        put(2 * q, xv.x, xv.y);
+        put(2 * q + 1, xv.z, xv.w);
+    }
+    for (int p = (a.cols >> 1) + tid; p < nc * 64; p += blockDim.x) put(p, 0.f, 0.f);   // padding
+    unsigned have = 0;   // epilogue lanes: rank-k values of segment g fetched
+    for (int g = 0; g < a.nseg; g++) {
+        if (a.seg[g].k > 0 && a.seg[g].tmp_k) {
+            if (tid < a.seg[g].k) tkl[g][tid] = a.seg[g].tmp_k[tid];
+            have |= 1u << g;
+        }
+    }
+    lds_barrier();
+
+    const uint32_t lane_off = (uint32_t)lane * 4u;
+    const int m = lane & 15, lg = lane >> 4;
+    auto step = [&](int g, int c, const uint4 cw, const uint32_t sw, float& acc) {
+        const unsigned char* tb = TB > 0 ? reinterpret_cast<const unsigned char*>(stab) : dyn + toff(g);
+        const uint32_t w4[4] = {cw.x, cw.y, cw.z, cw.w};
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            float4v d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                // rows m >= 2 of A only feed rows m >= 2 of D, which are never
+                // read: every lane loads row m & 1 (no masking, no zeroing)
+                const uint4 xv = X[(((c * 2 + h) * 2 + t) * 4 + lg) * 2 + (m & 1)];
+                u32x4v aw;
+                aw[0] = xv.x; aw[1] = xv.y; aw[2] = xv.z; aw[3] = xv.w;
+                const uint32_t w = w4[2 * h + t];
+                u32x4v bw;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const uint32_t addr = __builtin_amdgcn_perm(w, lane_off, 0x0C0C0400u + (e << 8));
+                    bw[e] = *reinterpret_cast<const uint32_t*>(tb + addr);
+                }
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, aw), __builtin_bit_cast(half8v, bw),
+                                                          d, 0, 0, 0);
+            }
+            const uint16_t sh = (uint16_t)(h ? (sw >> 16) : (sw & 0xFFFFu));
+            acc = fmaf(d[0] + d[1], h2f(sh), acc);
+        }
+    };
+
+    const int rpos = a.epilogue == kEpiRopeKV ? (a.rope.pos_dev ? *a.rope.pos_dev : a.rope.pos) : 0;
+    float pre = 0.f;                       // epilogue inputs of the current unit,
+    float2 pcs = make_float2(1.f, 0.f);    // fetched when the unit starts
+    auto prefetch = [&](int uu) {
+        if (wid == 0 && lane < 16 && uu < nunits) {
+            const int g = seg_of(uu);
+            const HexSeg& sp = g == 0 ? a.seg[0] : (g == 1 ? a.seg[1] : a.seg[2]);
+            const int prow = (paired ? uu : uu - ubase(g)) * 16 + lane;
+            if (prow < sp.rows) {
+                if (a.epilogue == kEpiResidual) pre = a.resid[prow];
+                if (a.epilogue == kEpiRopeKV && g != 2)
+                    pcs = a.rope.cs[(size_t)rpos * (a.rope.hd >> 1) + ((prow % a.rope.hd) >> 1)];
+            }
+        }
+    };
+    int rbuf = 0;
+    auto unit_end = [&](int u, float& acc) {
+        const int g = seg_of(u);
+        if (lane < 16) red[rbuf][wid][lane] = acc;
+        acc = 0.f;
+        lds_barrier();
+        if (wid == 0 && lane < 16) {
+            float fin0 = 0.f, fin1 = 0.f;
+#pragma unroll
+            for (int gi = 0; gi < 2; gi++) {
+                if (gi >= G) break;
+                const int sg_i = paired ? gi : g;
+                const HexSeg& sg = sg_i == 0 ? a.seg[0] : (sg_i == 1 ? a.seg[1] : a.seg[2]);
+                const int rb = paired ? u : u - ubase(sg_i);
+                const int row = rb * 16 + lane;
+                float t = 0.f;
+                for (int w = 0; w < WR; w++) t += red[rbuf][gi * WR + w][lane];
+                t *= down;
+                if (row < sg.rows) {
+                    if (sg.row_ptr) {
+                        const uint32_t e = sg.row_ptr[row + 1];
+                        for (uint32_t i = sg.row_ptr[row]; i < e; i++) t += sg.kdel[i] * xnorm(a, sg.kcols[i], inv);
+                    }
+                    if (sg.k > 0) {
+                        if (!((have >> sg_i) & 1u)) {
+                            // bounded wait for the published rank-k words of
+                            // this segment (normally already there)
+                            int off = 0;
+                            for (int g2 = 0; g2 < sg_i; g2++)
+                                if (!a.seg[g2].tmp_k && a.seg[g2].k > 0) off += a.seg[g2].k;
+                            int spins = 0;
+                            for (int jj = 0; jj < sg.k; jj++) {
+                                unsigned long long wv;
+                                while (((wv = __hip_atomic_load(&a.pub[off + jj], __ATOMIC_RELAXED,
+                                                                __HIP_MEMORY_SCOPE_AGENT)) >> 32) == 0 &&
+                                       spins < (1 << 20)) {
+                                    if (++spins == (1 << 20)) *a.err = 1u;
+                                    __builtin_amdgcn_s_sleep(1);
+                                }
+                                tkl[sg_i][jj] = __uint_as_float((unsigned)wv);
+                            }
+                            have |= 1u << sg_i;
+                        }
+                        const uint16_t* up_ = sg.U + (size_t)row * sg.k;
+                        for (int jj = 0; jj < sg.k; jj++) t += h2f(up_[jj]) * tkl[sg_i][jj];
+                    }
+                }
+                if (gi == 0) fin0 = t;
+                else fin1 = t;
+            }
+            const HexSeg& s0 = paired ? a.seg[0] : (g == 0 ? a.seg[0] : (g == 1 ? a.seg[1] : a.seg[2]));
+            const int row = (paired ? u : u - ubase(g)) * 16 + lane;
+            if (paired) {
+                if (row < s0.rows) s0.out[row] = (fin0 / (1.0f + expf(-fin0))) * fin1;
+            } else if (a.epilogue == kEpiStore) {
+                if (row < s0.rows) s0.out[row] = fin0;
+            } else if (a.epilogue == kEpiResidual) {
+                if (row < s0.rows) a.resid[row] = pre + fin0;
+            } else {
+                // kEpiRopeKV: rows 2i, 2i+1 of a head are one rotation pair
+                // (interleaved RoPE, gsd_lq_cpu_engine.c:213-256) in lanes
+                // 2i, 2i+1; evaluated without contraction like the reference
+#pragma clang fp contract(off)
+                const RopeKV& r = a.rope;
+                const float partner = __shfl_xor(fin0, 1, 64);
+                const size_t base = ((size_t)r.layer * r.max_seq + (size_t)rpos) * (size_t)r.n_kv * r.hd;
+                if (row < s0.rows) {
+                    if (g == 2) {
+                        r.v_cache[base + row] = f2h(fin0);
+                    } else {
+                        const bool odd = (lane & 1) != 0;
+                        const float x0 = odd ? partner : fin0, x1 = odd ? fin0 : partner;
+                        const float2 cs = pcs;
+                        const float y = odd ? (x0 * cs.y + x1 * cs.x) : (x0 * cs.x - x1 * cs.y);
+                        if (g == 0) s0.out[row] = y;
+                        else r.k_cache[base + row] = f2h(y);
+                    }
+                }
+            }
+        }
+        rbuf ^= 1;
+        prefetch(u + nblk);
+    };
+
+    prefetch(u0);
+    float acc = 0.f;
+    int cj = 0, ck = 0, cu = u0;
+    int cg = seg_of(min(u0, nunits - 1));
+    auto cadvance = [&]() {
+        if (++cj == P) {
+            if (ck < my_units) unit_end(cu, acc);
+            cj = 0;
+            ++ck;
+            cu += nblk;
+            cg = seg_of(min(cu, nunits - 1));
+        }
+    };
+    // two steps in flight at all times: buffer A holds the even steps, B the
+    // odd ones; every load is issued (the cursor clamps past the end), and the
+    // odd half of the last pair may compute a step past the end that no unit
+    // end collects
+    for (int s = 0; s < nsteps; s += 2) {
+        step(cg, wr + cj * WR, cA, sA, acc);
+        lissue(cA, sA);
+        cadvance();
+        step(cg, wr + cj * WR, cB, sB, acc);
+        lissue(cB, sB);
+        cadvance();
+    }
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------------
@@ -960,6 +1395,63 @@ hipError_t launch_hexmv(const HexArgs& a, hipStream_t st) {
         GSD_HEXMV_DISPATCH(true, 2)
     }
 #undef GSD_HEXMV_DISPATCH
+}
+
+template <int TB>
+hipError_t launch_hexmv4_t(const HexArgs& a, hipStream_t st, int nw, size_t lds, int nunits, int nlead) {
+    static int per_cu = 0;
+    static size_t attr_lds = 0;
+    if (lds > attr_lds) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&hexmv4_kernel<TB>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        attr_lds = lds;
+        per_cu = 0;
+    }
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, hexmv4_kernel<TB>, nw * 64, lds) != hipSuccess || n < 1)
+        return hipErrorInvalidConfiguration;
+    per_cu = n;
+    const int ncu = device_cu_count() > 0 ? device_cu_count() : 256;
+    int grid = ncu * per_cu;
+    if (grid > nunits) grid = nunits;
+    // publishing blocks first: dispatched in order, they are resident before
+    // any matvec block waits on them
+    hipLaunchKernelGGL((hexmv4_kernel<TB>), dim3(grid + nlead), dim3(nw * 64), lds, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_hexmv4(const HexArgs& a, hipStream_t st) {
+    if (a.nseg < 1 || a.nseg > kMaxSeg || a.cols <= 0 || a.cols % 64) return hipErrorInvalidValue;
+    const int nc = (a.cols + 127) / 128;
+    const bool paired = a.epilogue == kEpiSwiGLU;
+    if (paired && (a.nseg != 2 || a.seg[0].rows != a.seg[1].rows)) return hipErrorInvalidValue;
+    if (a.epilogue == kEpiRopeKV && a.nseg != 3) return hipErrorInvalidValue;
+    bool shared = true;
+    int nlead = 0, nunits = 0, tab_bytes = 0;
+    for (int g = 0; g < a.nseg; g++) {
+        const HexSeg& s = a.seg[g];
+        if (!s.codes_t || !s.scales_t || !s.fields || s.n_pts < 1 || s.n_pts > kTableSlots) return hipErrorInvalidValue;
+        shared = shared && s.fields == a.seg[0].fields && s.n_pts == a.seg[0].n_pts;
+        if (!s.tmp_k && s.k > 0) nlead += s.k;
+        nunits += (s.rows + 15) / 16;
+        tab_bytes += s.n_pts * 256;
+    }
+    if (paired) nunits = (a.seg[0].rows + 15) / 16;
+    if (nlead > 0 && (!a.pub || !a.err)) return hipErrorInvalidValue;
+    if (nunits == 0) return hipSuccess;
+    // waves per row-block: up to 16 (8 per group when paired), at most one
+    // per 128-column chunk
+    // waves per row-block: the largest power of two <= 16 / G dividing the
+    // chunk count (so every wave has the same number of chunks per unit)
+    const int G = paired ? 2 : 1;
+    int wr = kMv4MaxWaves / G;
+    while (wr > 1 && nc % wr != 0) wr >>= 1;
+    const int nw = wr * G;
+    const size_t xbytes = (size_t)nc * 512;
+    if (shared && a.seg[0].n_pts == 217) return launch_hexmv4_t<217>(a, st, nw, xbytes, nunits, nlead);
+    if (shared && a.seg[0].n_pts == 127) return launch_hexmv4_t<127>(a, st, nw, xbytes, nunits, nlead);
+    return launch_hexmv4_t<0>(a, st, nw, xbytes + (size_t)tab_bytes, nunits, nlead);
 }
 
 hipError_t launch_lowrank(const float* x, const uint16_t* Vt, const float* S, float* tmp_k, int k, int cols,
