@@ -149,6 +149,55 @@ def bench_linear(bank, steps, warmup):
     return gbs, ms_step, roof
 
 
+MFMA_F16_PEAK_TFLOPS = 2500.0   # MI355X dense fp16 / bf16 matrix peak
+
+
+def bench_prefill(bank, ms=(16, 128, 512), reps=3):
+    """Batched projection (prefill) over the bank's Turbo layer sets: for each
+    M, the 7 tensors of every distinct layer through gsdh_model_matmul,
+    graph-captured; FLOPs = 2*M*rows*cols, bytes = packed weights + bf16 X +
+    fp32 Y.  Roofline: MFMA (fp16 dense peak) for M >= 128, HBM for M = 16."""
+    model = build_model(bank, bank.n)
+    lib = model.cl.lib
+    shapes = [(t, bank.packed[(0, t)]["rows"], bank.packed[(0, t)]["cols"]) for t in layer_shapes()]
+    slot = {"attn_q": 0, "attn_k": 1, "attn_v": 2, "attn_output": 3, "ffn_gate": 4, "ffn_up": 5, "ffn_down": 6}
+    mmax, cmax = max(ms), max(c for _, _, c in shapes)
+    rmax = max(r for _, r, _ in shapes)
+    x = ctypes.c_void_p()
+    y = ctypes.c_void_p()
+    lib.gsdh_malloc(ctypes.byref(x), mmax * cmax * 2)
+    lib.gsdh_malloc(ctypes.byref(y), mmax * rmax * 4)
+    rng = np.random.default_rng(5)
+    xb = (rng.standard_normal(mmax * cmax).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    lib.gsdh_memcpy_h2d(x, xb.ctypes.data_as(ctypes.c_void_p), xb.nbytes, None)
+    lib.gsdh_stream_sync(None)
+    out = {}
+    flops_layer = sum(2 * r * c for _, r, c in shapes)
+    wbytes_layer = bank.layer_bytes[0]
+    for M in ms:
+        issue = lambda: [lib.gsdh_model_matmul(model._m, l, slot[t], x, M, y)
+                         for l in range(bank.n) for t, _, _ in shapes]
+        issue()                                   # workspace for this M, outside the capture
+        lib.gsdh_stream_sync(lib.gsdh_model_stream(model._m))
+        ge = capture(model, issue)
+        time_graph(model, ge, 1)
+        ms_total = time_graph(model, ge, reps)
+        lib.gsdh_graph_destroy(ge)
+        us_layer = ms_total * 1e3 / (reps * bank.n)
+        tflops = M * flops_layer / (us_layer * 1e-6) / 1e12
+        nbytes = wbytes_layer + sum(2 * M * c + 4 * M * r for _, r, c in shapes)
+        gbs = nbytes / (us_layer * 1e-6) / 1e9
+        bound = "mfma" if M >= 128 else "hbm"
+        out[f"M{M}"] = {"us_per_layer": round(us_layer, 2), "tflops": round(tflops, 2), "GBs": round(gbs, 1),
+                        "tokens_per_s_per_layer": round(M / (us_layer * 1e-6), 1), "bound": bound,
+                        "frac": round(tflops / MFMA_F16_PEAK_TFLOPS if bound == "mfma" else gbs / HBM_PEAK_GBS, 4)}
+        log(f"prefill M={M}: {us_layer:.1f} us/layer, {tflops:.1f} TFLOP/s, {gbs:.0f} GB/s")
+    lib.gsdh_free(x)
+    lib.gsdh_free(y)
+    model.close()
+    return out
+
+
 def bench_decode(bank, n_prompt=64, n_new=128):
     """Greedy decode tok/s of a 32-layer 7B-shaped model (layers are copies of
     the bank's distinct layers, each copy its own HBM allocation)."""
@@ -251,6 +300,7 @@ def main():
     ap.add_argument("--no-precision", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--probe", choices=["gateup", "copy"], help="run one kernel for rocprofv3 counters")
     a = ap.parse_args()
     if a.probe:
@@ -268,6 +318,9 @@ def main():
     gbs, ms_step, roof = bench_linear(turbo, a.steps, a.warmup)
     log(f"turbo layer set: {gbs:.1f} GB/s, {ms_step * 1e3:.1f} us/step; gate/up {roof['achieved']} GB/s")
     extra = {}
+    if not a.no_prefill:
+        extra["prefill_turbo"] = dict(bench_prefill(turbo), workload="Turbo 7B layer set (7 tensors), X bf16 "
+                                      "[M][cols] -> Y fp32, fp16 MFMA with fp32 accumulation")
     if not a.no_precision:
         prec = LayerBank("precision", max(3, a.layers // 2))
         pg, pms, proof = bench_linear(prec, a.steps, a.warmup)

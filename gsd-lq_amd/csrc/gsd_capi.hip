@@ -284,6 +284,8 @@ struct gsdh_model {
     float2* cs = nullptr;
     float* ws = nullptr;
     unsigned* counters = nullptr;
+    void* mm_ws = nullptr;          // prefill staging (A fragments | descales | rank-k values)
+    size_t mm_ws_bytes = 0;
     unsigned long long* pub = nullptr;   // rank-k publication words, one range per matvec launch
     int pub_words = 0, pub_next = 0;
     int chunk = 64, max_splits = 1;
@@ -538,6 +540,7 @@ int gsdh_model_destroy(gsdh_model* m) {
     for (auto& t : m->hex)
         if (t.block) (void)hipFree(t.block);
     for (void* p : m->allocs) (void)hipFree(p);
+    if (m->mm_ws) (void)hipFree(m->mm_ws);
     if (m->st_host) (void)hipHostFree(m->st_host);
     if (m->stream) (void)hipStreamDestroy(m->stream);
     delete m;
@@ -714,6 +717,46 @@ int gsdh_generate_greedy(gsdh_model* m, const int* prompt, int n_prompt, int sta
     (void)hipStreamSynchronize(m->stream);
     (void)hipHostFree(ring);
     return rc;
+}
+
+int gsdh_model_matmul(gsdh_model* m, int layer, int slot, const uint16_t* X, int M, float* Y) {
+    if (!m || !X || !Y) return fail(-1, "matmul: null argument");
+    if (slot < 0 || slot > GSDH_LM_HEAD) return fail(-1, "matmul: slot %d", slot);
+    if (slot != GSDH_LM_HEAD && (layer < 0 || layer >= m->c.n_layers)) return fail(-1, "matmul: layer %d", layer);
+    if (M <= 0) return fail(-1, "matmul: M %d", M);
+    const HexDev& t = m->slot(layer, slot);
+    if (!t.set) return fail(-1, "matmul: layer %d slot %d not set", layer, slot);
+    const size_t xa = (hexmm_xa_bytes(M, t.cols) + 255) / 256 * 256;
+    const size_t xs = ((size_t)(M + 15) / 16 * 16 * 4 + 255) / 256 * 256;
+    const size_t tk = ((size_t)M * kMaxRank * 4 + 255) / 256 * 256;
+    const MatmulPlan plan = hexmm_plan(M, t.rows, t.cols);
+    const int nsplit = plan.nsplit;
+    const size_t pt = nsplit > 1 ? (size_t)nsplit * ((M + 15) / 16 * 16) * t.rows * 4 : 0;
+    if (xa + xs + tk + pt > m->mm_ws_bytes) {
+        HIPCHK(hipStreamSynchronize(m->stream));
+        if (m->mm_ws) (void)hipFree(m->mm_ws);
+        m->mm_ws = nullptr;
+        m->mm_ws_bytes = 0;
+        HIPCHK(hipMalloc(&m->mm_ws, xa + xs + tk + pt));
+        m->mm_ws_bytes = xa + xs + tk + pt;
+    }
+    char* w = static_cast<char*>(m->mm_ws);
+    MatmulArgs a{};
+    fill_seg(a.w, t, m, nullptr);
+    a.X = X;
+    a.xa = reinterpret_cast<uint4*>(w);
+    a.xs = reinterpret_cast<float*>(w + xa);
+    a.tmp_k = t.k > 0 ? reinterpret_cast<float*>(w + xa + xs) : nullptr;
+    a.Y = Y;
+    a.M = M;
+    a.cols = t.cols;
+    a.nsplit = nsplit;
+    a.tg = plan.tg;
+    a.rbw = plan.rbw;
+    a.part = nsplit > 1 ? reinterpret_cast<float*>(w + xa + xs + tk) : nullptr;
+    if (t.k > 0) HIPCHK(launch_lowrank_batched(X, t.Vt, t.Sv, reinterpret_cast<float*>(w + xa + xs), M, t.k, t.cols, m->stream));
+    HIPCHK(launch_hexmm(a, m->stream));
+    return 0;
 }
 
 int gsdh_model_run_linear(gsdh_model* m, int layer, int mask) {

@@ -88,6 +88,36 @@ hipError_t launch_hexmv(const HexArgs& a, hipStream_t stream);
 // MFMA matvec over the tiled layout (codes_t / scales_t / fields of every
 // segment); same epilogues, norm and rank-k handling as launch_hexmv.
 hipError_t launch_hexmv4(const HexArgs& a, hipStream_t stream);
+
+// Batched projection (prefill) on the matrix cores: Y[m][r] = W x_m for M
+// tokens, W one packed tensor in the tiled layout.  X is bf16 [M][cols];
+// xa is the fp16 A-operand staging of X (hexmm_xa_bytes), xs the per-token
+// descale factors [ceil(M/16)*16]; tmp_k [M][k] the tokens' rank-k values
+// (null when k == 0).
+struct MatmulArgs {
+    HexSeg w;                  // codes_t, scales_t, fields, rows, n_pts, kinks, U, k
+    const uint16_t* X;
+    uint4* xa;
+    float* xs;
+    const float* tmp_k;
+    float* Y;
+    float* part;               // split-K partials [nsplit][ceil(M/16)*16][rows] (nsplit > 1)
+    int M, cols;
+    int nsplit;                // column splits (1: blocks write Y directly)
+    int tg, rbw;               // tiling (hexmm_plan)
+};
+size_t hexmm_xa_bytes(int M, int cols);
+// Tiling of a batched projection: token groups per block (tg: 1, 2, 4, 8),
+// row blocks per wave (rbw) and column splits (nsplit), chosen so the grid
+// fills the chip with the fewest re-decodes of the weights.
+struct MatmulPlan {
+    int tg, rbw, nsplit;
+};
+MatmulPlan hexmm_plan(int M, int rows, int cols);
+hipError_t launch_hexmm(const MatmulArgs& a, hipStream_t stream);
+// tmp[m][j] = S[j] * sum_c bf16(X[m][c]) * Vt[j][c]
+hipError_t launch_lowrank_batched(const uint16_t* X, const uint16_t* Vt, const float* S, float* tmp,
+                                  int M, int k, int cols, hipStream_t stream);
 hipError_t launch_lowrank(const float* x, const uint16_t* Vt, const float* S, float* tmp_k,
                           int k, int cols, hipStream_t stream);
 hipError_t launch_rmsnorm(const float* x, const float* w, float* out, int dim, float eps,

@@ -19,6 +19,7 @@
 //     blocks 0..sum(k)-1, and published to the others through flags;
 //   * epilogue fusions: kinks and the U tmp_k term, then store / residual add /
 //     SwiGLU of paired gate-up rows.
+#include <algorithm>
 #include <cstdlib>
 
 #include "gsd_internal.h"
@@ -1356,6 +1357,252 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(8))) 
     }
 }
 
+// ------------------------------------------------------------------------
+// hexmm: batched projection for prefill (no reference kernel: the reference
+// prefills token by token, chat.py:1128-1130).  Same lattice form and tiled
+// weight layout as hexmv4; the MFMA A rows are 16 tokens instead of the hi/lo
+// parts of one vector:
+//   A[m][k] = token m's (u, v) per pair, fp16 after a per-token power-of-two
+//             prescale (single rounding: ~1e-4 relative on the outputs),
+//   B[k][n] = row n's (r0, r1), decoded once per 128-column chunk and reused
+//             for every token group of the block,
+//   D lane l = tokens 4(l >> 4) .. +3 of row l & 15.
+// A block is 8 waves; wave w owns RBW row-blocks; the block covers TG token
+// groups.  Per chunk the A fragments of the block's tokens are staged in LDS
+// (loaded into registers one chunk ahead), the codes are double-buffered in
+// registers.  Tiles of one row range are placed on one XCD (block b runs on
+// XCD b % 8), so their weight reads share that XCD's L2.
+// ------------------------------------------------------------------------
+__device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// X bf16 [M][cols] -> A fragments xa[(g16 * nc + c) * 4 + (h * 2 + t)][lane] (uint4
+// = (u, v) fp16 of 4 pairs), lane = (m & 15) + 16 * lg, pair 64c + 32h + 8lg + 4t + e;
+// xs[m] = the token's descale.  One block per token (padded tokens: zeros).
+__global__ void __launch_bounds__(256) hexmm_xprep_kernel(const uint16_t* X, int M, int cols, uint4* xa, float* xs) {
+    __shared__ float scratch[16];
+    constexpr float kS32 = 0.866025403784438646763723170752936183f;
+    const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int nc = (cols + 127) >> 7, np = cols >> 1;
+    const bool valid = m < M;
+    const uint16_t* xr = X + (size_t)(valid ? m : 0) * cols;
+    float mx = 0.f;
+    if (valid)
+        for (int p = tid; p < np; p += 256) {
+            const float xa_ = bf2f(xr[2 * p]), xb_ = bf2f(xr[2 * p + 1]);
+            mx = fmaxf(mx, fmaxf(fabsf(xa_), fabsf(fmaf(kS32, xb_, 0.5f * xa_))));
+        }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    if (lane == 0) scratch[wid] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(scratch[0], scratch[1]), fmaxf(scratch[2], scratch[3]));
+    int ex = 0;
+    if (mx > 0.f && mx < INFINITY) (void)frexpf(mx, &ex);
+    const float up = ldexpf(1.f, 14 - ex);
+    if (tid == 0) xs[m] = valid ? ldexpf(1.f, ex - 14) : 0.f;
+    uint32_t* x32 = reinterpret_cast<uint32_t*>(xa);
+    const int g16 = m >> 4, ml = m & 15;
+    for (int p = tid; p < nc * 64; p += 256) {
+        float u = 0.f, v = 0.f;
+        if (valid && p < np) {
+            const float xa_ = bf2f(xr[2 * p]), xb_ = bf2f(xr[2 * p + 1]);
+            u = xa_ * up;
+            v = fmaf(kS32, xb_, 0.5f * xa_) * up;
+        }
+        const int c = p >> 6, h = (p >> 5) & 1, lg = (p >> 3) & 3, t = (p >> 2) & 1, e = p & 3;
+        const size_t idx = ((((size_t)g16 * nc + c) * 4 + h * 2 + t) * 64 + ml + 16 * lg) * 4 + e;
+        x32[idx] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)u) |
+                   ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v) << 16);
+    }
+}
+
+__global__ void __launch_bounds__(256) lowrank_batched_kernel(const uint16_t* X, const uint16_t* Vt, const float* S,
+                                                             float* tmp, int k, int cols) {
+    __shared__ float scratch[16];
+    const int m = blockIdx.x, j = blockIdx.y;
+    float p = 0.f;
+    for (int c = threadIdx.x; c < cols; c += blockDim.x)
+        p = fmaf(bf2f(X[(size_t)m * cols + c]), h2f(Vt[(size_t)j * cols + c]), p);
+    p = block_sum(p, scratch);
+    if (threadIdx.x == 0) tmp[(size_t)m * k + j] = p * S[j];
+}
+
+template <int TB, int TG, int RBW>
+__global__ void __launch_bounds__(512) hexmm_kernel(const MatmulArgs a) {
+    constexpr int W = 8;
+    __shared__ __attribute__((aligned(16))) uint32_t stab[TB > 0 ? TB * 64 : 1];
+    __shared__ uint4 As[TG * 4 * 64];
+    extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int nc = (a.cols + 127) >> 7;
+    const int rows = a.w.rows, nrb = (rows + 15) >> 4, ng = (a.M + 15) >> 4;
+    const int n_rt = (nrb + W * RBW - 1) / (W * RBW), n_tt = (ng + TG - 1) / TG;
+    const int S = a.nsplit, cps = (nc + S - 1) / S;
+    // XCD-aware tile order: the token tiles and column splits of one row
+    // tile share XCD b % 8
+    const int xcd = (int)blockIdx.x & 7, q = (int)blockIdx.x >> 3;
+    const int rt = (q / (n_tt * S)) * 8 + xcd, tt = (q % (n_tt * S)) / S, ks = q % S;
+    if (rt >= n_rt) return;
+    const int rb0 = rt * W * RBW + wid * RBW;
+    const int g0 = tt * TG;
+    const int c0 = ks * cps, c1 = min(nc, c0 + cps);
+    if (c0 >= c1) return;
+
+    // codes of this wave's row blocks for chunk c
+    auto load = [&](int c, uint4 (&cw)[RBW], uint32_t (&sw)[RBW]) {
+        c = min(c, nc - 1);
+#pragma unroll
+        for (int r = 0; r < RBW; r++) {
+            const size_t i = (size_t)min(rb0 + r, nrb - 1) * nc + c;
+            cw[r] = a.w.codes_t[i * 64 + lane];
+            sw[r] = a.w.scales_t[i * 16 + (lane & 15)];
+        }
+    };
+    // this thread's share of the block's A fragments for chunk c
+    constexpr int APT = (TG * 256 + 511) / 512;
+    auto aload = [&](int c, uint4 (&av)[APT]) {
+        c = min(c, nc - 1);
+#pragma unroll
+        for (int i = 0; i < APT; i++) {
+            const int j = tid + i * 512;
+            const int tg = j >> 8, g = min(g0 + tg, ng - 1);
+            av[i] = j < TG * 256 ? a.xa[((size_t)g * nc + c) * 256 + (j & 255)] : make_uint4(0u, 0u, 0u, 0u);
+        }
+    };
+    uint4 av[APT];
+    aload(c0, av);
+    uint4 cA[RBW], cB[RBW];
+    uint32_t sA[RBW], sB[RBW];
+    load(c0, cA, sA);
+    load(c0 + 1, cB, sB);
+
+    // codebook: entry e of lane l at byte e * 256 + l * 4
+    const int n_pts = a.w.n_pts;
+    uint32_t* tabw = TB > 0 ? stab : reinterpret_cast<uint32_t*>(dyn);
+    for (int e = wid; e < (TB > 0 ? TB : n_pts); e += W) tabw[e * 64 + lane] = a.w.fields[e];
+    const unsigned char* tb = TB > 0 ? reinterpret_cast<const unsigned char*>(stab) : dyn;
+    const uint32_t lane_off = (uint32_t)lane * 4u;
+
+    float4v acc[RBW][TG];
+#pragma unroll
+    for (int r = 0; r < RBW; r++)
+#pragma unroll
+        for (int g = 0; g < TG; g++) acc[r][g] = float4v{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](const uint4 (&cw)[RBW], const uint32_t (&sw)[RBW]) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            float4v d[RBW][TG];
+#pragma unroll
+            for (int r = 0; r < RBW; r++)
+#pragma unroll
+                for (int g = 0; g < TG; g++) d[r][g] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                u32x4v bw[RBW];
+#pragma unroll
+                for (int r = 0; r < RBW; r++) {
+                    const uint32_t w4[4] = {cw[r].x, cw[r].y, cw[r].z, cw[r].w};
+                    const uint32_t w = w4[2 * h + t];
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        bw[r][e] = *reinterpret_cast<const uint32_t*>(
+                            tb + __builtin_amdgcn_perm(w, lane_off, 0x0C0C0400u + (e << 8)));
+                }
+#pragma unroll
+                for (int g = 0; g < TG; g++) {
+                    const uint4 xv = As[(g * 4 + h * 2 + t) * 64 + lane];
+                    u32x4v aw;
+                    aw[0] = xv.x; aw[1] = xv.y; aw[2] = xv.z; aw[3] = xv.w;
+#pragma unroll
+                    for (int r = 0; r < RBW; r++)
+                        d[r][g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, aw),
+                                                                        __builtin_bit_cast(half8v, bw[r]), d[r][g], 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < RBW; r++) {
+                const float sc = h2f((uint16_t)(h ? (sw[r] >> 16) : (sw[r] & 0xFFFFu)));
+#pragma unroll
+                for (int g = 0; g < TG; g++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[r][g][i] = fmaf(d[r][g][i], sc, acc[r][g][i]);
+            }
+        }
+    };
+
+    // chunks in pairs (codes A / B alternate); the A fragments of chunk c go
+    // to LDS between two barriers, those of c + 1 are already in flight
+    for (int c = c0; c < c1; c += 2) {
+        lds_barrier();
+#pragma unroll
+        for (int i = 0; i < APT; i++)
+            if (tid + i * 512 < TG * 256) As[tid + i * 512] = av[i];
+        aload(c + 1, av);
+        lds_barrier();
+        compute(cA, sA);
+        load(c + 2, cA, sA);
+        if (c + 1 < c1) {
+            lds_barrier();
+#pragma unroll
+            for (int i = 0; i < APT; i++)
+                if (tid + i * 512 < TG * 256) As[tid + i * 512] = av[i];
+            aload(c + 2, av);
+            lds_barrier();
+            compute(cB, sB);
+            load(c + 3, cB, sB);
+        }
+    }
+
+    // epilogue: token m = 16 (g0 + g) + 4 (lane >> 4) + i, row 16 rb + (lane & 15)
+#pragma unroll
+    for (int r = 0; r < RBW; r++) {
+        const int row = (rb0 + r) * 16 + (lane & 15);
+        if (row >= rows) continue;
+#pragma unroll
+        for (int g = 0; g < TG; g++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int m = (g0 + g) * 16 + 4 * (lane >> 4) + i;
+                if (m >= a.M) continue;
+                if (S > 1) {   // partial sum of this column split; hexmm_reduce finishes
+                    a.part[((size_t)ks * ng * 16 + m) * rows + row] = acc[r][g][i];
+                    continue;
+                }
+                float y = acc[r][g][i] * a.xs[m];
+                if (a.w.row_ptr) {
+                    const uint32_t e = a.w.row_ptr[row + 1];
+                    for (uint32_t j = a.w.row_ptr[row]; j < e; j++)
+                        y += a.w.kdel[j] * bf2f(a.X[(size_t)m * a.cols + a.w.kcols[j]]);
+                }
+                if (a.w.k > 0)
+                    for (int j = 0; j < a.w.k; j++)
+                        y += h2f(a.w.U[(size_t)row * a.w.k + j]) * a.tmp_k[(size_t)m * a.w.k + j];
+                a.Y[(size_t)m * rows + row] = y;
+            }
+        }
+    }
+}
+
+// Column-split partials -> Y: descale, then kinks and rank-k terms (the same
+// epilogue as hexmm_kernel); partials summed in split order (deterministic).
+__global__ void __launch_bounds__(256) hexmm_reduce_kernel(const MatmulArgs a) {
+    const int rows = a.w.rows, ng = (a.M + 15) >> 4;
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)a.M * rows) return;
+    const int m = (int)(i / rows), row = (int)(i % rows);
+    float s = 0.f;
+    for (int k = 0; k < a.nsplit; k++) s += a.part[((size_t)k * ng * 16 + m) * rows + row];
+    float y = s * a.xs[m];
+    if (a.w.row_ptr) {
+        const uint32_t e = a.w.row_ptr[row + 1];
+        for (uint32_t j = a.w.row_ptr[row]; j < e; j++) y += a.w.kdel[j] * bf2f(a.X[(size_t)m * a.cols + a.w.kcols[j]]);
+    }
+    if (a.w.k > 0)
+        for (int j = 0; j < a.w.k; j++) y += h2f(a.w.U[(size_t)row * a.w.k + j]) * a.tmp_k[(size_t)m * a.w.k + j];
+    a.Y[i] = y;
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------------
@@ -1452,6 +1699,86 @@ hipError_t launch_hexmv4(const HexArgs& a, hipStream_t st) {
     if (shared && a.seg[0].n_pts == 217) return launch_hexmv4_t<217>(a, st, nw, xbytes, nunits, nlead);
     if (shared && a.seg[0].n_pts == 127) return launch_hexmv4_t<127>(a, st, nw, xbytes, nunits, nlead);
     return launch_hexmv4_t<0>(a, st, nw, xbytes + (size_t)tab_bytes, nunits, nlead);
+}
+
+size_t hexmm_xa_bytes(int M, int cols) {
+    const size_t ng = ((size_t)M + 15) / 16, nc = ((size_t)cols + 127) / 128;
+    return ng * nc * 4 * 64 * 16;
+}
+
+template <int TB, int TG, int RBW>
+hipError_t launch_hexmm_t(const MatmulArgs& a, hipStream_t st) {
+    const int nrb = (a.w.rows + 15) / 16, ng = (a.M + 15) / 16;
+    const int n_rt = (nrb + 8 * RBW - 1) / (8 * RBW), n_tt = (ng + TG - 1) / TG;
+    const int grid = 8 * n_tt * a.nsplit * ((n_rt + 7) / 8);
+    const size_t lds = TB > 0 ? 0 : (size_t)a.w.n_pts * 256;
+    if (lds > 0) {
+        static size_t attr = 0;
+        if (lds > attr) {
+            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&hexmm_kernel<TB, TG, RBW>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return e;
+            attr = lds;
+        }
+    }
+    hipLaunchKernelGGL((hexmm_kernel<TB, TG, RBW>), dim3(grid), dim3(512), lds, st, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a.nsplit <= 1) return e;
+    const size_t n = (size_t)a.M * a.w.rows;
+    hipLaunchKernelGGL(hexmm_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+MatmulPlan hexmm_plan(int M, int rows, int cols) {
+    // fewest token tiles (largest tg: the weights are decoded once per token
+    // tile) that still give about 3/4 of a block per CU; when no tiling does,
+    // split the columns (at least 4 chunks per split, partials within twice
+    // the code bytes)
+    const int nc = (cols + 127) / 128, nrb = (rows + 15) / 16, ng = (M + 15) / 16;
+    const int ncu = device_cu_count() > 0 ? device_cu_count() : 256;
+    MatmulPlan p{1, 1, 1};
+    int tiles = 0;
+    for (int tg = 8; tg >= 1; tg >>= 1) {
+        if (tg > 1 && tg > ng) continue;
+        const int rbw = tg == 8 ? 2 : 1;
+        tiles = ((nrb + 8 * rbw - 1) / (8 * rbw)) * ((ng + tg - 1) / tg);
+        p = MatmulPlan{tg, rbw, 1};
+        if (4 * tiles >= 3 * ncu) return p;
+    }
+    int s = (2 * ncu + tiles - 1) / tiles;
+    s = std::min(s, std::max(1, nc / 4));
+    const long long cap = ((long long)rows * cols) / (4LL * (ng * 16) * rows);
+    p.nsplit = (int)std::max<long long>(1, std::min<long long>(s, cap));
+    return p;
+}
+
+template <int TB>
+hipError_t launch_hexmm_tb(const MatmulArgs& a, hipStream_t st) {
+    if (a.tg == 8 && a.rbw == 2) return launch_hexmm_t<TB, 8, 2>(a, st);
+    if (a.tg == 4 && a.rbw == 1) return launch_hexmm_t<TB, 4, 1>(a, st);
+    if (a.tg == 2 && a.rbw == 1) return launch_hexmm_t<TB, 2, 1>(a, st);
+    if (a.tg == 1 && a.rbw == 1) return launch_hexmm_t<TB, 1, 1>(a, st);
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_hexmm(const MatmulArgs& a, hipStream_t st) {
+    if (a.M <= 0 || a.cols <= 0 || a.cols % 64 || !a.w.codes_t || !a.w.scales_t || !a.w.fields) return hipErrorInvalidValue;
+    if (a.nsplit < 1 || (a.nsplit > 1 && !a.part)) return hipErrorInvalidValue;
+    if (a.w.k > 0 && (!a.tmp_k || !a.w.U)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(hexmm_xprep_kernel, dim3(((a.M + 15) / 16) * 16), dim3(256), 0, st, a.X, a.M, a.cols, a.xa,
+                       a.xs);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (a.w.n_pts == 217) return launch_hexmm_tb<217>(a, st);
+    if (a.w.n_pts == 127) return launch_hexmm_tb<127>(a, st);
+    return launch_hexmm_tb<0>(a, st);
+}
+
+hipError_t launch_lowrank_batched(const uint16_t* X, const uint16_t* Vt, const float* S, float* tmp, int M, int k,
+                                  int cols, hipStream_t st) {
+    if (k <= 0) return hipSuccess;
+    hipLaunchKernelGGL(lowrank_batched_kernel, dim3(M, k), dim3(256), 0, st, X, Vt, S, tmp, k, cols);
+    return hipGetLastError();
 }
 
 hipError_t launch_lowrank(const float* x, const uint16_t* Vt, const float* S, float* tmp_k, int k, int cols,

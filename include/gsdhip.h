@@ -153,6 +153,19 @@ int gsdh_forward_token(gsdh_model* m, int token_id, int pos, int want_logits,
 int gsdh_generate_greedy(gsdh_model* m, const int* prompt, int n_prompt, int start_pos, int n_new,
                          int* tokens_out, float* margins_out);
 
+/* Batched projection for prefill on the matrix cores: Y[m][r] = (W x_m)[r] for
+ * the packed tensor (layer, slot) of the model and M tokens at once, kinks and
+ * rank-k terms included (each token's rank-k projection from its bf16 row).
+ * X: device bf16 [M][cols]; Y: device fp32 [M][rows]; asynchronous on the
+ * model stream (gsdh_stream_sync(gsdh_model_stream(m)) to wait).  The
+ * arithmetic is the fused matvec's (run_gpu_native_chat.py:196-267 /
+ * gsd_lq_cpu_engine.c:129-183) per token, with the token's (u, v) pair terms
+ * rounded once to fp16 (about 1e-4 relative).  No counterpart in the
+ * reference, which prefills token by token (run_gpu_native_chat.py:1128-1130).
+ * Grows its staging workspace with hipMalloc when M or cols exceed earlier
+ * calls (so a first call of a size is not graph-capturable). */
+int gsdh_model_matmul(gsdh_model* m, int layer, int slot, const uint16_t* X, int M, float* Y);
+
 /* Benchmark hook: runs the model's matvec launches of `layer` (mask bit i =
  * launch i of {qkv, o, gate+up, down}) on the model stream with the current
  * activations, without attention or synchronisation. */
