@@ -293,7 +293,10 @@ struct gsdh_model {
     StepState* st_host = nullptr;   // pinned
     int* gen_tok = nullptr;
     float* gen_margin = nullptr;
-    hipGraphExec_t g_full = nullptr, g_prefill = nullptr;
+    // per-token graphs: with and without the lm_head / argmax, for any
+    // position (split attention + merge) and for positions < kShortCtx (one
+    // attention block per KV head, no merge launch)
+    hipGraphExec_t g_full = nullptr, g_prefill = nullptr, g_full_s = nullptr, g_prefill_s = nullptr;
     hipGraph_t capture_graph = nullptr;
     size_t dev_bytes = 0;
     bool finalized = false;
@@ -390,7 +393,7 @@ int issue_linear(gsdh_model* m, int l, int mask) {
 }
 
 // The per-token launch sequence (run_gpu_native_chat.py:892-969, fused).
-int issue_token(gsdh_model* m, bool with_head) {
+int issue_token(gsdh_model* m, bool with_head, bool short_ctx) {
     const auto& c = m->c;
     m->pub_next = 0;
     HIPCHK(launch_embed(m->embed, &m->st->token, m->x, c.hidden, m->pub, m->pub_words, m->stream));
@@ -409,6 +412,10 @@ int issue_token(gsdh_model* m, bool with_head) {
         a.layer = l; a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.hd = c.head_dim; a.max_seq = c.max_seq_len;
         a.sm_scale = 1.0f / (float)std::sqrt((double)c.head_dim);
         a.chunk = m->chunk; a.max_splits = m->max_splits; a.ws = m->ws; a.counters = m->counters;
+        if (short_ctx) {   // positions < kShortCtx: one block per KV head
+            a.chunk = kShortCtx;
+            a.max_splits = 1;
+        }
         HIPCHK(launch_attention(a, m->stream));
         rc = issue_linear(m, l, 2 | 4 | 8);
         if (rc) return rc;
@@ -427,10 +434,15 @@ int issue_token(gsdh_model* m, bool with_head) {
     return 0;
 }
 
-int capture(gsdh_model* m, bool with_head, hipGraphExec_t* out) {
+hipGraphExec_t token_graph(const gsdh_model* m, bool with_head, int pos) {
+    if (pos < kShortCtx) return with_head ? m->g_full_s : m->g_prefill_s;
+    return with_head ? m->g_full : m->g_prefill;
+}
+
+int capture(gsdh_model* m, bool with_head, bool short_ctx, hipGraphExec_t* out) {
     hipGraph_t g = nullptr;
     HIPCHK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
-    int rc = issue_token(m, with_head);
+    int rc = issue_token(m, with_head, short_ctx);
     hipError_t e = hipStreamEndCapture(m->stream, &g);
     if (rc) {
         if (g) (void)hipGraphDestroy(g);
@@ -535,8 +547,8 @@ int gsdh_model_create(const gsdh_model_config* cfg, gsdh_model** out) {
 int gsdh_model_destroy(gsdh_model* m) {
     if (!m) return 0;
     if (m->stream) (void)hipStreamSynchronize(m->stream);
-    if (m->g_full) (void)hipGraphExecDestroy(m->g_full);
-    if (m->g_prefill) (void)hipGraphExecDestroy(m->g_prefill);
+    for (hipGraphExec_t g : {m->g_full, m->g_prefill, m->g_full_s, m->g_prefill_s})
+        if (g) (void)hipGraphExecDestroy(g);
     for (auto& t : m->hex)
         if (t.block) (void)hipFree(t.block);
     for (void* p : m->allocs) (void)hipFree(p);
@@ -657,8 +669,10 @@ int gsdh_model_finalize(gsdh_model* m) {
         for (int s = 0; s < 7; s++)
             if (!m->slot(l, s).set) return fail(-1, "finalize: layer %d slot %d not set", l, s);
     if (!m->slot(0, GSDH_LM_HEAD).set) return fail(-1, "finalize: lm_head not set");
-    int rc = capture(m, true, &m->g_full);
-    if (!rc) rc = capture(m, false, &m->g_prefill);
+    int rc = capture(m, true, false, &m->g_full);
+    if (!rc) rc = capture(m, false, false, &m->g_prefill);
+    if (!rc) rc = capture(m, true, true, &m->g_full_s);
+    if (!rc) rc = capture(m, false, true, &m->g_prefill_s);
     if (rc) return rc;
     m->finalized = true;
     return 0;
@@ -674,7 +688,7 @@ int gsdh_forward_token(gsdh_model* m, int token_id, int pos, int want_logits, fl
     *h = StepState{};
     h->token = token_id; h->pos = pos;
     HIPCHK(hipMemcpyAsync(m->st, h, sizeof(StepState), hipMemcpyHostToDevice, m->stream));
-    HIPCHK(hipGraphLaunch(want_logits ? m->g_full : m->g_prefill, m->stream));
+    HIPCHK(hipGraphLaunch(token_graph(m, want_logits != 0, pos), m->stream));
     if (want_logits && logits_host)
         HIPCHK(hipMemcpyAsync(logits_host, m->logits, (size_t)m->c.vocab * 4, hipMemcpyDeviceToHost, m->stream));
     HIPCHK(hipMemcpyAsync(m->st_host + 1, m->st, sizeof(StepState), hipMemcpyDeviceToHost, m->stream));
@@ -699,11 +713,13 @@ int gsdh_generate_greedy(gsdh_model* m, const int* prompt, int n_prompt, int sta
         ring[i] = StepState{};
         ring[i].token = prompt[i]; ring[i].pos = start_pos + i;
         hipError_t e = hipMemcpyAsync(m->st, &ring[i], sizeof(StepState), hipMemcpyHostToDevice, m->stream);
-        if (e == hipSuccess) e = hipGraphLaunch(i == n_prompt - 1 ? m->g_full : m->g_prefill, m->stream);
+        if (e == hipSuccess) e = hipGraphLaunch(token_graph(m, i == n_prompt - 1, start_pos + i), m->stream);
         if (e != hipSuccess) rc = fail((int)e, "generate prefill: %s", hipGetErrorString(e));
     }
     for (int i = 1; i < n_new && !rc; i++) {
-        hipError_t e = hipGraphLaunch(m->g_full, m->stream);
+        // the device advances the position: this launch runs the token at
+        // start_pos + n_prompt - 1 + i
+        hipError_t e = hipGraphLaunch(token_graph(m, true, start_pos + n_prompt - 1 + i), m->stream);
         if (e != hipSuccess) rc = fail((int)e, "generate decode: %s", hipGetErrorString(e));
     }
     if (!rc) {

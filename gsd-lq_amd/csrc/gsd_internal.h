@@ -127,6 +127,10 @@ hipError_t launch_swiglu(const float* g, const float* u, float* out, int dim, hi
 hipError_t launch_rope_kv(float* q, const float* k, const float* v, const RopeKV& r,
                           const float2* cs_inline, hipStream_t stream);
 
+// Contexts up to this length run attention as one block per KV head (the
+// score buffer of attn_kernel holds 256 positions).
+constexpr int kShortCtx = 256;
+
 struct AttnArgs {
     const float* q;
     const uint16_t* k_cache;

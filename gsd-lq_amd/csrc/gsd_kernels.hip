@@ -1843,6 +1843,9 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
 #undef GSD_ATTN_G
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    // one split (contexts up to `chunk`): the attention kernel writes the
+    // output itself and no merge launch is needed
+    if (a.max_splits <= 1) return hipSuccess;
     hipLaunchKernelGGL(attn_merge_kernel, dim3(a.n_heads), dim3(a.hd), 0, st, a);
     return hipGetLastError();
 }

@@ -92,6 +92,28 @@ def test_generate_greedy_matches_oracle():
     gpu.close()
 
 
+def test_decode_across_short_context_switch():
+    """Positions below 256 run one attention block per KV head (no merge
+    launch), later ones the split attention: decoding through the switch
+    matches the oracle token for token, and forward_token agrees on both
+    sides of it."""
+    banner("greedy decode across position 256")
+    gpu, ref = _models(_spec(mode="precision", kinks_per_row=1), max_seq=512)
+    rng = np.random.default_rng(20)     # smallest oracle margin 6e-3 over the 48 steps
+    prompt = rng.integers(0, gpu.vocab_size, 230).tolist()
+    toks, margins = gpu.generate_greedy(prompt, 48)
+    want, wm = ref.generate_greedy(prompt, 48)
+    assert toks == want
+    assert np.allclose(margins, wm, rtol=1e-2, atol=1e-4)
+    # rewrite positions 255 and 256, then the last generated token's position
+    # (the oracle's loop has already run it, the engine's need not) and 278
+    for pos in (255, 256, len(prompt) + 47, len(prompt) + 48):
+        a = gpu.forward_token(toks[0], pos)
+        b = ref.forward_token(toks[0], pos)
+        assert rel_l2(a, b) < 1e-3, pos
+    gpu.close()
+
+
 def test_model_rejects_invalid_codes():
     from gsdlq import synth
     import run_gpu_native_chat as chat
