@@ -24,18 +24,25 @@ def _spec(**kw):
     return synth.SynthSpec(**base)
 
 
-def _models(spec, max_seq=256, interleaved=1):
+ENGINES = ("persistent", "graph")
+
+
+def _models(spec, max_seq=256, interleaved=1, engine="graph"):
     from gsdlq import synth
     import run_gpu_native_chat as chat
     src = synth.SynthSource(spec)
     gpu = chat.GPUMistralV2Model(src, rope_interleaved=interleaved, max_seq_len=max_seq, verbose=False)
+    assert gpu.engine == "graph"
+    gpu.set_engine(engine)   # every model here qualifies for the one-launch token kernel
+    assert gpu.engine == engine
     ref = O.OracleModel(src, kind="port", max_seq_len=max_seq, rope_interleaved=interleaved)
     return gpu, ref
 
 
-def test_tiny_model_golden(golden):
-    banner("tiny model vs reference-engine golden")
-    gpu, _ = _models(_spec())
+@pytest.mark.parametrize("engine", ENGINES)
+def test_tiny_model_golden(golden, engine):
+    banner(f"tiny model vs reference-engine golden ({engine})")
+    gpu, _ = _models(_spec(), engine=engine)
     prompt = golden["tiny_prompt"].tolist()
     for pos, t in enumerate(prompt):
         lg = gpu.forward_token(t, pos)
@@ -51,15 +58,16 @@ def test_tiny_model_golden(golden):
     gpu.close()
 
 
+@pytest.mark.parametrize("engine", ENGINES)
 @pytest.mark.parametrize("mode,kpr,il,shape", [
     ("turbo", 0, 1, dict()),
     ("precision", 3, 1, dict()),
     ("precision", 0, 0, dict(n_heads=8, n_kv_heads=8, head_dim=32 * 2)),
     ("turbo", 1, 1, dict(n_layers=3, hidden=512, ffn=1344, n_heads=8, n_kv_heads=2, head_dim=128, vocab=1000)),
 ])
-def test_model_stepwise_vs_oracle(mode, kpr, il, shape):
-    banner(f"stepwise model {mode} kinks {kpr} interleaved {il} {shape}")
-    gpu, ref = _models(_spec(mode=mode, kinks_per_row=kpr, **shape), interleaved=il)
+def test_model_stepwise_vs_oracle(mode, kpr, il, shape, engine):
+    banner(f"stepwise model {mode} kinks {kpr} interleaved {il} {shape} ({engine})")
+    gpu, ref = _models(_spec(mode=mode, kinks_per_row=kpr, **shape), interleaved=il, engine=engine)
     rng = np.random.default_rng(3)
     toks = rng.integers(0, gpu.vocab_size, 40).tolist()
     for pos, t in enumerate(toks):
@@ -77,9 +85,10 @@ def test_model_stepwise_vs_oracle(mode, kpr, il, shape):
     gpu.close()
 
 
-def test_generate_greedy_matches_oracle():
-    banner("generate_greedy vs oracle")
-    gpu, ref = _models(_spec(mode="turbo", kinks_per_row=1))
+@pytest.mark.parametrize("engine", ENGINES)
+def test_generate_greedy_matches_oracle(engine):
+    banner(f"generate_greedy vs oracle ({engine})")
+    gpu, ref = _models(_spec(mode="turbo", kinks_per_row=1), engine=engine)
     prompt = [1, 5, 9, 200, 33, 2]
     toks, margins = gpu.generate_greedy(prompt, 24)
     want, wm = ref.generate_greedy(prompt, 24)
@@ -92,13 +101,15 @@ def test_generate_greedy_matches_oracle():
     gpu.close()
 
 
-def test_decode_across_short_context_switch():
-    """Positions below 256 run one attention block per KV head (no merge
-    launch), later ones the split attention: decoding through the switch
-    matches the oracle token for token, and forward_token agrees on both
-    sides of it."""
-    banner("greedy decode across position 256")
-    gpu, ref = _models(_spec(mode="precision", kinks_per_row=1), max_seq=512)
+@pytest.mark.parametrize("engine", ENGINES)
+def test_decode_across_short_context_switch(engine):
+    """Below 256 positions attention is one split (graph engine: one block per
+    KV head and no merge launch; persistent engine: one item per query head
+    and no merge step), later ones are split and merged: decoding through the
+    switch matches the oracle token for token, and forward_token agrees on
+    both sides of it."""
+    banner(f"greedy decode across position 256 ({engine})")
+    gpu, ref = _models(_spec(mode="precision", kinks_per_row=1), max_seq=512, engine=engine)
     rng = np.random.default_rng(20)     # smallest oracle margin 6e-3 over the 48 steps
     prompt = rng.integers(0, gpu.vocab_size, 230).tolist()
     toks, margins = gpu.generate_greedy(prompt, 48)
