@@ -838,11 +838,14 @@ __global__ void unpack_kernel(const uint8_t* codes, int64_t n, int R, int32_t* i
 // pair is one v_perm_b32 (LDS address of the lane's own copy of the codebook:
 // code << 8 | lane * 4, so the 64 lanes never share a bank).
 //
-// Work split: a block of W waves takes row-blocks (16 rows) in turn; its waves
-// split the 128-column chunks of a row-block (double-buffered 16-byte code
-// loads, one chunk in flight while the other is computed) and reduce through
-// LDS; wave 0's lanes 0-15 run the epilogue.  For the paired gate/up launch
-// the waves form two groups (gate row-block, up row-block of the same rows).
+// Work split: one block of W waves per CU takes row-blocks (16 rows) in turn;
+// its waves split the 128-column chunks of a row-block (16-byte code loads,
+// four chunks in flight per wave) and reduce through LDS; wave 0's lanes 0-15
+// run the epilogue.  For the paired gate/up launch the waves form two groups
+// (gate row-block, up row-block of the same rows).  A wave only ever reads
+// its own chunks of x, so it stages them itself (its own LDS region and
+// power-of-two prescale), and the RMSNorm factor multiplies the finished
+// sums: nothing waits for all of x before the weights stream.
 // ------------------------------------------------------------------------
 constexpr int kMv4MaxWaves = 16;
 
@@ -855,7 +858,7 @@ __device__ __forceinline__ float xnorm(const HexArgs& a, int c, float inv) {
 // Rank-k value `lead` of a launch (segments without tmp_k, in order):
 // S[j] * sum_c x'[c] * Vt[j][c] (gsd_lq_cpu_engine.c:110-127), published as
 // one 64-bit word 1 << 32 | float bits.
-__device__ void mv4_publish(const HexArgs& a, int lead, float* scratch) {
+__device__ __forceinline__ void mv4_publish(const HexArgs& a, int lead, float* scratch) {
     int g = 0, jj = lead;
     for (; g < a.nseg; g++) {
         const int k = a.seg[g].tmp_k ? 0 : a.seg[g].k;
@@ -883,16 +886,41 @@ __device__ void mv4_publish(const HexArgs& a, int lead, float* scratch) {
 // TB > 0: every segment uses the same codebook of TB points, held at a
 // static LDS address; TB == 0: per-segment codebooks in dynamic LDS.
 template <int TB>
-__global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(8))) hexmv4_kernel(const HexArgs a) {
+__global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) hexmv4_kernel(const HexArgs a) {
     __shared__ __attribute__((aligned(16))) uint32_t stab[TB > 0 ? TB * 64 : 1];
     __shared__ float red[2][kMv4MaxWaves][16];
     __shared__ float tkl[kMaxSeg][kMaxRank];
     __shared__ float scratch[32];
+    __shared__ float ssq[kMv4MaxWaves];   // sum of x^2 over each wave's columns
     extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
 
-    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, NW = (int)(blockDim.x >> 6);
+    // wid in a scalar register: the segment selections below (seg_of) then
+    // read the kernel arguments with scalar loads; a per-lane index makes
+    // them vector loads whose vmcnt wait drains the code loads in flight
+    const int tid = threadIdx.x, lane = tid & 63, NW = (int)(blockDim.x >> 6);
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nc = (a.cols + 127) >> 7;
     const bool paired = a.epilogue == kEpiSwiGLU;
+    // segment g of the arguments, indexed in the kernel-argument segment (a
+    // select chain over a.seg[0..2] becomes an indexed private copy of the
+    // whole argument block)
+    using KSeg = const __attribute__((address_space(4))) HexSeg;
+    using KArgs = const __attribute__((address_space(4))) HexArgs;
+    KArgs* kargs = (KArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+    __asm__ volatile("" : "+s"(kargs));
+    KSeg* kseg = kargs->seg;
+    {
+        // one round trip brings every 64-byte line of the arguments into the
+        // scalar cache; the reads below, which depend on each other, then hit
+        // instead of missing one after another
+        using KW = const __attribute__((address_space(4))) uint32_t;
+        KW* kw = reinterpret_cast<KW*>(kargs);
+        static_assert(sizeof(HexArgs) <= 10 * 64, "argument lines touched below");
+        uint32_t t0 = kw[0], t1 = kw[16], t2 = kw[32], t3 = kw[48], t4 = kw[64];
+        uint32_t t5 = kw[80], t6 = kw[96], t7 = kw[112], t8 = kw[128];
+        uint32_t t9 = kw[(sizeof(HexArgs) - 4) / 4];
+        __asm__ volatile("" ::"s"(t0), "s"(t1), "s"(t2), "s"(t3), "s"(t4), "s"(t5), "s"(t6), "s"(t7), "s"(t8), "s"(t9));
+    }
     const int G = paired ? 2 : 1, WR = NW / G, grp = wid / WR, wr = wid - grp * WR;
 
     // rank-k publishing blocks first
@@ -921,12 +949,11 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(8))) 
     const int toff2 = TB == 0 && a.nseg > 1 ? toff1 + a.seg[1].n_pts * 256 : toff1;
     const int tab_bytes = TB == 0 && a.nseg > 2 ? toff2 + a.seg[2].n_pts * 256 : toff2;
     auto toff = [&](int g) { return g == 0 ? 0 : (g == 1 ? toff1 : toff2); };
-    uint4* X = reinterpret_cast<uint4*>(dyn + tab_bytes);
 
     // this wave's steps: P chunks (wr, wr + WR, ...) of each of the block's
     // units in turn (units u0, u0 + nblk, ...); P is the same for every wave
     // (WR divides nc), so unit ends, and their barriers, fall on the same step
-    // in all waves.  The load cursor runs two steps ahead of the compute
+    // in all waves.  The load cursor runs four steps ahead of the compute
     // cursor; both advance by compare-and-reset, and per-unit base pointers
     // are recomputed only when a unit starts.  Past the last unit the load
     // cursor stays on the last unit (valid addresses, unused data).
@@ -941,9 +968,8 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(8))) 
         const int uu = min(u0 + k * nblk, nunits - 1);
         const int g = seg_of(uu);
         const int rb = paired ? uu : uu - ubase(g);
-        const HexSeg& sg = g == 0 ? a.seg[0] : (g == 1 ? a.seg[1] : a.seg[2]);
-        lcb = sg.codes_t + (size_t)rb * nc * 64;
-        lsb = sg.scales_t + (size_t)rb * nc * 16;
+        lcb = kseg[g].codes_t + (size_t)rb * nc * 64;
+        lsb = kseg[g].scales_t + (size_t)rb * nc * 16;
     };
     auto lissue = [&](uint4& cw, uint32_t& sw) {
         const int c = wr + lj * WR;
@@ -955,138 +981,144 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(8))) 
         }
     };
 
-    // prologue loads in the order they are needed: x (and the norm
-    // weights) first, then the first chunk of codes (HBM), so waiting for x
-    // never waits behind the codes
-    constexpr int XPT = 4, WPT = 1;   // float4 of x / norm weights held in registers
-    const int nq = a.cols >> 2;
-    float4 xq[XPT], wq[WPT];
+    // Each wave stages only its own columns of x (chunks wr + p * WR,
+    // p < P) as the MFMA A operand, in a region of LDS no other wave reads:
+    // no barrier waits for x, and the weights stream from the first
+    // instructions on.  The RMSNorm factor is applied to the finished dot
+    // products: y = inv * (W (x * w)), the sums of x^2 of the group's waves
+    // meeting in LDS by the first unit end.
+    // uniform values that no launch writes while it runs (the position, the
+    // codebook fields) are read through the constant address space: scalar
+    // loads, which never wait behind the vector loads of the codes
+    using KI32 = const __attribute__((address_space(4))) int;
+    using KU32 = const __attribute__((address_space(4))) uint32_t;
+    const int rpos = a.epilogue == kEpiRopeKV ? (a.rope.pos_dev ? *(KI32*)a.rope.pos_dev : a.rope.pos) : 0;
+    uint32_t* X32 = reinterpret_cast<uint32_t*>(dyn + tab_bytes) + (size_t)wid * P * 128;
+    const uint4* Xw = reinterpret_cast<const uint4*>(X32);
+    constexpr int kXP = 8;   // chunks of x per batch of loads
+    float2 xv[kXP], wv[kXP];
+    auto xload = [&](int p0) {
 #pragma unroll
-    for (int i = 0; i < XPT; i++) {
-        const int q = tid + i * (int)blockDim.x;
-        xq[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (i < WPT) wq[i] = make_float4(1.f, 1.f, 1.f, 1.f);
-        if (q < nq) {
-            xq[i] = reinterpret_cast<const float4*>(a.x)[q];
-            if (i < WPT && a.norm_w) wq[i] = reinterpret_cast<const float4*>(a.norm_w)[q];
+        for (int i = 0; i < kXP; i++) {
+            const int p = p0 + i, col = (wr + p * WR) * 128 + 2 * lane;
+            xv[i] = make_float2(0.f, 0.f);
+            wv[i] = make_float2(1.f, 1.f);
+            if (p < P && col < a.cols) {
+                xv[i] = *reinterpret_cast<const float2*>(a.x + col);
+                if (a.norm_w) wv[i] = *reinterpret_cast<const float2*>(a.norm_w + col);
+            }
         }
-    }
-    auto xw = [&](int i, int q, float4& xv, float4& wv) {   // x and w of float4 q = tid + i * blockDim
-        xv = i < XPT ? xq[i] : reinterpret_cast<const float4*>(a.x)[q];
-        if (i < WPT) wv = wq[i];
-        else wv = a.norm_w ? reinterpret_cast<const float4*>(a.norm_w)[q] : make_float4(1.f, 1.f, 1.f, 1.f);
     };
+    // pair `lane` of local chunk p: (u, v) = (xa wa, xa wa / 2 + xb wb sqrt(3)/2)
+    // at dword (((p * 2 + h) * 2 + t) * 4 + g) * 8 + e, and + 4 for the low
+    // part (the A-operand order read by step())
+    constexpr float kS32 = 0.866025403784438646763723170752936183f;
+    const int xoff = ((((lane >> 5) & 1) * 2 + ((lane >> 2) & 1)) * 4 + ((lane >> 3) & 3)) * 8 + (lane & 3);
+    float ss = 0.f, mx = 0.f;
+    auto xfirst = [&](int p0) {   // fp32 (u, v) in place, sum x^2, max |u|, |v|
+#pragma unroll
+        for (int i = 0; i < kXP; i++) {
+            const int p = p0 + i;
+            if (p < P) {
+                ss = fmaf(xv[i].x, xv[i].x, ss);
+                ss = fmaf(xv[i].y, xv[i].y, ss);
+                const float xa = xv[i].x * wv[i].x, xb = xv[i].y * wv[i].y;
+                const float u = xa, v = fmaf(kS32, xb, 0.5f * xa);
+                mx = fmaxf(mx, fmaxf(fabsf(u), fabsf(v)));
+                X32[p * 128 + xoff] = __float_as_uint(u);
+                X32[p * 128 + xoff + 4] = __float_as_uint(v);
+            }
+        }
+    };
+
+    // this wave's first steps (see the main loop) go out right behind its x:
+    // the segment pointers come from scalar loads of the kernel arguments,
+    // and vector loads complete in issue order, so the wait for x does not
+    // wait for the codes, whose latency overlaps that of x
+    xload(0);
+    uint4 cw0, cw1, cw2, cw3;
+    uint32_t sw0, sw1, sw2, sw3;
+    lset(0);
+    lissue(cw0, sw0);
+    lissue(cw1, sw1);
+    lissue(cw2, sw2);
+    lissue(cw3, sw3);
+
     // codebook copies: entry e of lane l at byte e * 256 + l * 4.  Wave w
     // writes entries 16w .. 16w + 15 (waves 16 apart when fewer than 16
     // waves cover the table); their fields come in one 64-byte scalar read
     // (the field tables are padded to 256 entries)
     uint32_t fv[16];
-    const int wid_u = __builtin_amdgcn_readfirstlane(wid);
-    if (TB > 0 && wid_u * 16 < TB) {
-        const uint32_t* fp = a.seg[0].fields + wid_u * 16;
+    if (TB > 0 && wid * 16 < TB) {
+        KU32* fp = (KU32*)a.seg[0].fields + wid * 16;
 #pragma unroll
         for (int j = 0; j < 16; j++) fv[j] = fp[j];
     }
-    uint4 cA, cB;
-    uint32_t sA, sB;
     if (TB > 0) {
-        if (wid_u * 16 < TB) {
+        if (wid * 16 < TB) {
 #pragma unroll
             for (int j = 0; j < 16; j++)
-                if (wid_u * 16 + j < TB) stab[(wid_u * 16 + j) * 64 + lane] = fv[j];
+                if (wid * 16 + j < TB) stab[(wid * 16 + j) * 64 + lane] = fv[j];
         }
         // fewer than TB / 16 waves: the remaining slices, one entry at a time
-        const uint32_t* f = a.seg[0].fields;
+        KU32* f = (KU32*)a.seg[0].fields;
         for (int e = NW * 16 + wid; e < TB; e += NW) stab[e * 64 + lane] = f[e];
     } else {
         for (int g = 0; g < a.nseg; g++) {
             uint32_t* t = reinterpret_cast<uint32_t*>(dyn + toff(g));
-            const uint32_t* f = a.seg[g].fields;
-            for (int e = wid; e < a.seg[g].n_pts; e += NW) t[e * 64 + lane] = f[e];
+            KU32* f = (KU32*)kseg[g].fields;
+            for (int e = wid; e < kseg[g].n_pts; e += NW) t[e * 64 + lane] = f[e];
         }
     }
-
-    // x' = (x * inv) * w (gsd_lq_cpu_engine.c:66-82), then (u, v) * 2^e as
-    // fp16 hi / lo in the A-operand order X[c][h][t][g][m].  One pass gives
-    // sum x^2 and max |x w|, |x_a w_a / 2 + s x_b w_b| (times inv: the
-    // largest |u|, |v| up to rounding), reduced together.
-    constexpr float kS32 = 0.866025403784438646763723170752936183f;
-    float ss = 0.f, mx = 0.f;
-    for (int i = 0; i < (nq + (int)blockDim.x - 1) / (int)blockDim.x; i++) {
-        const int q = tid + i * (int)blockDim.x;
-        if (q >= nq) break;
-        float4 xv, wv;
-        xw(i, q, xv, wv);
-        ss = fmaf(xv.x, xv.x, ss); ss = fmaf(xv.y, xv.y, ss); ss = fmaf(xv.z, xv.z, ss); ss = fmaf(xv.w, xv.w, ss);
-        const float p0 = xv.x * wv.x, p1 = xv.y * wv.y, p2 = xv.z * wv.z, p3 = xv.w * wv.w;
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(p0), fabsf(fmaf(kS32, p1, 0.5f * p0))),
-                             fmaxf(fabsf(p2), fabsf(fmaf(kS32, p3, 0.5f * p2)))));
+    unsigned have = 0;   // epilogue lanes: rank-k values of segment g fetched
+    using KF32 = const __attribute__((address_space(4))) float;
+    for (int g = 0; g < a.nseg; g++) {
+        if (kseg[g].k > 0 && kseg[g].tmp_k) {
+            for (int j = 0; j < kseg[g].k; j++) {   // uniform index: scalar loads
+                const float v = ((KF32*)kseg[g].tmp_k)[j];
+                if (wid == 0 && lane == 0) tkl[g][j] = v;
+            }
+            have |= 1u << g;
+        }
     }
-    // this wave's first two steps (see the main loop) go out once its x and
-    // codebook reads are back: x was written by the previous launch, possibly
-    // on another XCD, and its reads share the fabric with the code stream
-    lset(0);
-    lissue(cA, sA);
-    lissue(cB, sB);
+    // the only barrier before the first step: the codebook (and tkl)
+    lds_barrier();
+
+    xfirst(0);
+    for (int p0 = kXP; p0 < P; p0 += kXP) {   // more than kXP chunks per wave
+        xload(p0);
+        xfirst(p0);
+    }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
         ss += __shfl_xor(ss, o, 64);
         mx = fmaxf(mx, __shfl_xor(mx, o, 64));
     }
-    if (lane == 0) {
-        scratch[wid] = ss;
-        scratch[16 + wid] = mx;
-    }
-    lds_barrier();
-    ss = 0.f;
-    mx = 0.f;
-    for (int w = 0; w < NW; w++) {
-        ss += scratch[w];
-        mx = fmaxf(mx, scratch[16 + w]);
-    }
-    const float inv = a.norm_w ? 1.0f / sqrtf(ss / (float)a.cols + a.eps) : 1.f;
-    mx *= inv;
-    // power-of-two scale putting the largest |u|, |v| near [2^13, 2^14)
+    if (lane == 0) ssq[wid] = ss;
+    // power-of-two scale putting the wave's largest |u|, |v| near
+    // [2^13, 2^14): fp16 high and low parts then hold them to 2^-22
     int ex = 0;
     if (mx > 0.f && mx < INFINITY) (void)frexpf(mx, &ex);
     const float up = ldexpf(1.f, 14 - ex), down = ldexpf(1.f, ex - 14);
-    uint32_t* X32 = reinterpret_cast<uint32_t*>(X);
-    auto put = [&](int p, float xa, float xb) {   // pair p of the padded row
-        const float uu = xa * up, vv = fmaf(kS32, xb, 0.5f * xa) * up;
+    for (int p = 0; p < P; p++) {
+        const float uu = __uint_as_float(X32[p * 128 + xoff]) * up;
+        const float vv = __uint_as_float(X32[p * 128 + xoff + 4]) * up;
         const _Float16 uh = (_Float16)uu, vh = (_Float16)vv;
         const _Float16 ul = (_Float16)(uu - (float)uh), vl = (_Float16)(vv - (float)vh);
-        const int c = p >> 6, h = (p >> 5) & 1, g = (p >> 3) & 3, t = (p >> 2) & 1, e = p & 3;
-        const int base = ((((c * 2 + h) * 2 + t) * 4 + g) * 2) * 4 + e;
-        X32[base] = (uint32_t)__builtin_bit_cast(uint16_t, uh) | ((uint32_t)__builtin_bit_cast(uint16_t, vh) << 16);
-        X32[base + 4] = (uint32_t)__builtin_bit_cast(uint16_t, ul) | ((uint32_t)__builtin_bit_cast(uint16_t, vl) << 16);
-    };
-    for (int i = 0; i < (nq + (int)blockDim.x - 1) / (int)blockDim.x; i++) {
-        const int q = tid + i * (int)blockDim.x;
-        if (q >= nq) break;
-        float4 xv, wv;
-        xw(i, q, xv, wv);
-        if (a.norm_w) {
-            xv.x = (xv.x * inv) * wv.x; xv.y = (xv.y * inv) * wv.y;
-            xv.z = (xv.z * inv) * wv.z; xv.w = (xv.w * inv) * wv.w;
-        }
-        put(2 * q, xv.x, xv.y);
-        put(2 * q + 1, xv.z, xv.w);
+        X32[p * 128 + xoff] = (uint32_t)__builtin_bit_cast(uint16_t, uh) | ((uint32_t)__builtin_bit_cast(uint16_t, vh) << 16);
+        X32[p * 128 + xoff + 4] = (uint32_t)__builtin_bit_cast(uint16_t, ul) | ((uint32_t)__builtin_bit_cast(uint16_t, vl) << 16);
     }
-    for (int p = (a.cols >> 1) + tid; p < nc * 64; p += blockDim.x) put(p, 0.f, 0.f);   // padding
-    unsigned have = 0;   // epilogue lanes: rank-k values of segment g fetched
-    for (int g = 0; g < a.nseg; g++) {
-        if (a.seg[g].k > 0 && a.seg[g].tmp_k) {
-            if (tid < a.seg[g].k) tkl[g][tid] = a.seg[g].tmp_k[tid];
-            have |= 1u << g;
-        }
-    }
-    lds_barrier();
 
     const uint32_t lane_off = (uint32_t)lane * 4u;
     const int m = lane & 15, lg = lane >> 4;
-    auto step = [&](int g, int c, const uint4 cw, const uint32_t sw, float& acc) {
+    auto step = [&](int g, int p, const uint4 cw, const uint32_t sw, float& acc) {   // local chunk p
         const unsigned char* tb = TB > 0 ? reinterpret_cast<const unsigned char*>(stab) : dyn + toff(g);
         const uint32_t w4[4] = {cw.x, cw.y, cw.z, cw.w};
+        // the block scales leave sw before the step's loads are reissued
+        // (sw dead early: its next load lands in place instead of in a copy
+        // whose move at the loop end would wait for every load in flight)
+        float sc[2] = {h2f((uint16_t)(sw & 0xFFFFu)), h2f((uint16_t)(sw >> 16))};
+        __asm__ volatile("" : "+v"(sc[0]), "+v"(sc[1]));
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             float4v d = {0.f, 0.f, 0.f, 0.f};
@@ -1094,7 +1126,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(8))) 
             for (int t = 0; t < 2; t++) {
                 // rows m >= 2 of A only feed rows m >= 2 of D, which are never
                 // read: every lane loads row m & 1 (no masking, no zeroing)
-                const uint4 xv = X[(((c * 2 + h) * 2 + t) * 4 + lg) * 2 + (m & 1)];
+                const uint4 xv = Xw[(((p * 2 + h) * 2 + t) * 4 + lg) * 2 + (m & 1)];
                 u32x4v aw;
                 aw[0] = xv.x; aw[1] = xv.y; aw[2] = xv.z; aw[3] = xv.w;
                 const uint32_t w = w4[2 * h + t];
@@ -1107,20 +1139,17 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(8))) 
                 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, aw), __builtin_bit_cast(half8v, bw),
                                                           d, 0, 0, 0);
             }
-            const uint16_t sh = (uint16_t)(h ? (sw >> 16) : (sw & 0xFFFFu));
-            acc = fmaf(d[0] + d[1], h2f(sh), acc);
+            acc = fmaf(d[0] + d[1], sc[h], acc);
         }
     };
 
-    const int rpos = a.epilogue == kEpiRopeKV ? (a.rope.pos_dev ? *a.rope.pos_dev : a.rope.pos) : 0;
     float pre = 0.f;                       // epilogue inputs of the current unit,
     float2 pcs = make_float2(1.f, 0.f);    // fetched when the unit starts
     auto prefetch = [&](int uu) {
         if (wid == 0 && lane < 16 && uu < nunits) {
             const int g = seg_of(uu);
-            const HexSeg& sp = g == 0 ? a.seg[0] : (g == 1 ? a.seg[1] : a.seg[2]);
             const int prow = (paired ? uu : uu - ubase(g)) * 16 + lane;
-            if (prow < sp.rows) {
+            if (prow < kseg[g].rows) {
                 if (a.epilogue == kEpiResidual) pre = a.resid[prow];
                 if (a.epilogue == kEpiRopeKV && g != 2)
                     pcs = a.rope.cs[(size_t)rpos * (a.rope.hd >> 1) + ((prow % a.rope.hd) >> 1)];
@@ -1130,21 +1159,29 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(8))) 
     int rbuf = 0;
     auto unit_end = [&](int u, float& acc) {
         const int g = seg_of(u);
-        if (lane < 16) red[rbuf][wid][lane] = acc;
+        if (lane < 16) red[rbuf][wid][lane] = acc * down;
         acc = 0.f;
         lds_barrier();
         if (wid == 0 && lane < 16) {
+            // RMSNorm factor of x (gsd_lq_cpu_engine.c:66-82) from the sums of
+            // the first group's waves, which cover every column once
+            float inv = 1.f;
+            if (a.norm_w) {
+                float sx = 0.f;
+                for (int w = 0; w < WR; w++) sx += ssq[w];
+                inv = 1.0f / sqrtf(sx / (float)a.cols + a.eps);
+            }
             float fin0 = 0.f, fin1 = 0.f;
 #pragma unroll
             for (int gi = 0; gi < 2; gi++) {
                 if (gi >= G) break;
                 const int sg_i = paired ? gi : g;
-                const HexSeg& sg = sg_i == 0 ? a.seg[0] : (sg_i == 1 ? a.seg[1] : a.seg[2]);
+                KSeg& sg = kseg[sg_i];
                 const int rb = paired ? u : u - ubase(sg_i);
                 const int row = rb * 16 + lane;
                 float t = 0.f;
                 for (int w = 0; w < WR; w++) t += red[rbuf][gi * WR + w][lane];
-                t *= down;
+                t *= inv;
                 if (row < sg.rows) {
                     if (sg.row_ptr) {
                         const uint32_t e = sg.row_ptr[row + 1];
@@ -1177,7 +1214,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(8))) 
                 if (gi == 0) fin0 = t;
                 else fin1 = t;
             }
-            const HexSeg& s0 = paired ? a.seg[0] : (g == 0 ? a.seg[0] : (g == 1 ? a.seg[1] : a.seg[2]));
+            KSeg& s0 = kseg[paired ? 0 : g];
             const int row = (paired ? u : u - ubase(g)) * 16 + lane;
             if (paired) {
                 if (row < s0.rows) s0.out[row] = (fin0 / (1.0f + expf(-fin0))) * fin1;
@@ -1224,16 +1261,22 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(8))) 
             cg = seg_of(min(cu, nunits - 1));
         }
     };
-    // two steps in flight at all times: buffer A holds the even steps, B the
-    // odd ones; every load is issued (the cursor clamps past the end), and the
-    // odd half of the last pair may compute a step past the end that no unit
-    // end collects
-    for (int s = 0; s < nsteps; s += 2) {
-        step(cg, wr + cj * WR, cA, sA, acc);
-        lissue(cA, sA);
+    // four steps in flight at all times: buffer i holds the steps s with
+    // s % 4 == i; every load is issued (the cursor clamps past the end), and
+    // the last group of four may compute up to three steps past the end that
+    // no unit end collects
+    for (int s = 0; s < nsteps; s += 4) {
+        step(cg, cj, cw0, sw0, acc);
+        lissue(cw0, sw0);
         cadvance();
-        step(cg, wr + cj * WR, cB, sB, acc);
-        lissue(cB, sB);
+        step(cg, cj, cw1, sw1, acc);
+        lissue(cw1, sw1);
+        cadvance();
+        step(cg, cj, cw2, sw2, acc);
+        lissue(cw2, sw2);
+        cadvance();
+        step(cg, cj, cw3, sw3, acc);
+        lissue(cw3, sw3);
         cadvance();
     }
 }
@@ -1541,10 +1584,11 @@ hipError_t launch_hexmv4_t(const HexArgs& a, hipStream_t st, int nw, size_t lds,
         return hipErrorInvalidConfiguration;
     per_cu = n;
     const int ncu = device_cu_count() > 0 ? device_cu_count() : 256;
-    int grid = ncu * per_cu;
+    // publishing blocks first (dispatched in order, they are resident before
+    // any matvec block waits on them), and all blocks resident at once
+    int grid = ncu * per_cu - nlead;
+    if (grid < 1) grid = 1;
     if (grid > nunits) grid = nunits;
-    // publishing blocks first: dispatched in order, they are resident before
-    // any matvec block waits on them
     hipLaunchKernelGGL((hexmv4_kernel<TB>), dim3(grid + nlead), dim3(nw * 64), lds, st, a);
     return hipGetLastError();
 }
@@ -1576,7 +1620,7 @@ hipError_t launch_hexmv4(const HexArgs& a, hipStream_t st) {
     int wr = kMv4MaxWaves / G;
     while (wr > 1 && nc % wr != 0) wr >>= 1;
     const int nw = wr * G;
-    const size_t xbytes = (size_t)nc * 512;
+    const size_t xbytes = (size_t)G * nc * 512;   // every wave's own chunks of x
     if (shared && a.seg[0].n_pts == 217) return launch_hexmv4_t<217>(a, st, nw, xbytes, nunits, nlead);
     if (shared && a.seg[0].n_pts == 127) return launch_hexmv4_t<127>(a, st, nw, xbytes, nunits, nlead);
     return launch_hexmv4_t<0>(a, st, nw, xbytes + (size_t)tab_bytes, nunits, nlead);
