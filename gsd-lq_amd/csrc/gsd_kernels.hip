@@ -848,6 +848,9 @@ __global__ void unpack_kernel(const uint8_t* codes, int64_t n, int R, int32_t* i
 // sums: nothing waits for all of x before the weights stream.
 // ------------------------------------------------------------------------
 constexpr int kMv4MaxWaves = 16;
+// code steps (1 KB per wave each) in flight per wave: a CU streams about
+// (16 waves x depth KB) per load latency, so the depth sets its share of HBM
+constexpr int kMv4Depth = 4;
 
 // x'[c] of the launch (RMSNorm applied when norm_w is set), as the reference
 // forms it: (x * inv) * w.
@@ -897,10 +900,8 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     // wid in a scalar register: the segment selections below (seg_of) then
     // read the kernel arguments with scalar loads; a per-lane index makes
     // them vector loads whose vmcnt wait drains the code loads in flight
-    const int tid = threadIdx.x, lane = tid & 63, NW = (int)(blockDim.x >> 6);
+    const int tid = threadIdx.x, lane = tid & 63;
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int nc = (a.cols + 127) >> 7;
-    const bool paired = a.epilogue == kEpiSwiGLU;
     // segment g of the arguments, indexed in the kernel-argument segment (a
     // select chain over a.seg[0..2] becomes an indexed private copy of the
     // whole argument block)
@@ -910,17 +911,27 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     __asm__ volatile("" : "+s"(kargs));
     KSeg* kseg = kargs->seg;
     {
-        // one round trip brings every 64-byte line of the arguments into the
-        // scalar cache; the reads below, which depend on each other, then hit
-        // instead of missing one after another
+        // one round trip, before any other read of the arguments, brings
+        // every 64-byte line of them into the scalar cache; the reads below,
+        // which depend on each other, then hit instead of missing one after
+        // another
         using KW = const __attribute__((address_space(4))) uint32_t;
         KW* kw = reinterpret_cast<KW*>(kargs);
         static_assert(sizeof(HexArgs) <= 10 * 64, "argument lines touched below");
         uint32_t t0 = kw[0], t1 = kw[16], t2 = kw[32], t3 = kw[48], t4 = kw[64];
         uint32_t t5 = kw[80], t6 = kw[96], t7 = kw[112], t8 = kw[128];
         uint32_t t9 = kw[(sizeof(HexArgs) - 4) / 4];
-        __asm__ volatile("" ::"s"(t0), "s"(t1), "s"(t2), "s"(t3), "s"(t4), "s"(t5), "s"(t6), "s"(t7), "s"(t8), "s"(t9));
+        __asm__ volatile("" ::"s"(t0), "s"(t1), "s"(t2), "s"(t3), "s"(t4), "s"(t5), "s"(t6), "s"(t7), "s"(t8), "s"(t9)
+                         : "memory");
     }
+    // (argument values used right away pass through an asm placed after the
+    // batch, so nothing waits for them before the batch is out)
+    unsigned bdim = blockDim.x;
+    int cols0 = a.cols, epi0 = a.epilogue;
+    __asm__ volatile("" : "+s"(bdim), "+s"(cols0), "+s"(epi0));
+    const int NW = (int)(bdim >> 6);
+    const int nc = (cols0 + 127) >> 7;
+    const bool paired = epi0 == kEpiSwiGLU;
     const int G = paired ? 2 : 1, WR = NW / G, grp = wid / WR, wr = wid - grp * WR;
 
     // rank-k publishing blocks first
@@ -953,10 +964,12 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     // this wave's steps: P chunks (wr, wr + WR, ...) of each of the block's
     // units in turn (units u0, u0 + nblk, ...); P is the same for every wave
     // (WR divides nc), so unit ends, and their barriers, fall on the same step
-    // in all waves.  The load cursor runs four steps ahead of the compute
+    // in all waves.  The load cursor runs kMv4Depth steps ahead of the compute
     // cursor; both advance by compare-and-reset, and per-unit base pointers
-    // are recomputed only when a unit starts.  Past the last unit the load
-    // cursor stays on the last unit (valid addresses, unused data).
+    // are recomputed only when a unit starts.  Past the block's last unit
+    // the load cursor stays on that unit (valid addresses, unused data,
+    // lines the block has just read: a shared unit there would have every
+    // block's surplus loads meet on the same few HBM channels).
     const int P = nc / WR;   // >= 1
     const int u0 = (int)blockIdx.x - nlead;
     const int my_units = u0 < nunits ? (nunits - 1 - u0) / nblk + 1 : 0;
@@ -965,7 +978,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     const uint4* lcb = nullptr;
     const uint32_t* lsb = nullptr;
     auto lset = [&](int k) {
-        const int uu = min(u0 + k * nblk, nunits - 1);
+        const int uu = min(u0 + min(k, max(my_units - 1, 0)) * nblk, nunits - 1);
         const int g = seg_of(uu);
         const int rb = paired ? uu : uu - ubase(g);
         lcb = kseg[g].codes_t + (size_t)rb * nc * 64;
@@ -1036,13 +1049,11 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     // and vector loads complete in issue order, so the wait for x does not
     // wait for the codes, whose latency overlaps that of x
     xload(0);
-    uint4 cw0, cw1, cw2, cw3;
-    uint32_t sw0, sw1, sw2, sw3;
+    uint4 cw[kMv4Depth];
+    uint32_t sw[kMv4Depth];
     lset(0);
-    lissue(cw0, sw0);
-    lissue(cw1, sw1);
-    lissue(cw2, sw2);
-    lissue(cw3, sw3);
+#pragma unroll
+    for (int i = 0; i < kMv4Depth; i++) lissue(cw[i], sw[i]);
 
     // codebook copies: entry e of lane l at byte e * 256 + l * 4.  Wave w
     // writes entries 16w .. 16w + 15 (waves 16 apart when fewer than 16
@@ -1261,23 +1272,17 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
             cg = seg_of(min(cu, nunits - 1));
         }
     };
-    // four steps in flight at all times: buffer i holds the steps s with
-    // s % 4 == i; every load is issued (the cursor clamps past the end), and
-    // the last group of four may compute up to three steps past the end that
-    // no unit end collects
-    for (int s = 0; s < nsteps; s += 4) {
-        step(cg, cj, cw0, sw0, acc);
-        lissue(cw0, sw0);
-        cadvance();
-        step(cg, cj, cw1, sw1, acc);
-        lissue(cw1, sw1);
-        cadvance();
-        step(cg, cj, cw2, sw2, acc);
-        lissue(cw2, sw2);
-        cadvance();
-        step(cg, cj, cw3, sw3, acc);
-        lissue(cw3, sw3);
-        cadvance();
+    // kMv4Depth steps in flight at all times: buffer i holds the steps s
+    // with s % kMv4Depth == i; every load is issued (the cursor clamps past
+    // the end), and the last group may compute steps past the end that no
+    // unit end collects
+    for (int s = 0; s < nsteps; s += kMv4Depth) {
+#pragma unroll
+        for (int i = 0; i < kMv4Depth; i++) {
+            step(cg, cj, cw[i], sw[i], acc);
+            lissue(cw[i], sw[i]);
+            cadvance();
+        }
     }
 }
 
