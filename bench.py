@@ -15,8 +15,10 @@ factors + x (4 B/col) + y (4 B/row), each stream counted once.
 
 Also reported: the same for Precision mode (radius 6, rank 2; the file's u8
 codes), the dominant kernel's roofline (the fused gate/up launch, 2 x
-14336x4096), end-to-end greedy decode tok/s of a 32-layer 7B-shaped model,
-and the reference CPU engine timed on this host's cores on a bounded sample.
+14336x4096), decode attention with RoPE + K/V append at contexts 512 / 2048 /
+8192 (GB/s of K/V cache read), end-to-end greedy decode tok/s of a 32-layer
+7B-shaped model, and the reference CPU engine timed on this host's cores on a
+bounded sample.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3]
 """
@@ -284,6 +286,78 @@ def probe(kind: str, n: int):
     model.close()
 
 
+def bench_attention(ctxs=(512, 2048, 8192), reps=20):
+    """Decode attention with K/V append (32 query heads, 8 KV heads, head dim
+    128, RoPE theta 1e6) at contexts 512 / 2048 / 8192: per layer one RoPE +
+    fp16 K/V append at pos = ctx - 1 (gsdh_rope_and_store_kv) and one split
+    attention over the fp16 cache filled to ctx - 1 (gsdh_gqa_attention),
+    the engine's own kernels (gsd_lq_cpu_engine.c:185-330 computes the same).
+    Enough layers are rotated that the caches exceed 512 MB (beyond the
+    Infinity Cache); the launches of all layers are captured in one graph on
+    the stream of a small model context and timed with HIP events there.
+    Algorithmic bytes per layer: K + V read (ctx * 8 * 128 * 2 * 2) + the
+    4096-byte append + q and the output (2 * 4 * 4096)."""
+    import run_gpu_native_chat as chat
+    from gsdlq import hip, synth
+    n_heads, n_kv, hd, theta = 32, 8, 128, 1.0e6
+    sm_scale = float(1.0 / np.sqrt(hd))
+    # a small model context: its stream, graph capture and event timing
+    spec = synth.SynthSpec(n_layers=1, hidden=256, ffn=512, n_heads=4, n_kv_heads=2, head_dim=64, vocab=256,
+                           mode="turbo")
+    model = chat.GPUMistralV2Model(synth.SynthSource(spec), max_seq_len=16, verbose=False)
+    lib = model.cl.lib
+    sp = ctypes.c_void_p(lib.gsdh_model_stream(model._m))
+    rng = np.random.default_rng(3)
+    res = {}
+    for ctx in ctxs:
+        kv_layer = ctx * n_kv * hd * 2 * 2
+        L = max(4, -(-(512 << 20) // kv_layer))
+        bufs = {}
+        sizes = {"kc": L * kv_layer // 2, "vc": L * kv_layer // 2, "q": L * n_heads * hd * 4,
+                 "k": L * n_kv * hd * 4, "v": L * n_kv * hd * 4, "out": L * n_heads * hd * 4}
+        for nm, nb in sizes.items():
+            bufs[nm] = ctypes.c_void_p()
+            lib.gsdh_malloc(ctypes.byref(bufs[nm]), nb)
+        # one layer's worth of fp16 N(0,1) values, repeated over the layers
+        lay = rng.standard_normal(kv_layer // 4, dtype=np.float32).astype(np.float16)
+        for nm in ("kc", "vc"):
+            for l in range(L):
+                lib.gsdh_memcpy_h2d(ctypes.c_void_p(bufs[nm].value + l * lay.nbytes),
+                                    lay.ctypes.data_as(ctypes.c_void_p), lay.nbytes, None)
+        host = [rng.standard_normal(sizes[nm] // 4, dtype=np.float32) for nm in ("q", "k", "v")]
+        for nm, h in zip(("q", "k", "v"), host):
+            lib.gsdh_memcpy_h2d(bufs[nm], h.ctypes.data_as(ctypes.c_void_p), h.nbytes, None)
+        lib.gsdh_stream_sync(None)   # (host arrays referenced until here)
+        pos = ctx - 1
+        at = lambda nm, l, n: ctypes.c_void_p(bufs[nm].value + l * n * 4)
+
+        def run():
+            for l in range(L):
+                lib.gsdh_rope_and_store_kv(sp, at("q", l, n_heads * hd), at("k", l, n_kv * hd), at("v", l, n_kv * hd),
+                                           bufs["kc"], bufs["vc"], l, pos, n_heads, n_kv, hd, ctx,
+                                           ctypes.c_float(theta), 1)
+                lib.gsdh_gqa_attention(sp, at("q", l, n_heads * hd), bufs["kc"], bufs["vc"],
+                                       at("out", l, n_heads * hd), l, pos, n_heads, n_kv, hd, ctx,
+                                       ctypes.c_float(sm_scale))
+
+        run()                                    # sizes the attention workspace outside the capture
+        lib.gsdh_stream_sync(sp)
+        ge = capture(model, run)
+        time_graph(model, ge, 2)
+        us = time_graph(model, ge, reps) * 1e3 / (reps * L)
+        lib.gsdh_graph_destroy(ge)
+        for nm in bufs:
+            lib.gsdh_free(bufs[nm])
+        b = kv_layer + 4096 + 2 * 4 * n_heads * hd
+        gbs = b / (us * 1e-6) / 1e9
+        res[f"ctx{ctx}"] = {"us_per_layer": round(us, 2), "bytes_per_layer": b, "GBs": round(gbs, 1),
+                            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "layers_rotated": L}
+    model.close()
+    res["workload"] = ("32 q heads / 8 KV heads x 128, fp16 KV cache ~N(0,1) filled to ctx-1, RoPE + append at "
+                       "ctx-1, split attention; graph of all layers, HIP events")
+    return res
+
+
 def traffic_from_profile():
     """HBM bytes per gate/up launch from the committed counter summary
     (profiles/hexmv_gateup_traffic.txt: FETCH_SIZE and WRITE_SIZE per
@@ -315,6 +389,7 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-attention", action="store_true")
     ap.add_argument("--probe", choices=["gateup", "copy"], help="run one kernel for rocprofv3 counters")
     a = ap.parse_args()
     if a.probe:
@@ -335,6 +410,9 @@ def main():
     if not a.no_prefill:
         extra["prefill_turbo"] = dict(bench_prefill(turbo), workload="Turbo 7B layer set (7 tensors), X bf16 "
                                       "[M][cols] -> Y fp32, fp16 MFMA with fp32 accumulation")
+    if not a.no_attention:
+        extra["attention_c3"] = bench_attention()
+        log(f"attention: {extra['attention_c3']}")
     if not a.no_precision:
         prec = LayerBank("precision", max(3, a.layers // 2))
         pg, pms, proof = bench_linear(prec, a.steps, a.warmup)

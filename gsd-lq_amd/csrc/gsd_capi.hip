@@ -83,11 +83,12 @@ __attribute__((noinline)) void rope_cs(float theta, int hd, int pos, float* out 
     }
 }
 
-// Scratch of the attention twin: partials + per-KV-head counters.
+// Scratch of the attention twin: partial words + per-KV-head launch counters
+// (both zeroed when allocated).
 struct AttnScratch {
     std::mutex mu;
-    float* ws = nullptr;
-    size_t ws_floats = 0;
+    unsigned long long* ws = nullptr;
+    size_t ws_bytes = 0;
     unsigned* counters = nullptr;
     size_t n_counters = 0;
 } g_attn;
@@ -224,13 +225,14 @@ int gsdh_gqa_attention(void* stream, const float* q, const uint16_t* k_cache, co
     a.chunk = choose_chunk(n, n_kv_heads);
     a.max_splits = (n + a.chunk - 1) / a.chunk;
     std::lock_guard<std::mutex> lk(g_attn.mu);
-    const size_t need = attention_ws_floats(n_kv_heads, a.max_splits, G, head_dim);
-    if (need > g_attn.ws_floats) {
+    const size_t need = attention_ws_bytes(n_kv_heads, a.max_splits, G, head_dim);
+    if (need > g_attn.ws_bytes) {
         if (g_attn.ws) HIPCHK(hipFree(g_attn.ws));
         g_attn.ws = nullptr;
-        g_attn.ws_floats = 0;
-        HIPCHK(hipMalloc(&g_attn.ws, need * sizeof(float)));
-        g_attn.ws_floats = need;
+        g_attn.ws_bytes = 0;
+        HIPCHK(hipMalloc(&g_attn.ws, need));
+        HIPCHK(launch_fill_u32(reinterpret_cast<unsigned*>(g_attn.ws), 0u, need / 4, S(stream)));
+        g_attn.ws_bytes = need;
     }
     if ((size_t)n_kv_heads > g_attn.n_counters) {
         if (g_attn.counters) HIPCHK(hipFree(g_attn.counters));
@@ -283,7 +285,7 @@ struct gsdh_model {
     float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *h = nullptr, *logits = nullptr;
     uint16_t *kc = nullptr, *vc = nullptr;
     float2* cs = nullptr;
-    float* ws = nullptr;
+    unsigned long long* ws = nullptr;   // attention partial words
     unsigned* counters = nullptr;
     void* mm_ws = nullptr;          // prefill staging (A fragments | descales | rank-k values)
     size_t mm_ws_bytes = 0;
@@ -425,6 +427,7 @@ int issue_token(gsdh_model* m, bool with_head, bool short_ctx) {
         a.layer = l; a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.hd = c.head_dim; a.max_seq = c.max_seq_len;
         a.sm_scale = 1.0f / (float)std::sqrt((double)c.head_dim);
         a.chunk = m->chunk; a.max_splits = m->max_splits; a.ws = m->ws; a.counters = m->counters;
+        a.err = &m->st->err;
         if (short_ctx) {   // positions < kShortCtx: one block per KV head
             a.chunk = kShortCtx;
             a.max_splits = 1;
@@ -571,7 +574,7 @@ int gsdh_model_create(const gsdh_model_config* cfg, gsdh_model** out) {
     A((void**)&m->cs, (size_t)c.max_seq_len * (c.head_dim / 2) * sizeof(float2));
     m->chunk = choose_chunk(c.max_seq_len, c.n_kv_heads);
     m->max_splits = (c.max_seq_len + m->chunk - 1) / m->chunk;
-    A((void**)&m->ws, attention_ws_floats(c.n_kv_heads, m->max_splits, c.n_heads / c.n_kv_heads, c.head_dim) * 4);
+    A((void**)&m->ws, attention_ws_bytes(c.n_kv_heads, m->max_splits, c.n_heads / c.n_kv_heads, c.head_dim));
     A((void**)&m->counters, (size_t)c.n_kv_heads * 4);
     m->pub_words = (4 * c.n_layers + 1) * kLeadMax;
     A((void**)&m->pub, (size_t)m->pub_words * 8);
@@ -600,6 +603,10 @@ int gsdh_model_create(const gsdh_model_config* cfg, gsdh_model** out) {
     if (!rc) {
         // zero the KV cache and counters with kernels (no memset nodes anywhere)
         e = launch_fill_u32(m->counters, 0u, (size_t)c.n_kv_heads, m->stream);
+        if (e == hipSuccess)
+            e = launch_fill_u32(reinterpret_cast<unsigned*>(m->ws), 0u,
+                                attention_ws_bytes(c.n_kv_heads, m->max_splits, c.n_heads / c.n_kv_heads, c.head_dim) / 4,
+                                m->stream);
         if (e == hipSuccess) e = launch_fill_u32((unsigned*)m->pub, 0u, 2 * (size_t)m->pub_words, m->stream);
         if (e == hipSuccess) e = launch_fill_u32((unsigned*)m->kc, 0u, kvn / 2, m->stream);
         if (e == hipSuccess) e = launch_fill_u32((unsigned*)m->vc, 0u, kvn / 2, m->stream);

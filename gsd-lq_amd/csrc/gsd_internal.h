@@ -142,11 +142,18 @@ struct AttnArgs {
     float sm_scale;
     int chunk;            // positions per split
     int max_splits;       // grid.y
-    float* ws;            // partials [n_kv][max_splits][group][2 + hd]
-    unsigned* counters;   // [n_kv], zero between launches
+    // Splits of a KV head hand their partials (max, sum, o[hd] per query
+    // head) to the block of the last split as 64-bit words, epoch << 32 |
+    // float bits, one relaxed device-scope store each: a word read with the
+    // launch's epoch is that launch's value, so there is no fence and no
+    // clearing.  counters[kvh] counts the head's launches (the epoch is the
+    // count + 1); the merging block advances it.  Zero both at allocation.
+    unsigned long long* ws;   // [n_kv][max_splits][group][2 + hd]
+    unsigned* counters;       // [n_kv]
+    unsigned* err;            // set to 1 when a wait for a partial runs out (may be null)
 };
 hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
-size_t attention_ws_floats(int n_kv, int max_splits, int group, int hd);
+size_t attention_ws_bytes(int n_kv, int max_splits, int group, int hd);
 
 // embedding row of *token_dev to fp32 x; also zeroes clear[0..nclear) (the
 // rank-k publication words of the token's matvec launches)

@@ -579,19 +579,27 @@ __global__ void rope_kv_kernel(float* q, const float* k, const float* v, const R
 // loads 16 bytes (8 fp16 dims) of K or V, so a wave reads 64/LPP whole rows
 // per 16-byte load.  Dot products finish with DPP row reductions; every
 // reduction stays in VALU (DPP, permlane swaps) except the final cross-wave
-// one.  The last block of a KV head to finish merges the per-split
-// (max, sum, o) partials.
+// one.  The block of a KV head's last split merges the per-split
+// (max, sum, o) partials, handed over as epoch-tagged words.
 // ------------------------------------------------------------------------
+
+constexpr int kAttnStage = 8192;   // floats of LDS staging for the merge (32 KB)
 
 template <int HD, int G>
 __global__ void __launch_bounds__(256) attn_kernel(const AttnArgs a) {
     constexpr int LPP = HD / 8;          // lanes per position
     constexpr int PPW = 64 / LPP;        // positions per wave per step
     constexpr int PPB = 4 * PPW;         // positions per block per step
-    constexpr int UNR = 4;               // steps whose loads are issued together
+    // steps whose loads are issued together: a whole chunk (256 positions at
+    // most) of K and of V for HD <= 128, so one block has its 128 KB in
+    // flight at once (a decode block is alone on its CU: it is latency, not
+    // bandwidth, that a shallow issue depth runs into)
+    constexpr int UNR = 256 / PPB < 16 ? 256 / PPB : 16;
     __shared__ float sc[G][256];
     __shared__ float part[4][G][HD];
     __shared__ float ml[2][G];
+    __shared__ float lsp[1][256];   // merging block: every split's exp-sum
+    __shared__ float stage[kAttnStage];   // merging block: a batch of the splits' outputs
 
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int sub = lane % LPP, prow = lane / LPP;
@@ -601,6 +609,7 @@ __global__ void __launch_bounds__(256) attn_kernel(const AttnArgs a) {
     const int split = blockIdx.y;
     if (split >= nsplit) return;
     const int kvh = blockIdx.x;
+    const unsigned ep0 = a.counters[kvh];   // launches of this KV head so far (used at the end)
     const int t0 = split * a.chunk;
     const int t1 = min(n, t0 + a.chunk);
     const int cn = t1 - t0;
@@ -617,15 +626,34 @@ __global__ void __launch_bounds__(256) attn_kernel(const AttnArgs a) {
         qv[g][4] = q1.x; qv[g][5] = q1.y; qv[g][6] = q1.z; qv[g][7] = q1.w;
     }
 
-    // phase A: scores s[g][t] = (q_g . K_t) * sm_scale
+    // phase A: scores s[g][t] = (q_g . K_t) * sm_scale.  Every load is
+    // issued, past the chunk's end clamped to its last row (an L2 hit), so the
+    // load counts stay fixed; the V rows of the first batch go out right
+    // behind the K rows and arrive while the scores are computed.
     const int nsteps = (cn + PPB - 1) / PPB;
-    for (int s0 = 0; s0 < nsteps; s0 += UNR) {
-        uint4 kw[UNR];
+    uint4 kw[UNR], vw[UNR];
+    auto kload = [&](int s0) {
 #pragma unroll
         for (int u = 0; u < UNR; u++) {
             const int t = min(t0 + (s0 + u) * PPB + wid * PPW + prow, t1 - 1);
             kw[u] = *reinterpret_cast<const uint4*>(kb + (size_t)t * rowstride);
         }
+    };
+    auto vload = [&](int s0) {
+#pragma unroll
+        for (int u = 0; u < UNR; u++) {
+            const int t = min(t0 + (s0 + u) * PPB + wid * PPW + prow, t1 - 1);
+            vw[u] = *reinterpret_cast<const uint4*>(vb + (size_t)t * rowstride);
+        }
+    };
+    kload(0);
+    vload(0);
+    // one batch covers the whole chunk (<= 256 positions, the score buffer)
+    // when UNR * PPB >= 256: then the loops run once, known at compile time,
+    // and the loads' wait counts stay exact
+    const int nend = UNR * PPB >= 256 ? 1 : nsteps;
+    for (int s0 = 0; s0 < nend; s0 += UNR) {
+        if (s0 > 0) kload(s0);
 #pragma unroll
         for (int u = 0; u < UNR; u++) {
             const int tl = (s0 + u) * PPB + wid * PPW + prow;
@@ -663,13 +691,8 @@ __global__ void __launch_bounds__(256) attn_kernel(const AttnArgs a) {
     for (int g = 0; g < G; g++)
 #pragma unroll
         for (int e = 0; e < 8; e++) acc[g][e] = 0.f;
-    for (int s0 = 0; s0 < nsteps; s0 += UNR) {
-        uint4 vw[UNR];
-#pragma unroll
-        for (int u = 0; u < UNR; u++) {
-            const int t = min(t0 + (s0 + u) * PPB + wid * PPW + prow, t1 - 1);
-            vw[u] = *reinterpret_cast<const uint4*>(vb + (size_t)t * rowstride);
-        }
+    for (int s0 = 0; s0 < nend; s0 += UNR) {
+        if (s0 > 0) vload(s0);
 #pragma unroll
         for (int u = 0; u < UNR; u++) {
             const int tl = (s0 + u) * PPB + wid * PPW + prow;
@@ -705,40 +728,122 @@ __global__ void __launch_bounds__(256) attn_kernel(const AttnArgs a) {
         }
         return;
     }
-    // partials [kvh][split][g][2+HD]; attn_merge_kernel combines them
-    float* wsb = a.ws + ((size_t)kvh * a.max_splits + split) * G * (2 + HD);
-    for (int i = tid; i < G * HD; i += 256) {
-        const int g = i / HD, d = i % HD;
-        wsb[g * (2 + HD) + 2 + d] = (part[0][g][d] + part[1][g][d]) + (part[2][g][d] + part[3][g][d]);
+    // partials [kvh][split][g][2+HD] as epoch-tagged words (every block, all
+    // G heads); query head g is merged by the block of split nsplit - 1 - g
+    // (g mod nsplit when there are fewer splits than heads): no merge launch,
+    // no fence, and the merge reads spread over G blocks
+    const unsigned ep = ep0 + 1u;
+    const unsigned long long tag = (unsigned long long)ep << 32;
+    unsigned long long* wsk = a.ws + (size_t)kvh * a.max_splits * G * (2 + HD);
+    {
+        unsigned long long* wsb = wsk + (size_t)split * G * (2 + HD);
+        for (int i = tid; i < G * HD; i += 256) {
+            const int g = i / HD, d = i % HD;
+            const float o = (part[0][g][d] + part[1][g][d]) + (part[2][g][d] + part[3][g][d]);
+            __hip_atomic_store(wsb + g * (2 + HD) + 2 + d, tag | __float_as_uint(o), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (tid < G) {
+            __hip_atomic_store(wsb + tid * (2 + HD), tag | __float_as_uint(ml[0][tid]), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(wsb + tid * (2 + HD) + 1, tag | __float_as_uint(ml[1][tid]), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
-    if (tid < G) {
-        wsb[tid * (2 + HD)] = ml[0][tid];
-        wsb[tid * (2 + HD) + 1] = ml[1][tid];
+    const int back = nsplit - 1 - split;
+    if (back >= G) return;
+    // merge: out = sum_s f_s o_s / sum_s f_s l_s, f_s = exp(m_s - max m), in
+    // split order.  Word loads bypass the non-coherent caches (sc1) and go out
+    // together (out-of-range offsets read 0); a word without this launch's
+    // epoch is waited for (bounded), normally never.  Own split from LDS.
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        wsk, (short)0, nsplit * G * (2 + HD) * 8, 0x00020000);
+    auto ld = [&](int w) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, w * 8, 0, 16 /* sc1 */);
+        return ((unsigned long long)v[1] << 32) | v[0];
+    };
+    auto wait_word = [&](int w) {
+        unsigned long long v;
+        int spins = 0;
+        while (((v = __hip_atomic_load(wsk + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) >> 32) != ep &&
+               spins < (1 << 20)) {
+            if (++spins == (1 << 20) && a.err) *a.err = 1u;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        return __uint_as_float((unsigned)v);
+    };
+    auto value = [&](unsigned long long v, int w) {
+        return (v >> 32) == ep ? __uint_as_float((unsigned)v) : wait_word(w);
+    };
+    constexpr int SB = kAttnStage / HD;       // splits per staging batch
+    constexpr int MAXI = kAttnStage / 256;    // staged words per thread
+    for (int g = back; g < G; g += nsplit) {
+        __syncthreads();   // (LDS reuse across heads)
+        // one round trip: the (max, sum) words of every split and the first
+        // batch of output words go out together
+        unsigned long long v[MAXI];
+        auto stage_issue = [&](int s0) {
+            const int sn = min(SB, nsplit - s0);
+#pragma unroll
+            for (int j = 0; j < MAXI; j++) {
+                const int i = tid + 256 * j, sp = s0 + i / HD, d = i % HD;
+                v[j] = ld(i < sn * HD ? (sp * G + g) * (2 + HD) + 2 + d : -1);
+            }
+        };
+        auto stage_put = [&](int s0) {
+            const int sn = min(SB, nsplit - s0);
+#pragma unroll
+            for (int j = 0; j < MAXI; j++) {
+                const int i = tid + 256 * j, sp = s0 + i / HD, d = i % HD;
+                if (i < sn * HD)
+                    stage[i] = sp == split ? (part[0][g][d] + part[1][g][d]) + (part[2][g][d] + part[3][g][d])
+                                           : value(v[j], (sp * G + g) * (2 + HD) + 2 + d);
+            }
+        };
+        const int wm = (tid * G + g) * (2 + HD);   // (valid for tid < nsplit)
+        const unsigned long long vm = ld(tid < nsplit ? wm : -1), vl = ld(tid < nsplit ? wm + 1 : -1);
+        stage_issue(0);
+        for (int sp = tid; sp < nsplit; sp += 256) {
+            if (sp == split) {
+                sc[0][sp] = ml[0][g];
+                lsp[0][sp] = ml[1][g];
+            } else if (sp == tid) {
+                sc[0][sp] = value(vm, wm);
+                lsp[0][sp] = value(vl, wm + 1);
+            } else {   // (more than 256 splits: not launched, kept general)
+                const int w = (sp * G + g) * (2 + HD);
+                sc[0][sp] = wait_word(w);
+                lsp[0][sp] = wait_word(w + 1);
+            }
+        }
+        stage_put(0);
+        __syncthreads();
+        if (wid == 0) {
+            float M = -INFINITY;
+            for (int sp = lane; sp < nsplit; sp += 64) M = fmaxf(M, sc[0][sp]);
+            M = wave_allmax(M);
+            for (int sp = lane; sp < nsplit; sp += 64) sc[0][sp] = expf(sc[0][sp] - M);
+        }
+        __syncthreads();
+        float L = 0.f, O = 0.f;
+        for (int s0 = 0; s0 < nsplit; s0 += SB) {
+            if (s0 > 0) {
+                stage_issue(s0);
+                stage_put(s0);
+                __syncthreads();
+            }
+            const int sn = min(SB, nsplit - s0);
+            if (tid < HD)
+                for (int k = 0; k < sn; k++) {
+                    const float f = sc[0][s0 + k];
+                    L = fmaf(lsp[0][s0 + k], f, L);
+                    O = fmaf(stage[k * HD + tid], f, O);
+                }
+            __syncthreads();
+        }
+        if (tid < HD) a.out[(size_t)(group_base + g) * HD + tid] = O / L;
     }
-}
-
-// Merge of the per-split softmax partials (stream order after attn_kernel
-// makes them visible); a no-op when the context fits one split, in which
-// case attn_kernel wrote the output itself.  grid = n_heads blocks of HD.
-__global__ void attn_merge_kernel(const AttnArgs a) {
-    const int pos = a.pos_dev ? *a.pos_dev : a.pos;
-    const int nsplit = (pos + 1 + a.chunk - 1) / a.chunk;
-    if (nsplit <= 1) return;
-    const int G = a.n_heads / a.n_kv;
-    const int h = blockIdx.x, kvh = h / G, g = h % G, d = threadIdx.x;
-    const int HD = a.hd;
-    const float* base = a.ws + (size_t)kvh * a.max_splits * G * (2 + HD) + (size_t)g * (2 + HD);
-    const size_t sstride = (size_t)G * (2 + HD);
-    float M = -INFINITY;
-    for (int sp = 0; sp < nsplit; sp++) M = fmaxf(M, base[sp * sstride]);
-    float L = 0.f, O = 0.f;
-    for (int sp = 0; sp < nsplit; sp++) {
-        const float* pp = base + sp * sstride;
-        const float f = expf(pp[0] - M);
-        L = fmaf(pp[1], f, L);
-        O = fmaf(pp[2 + d], f, O);
-    }
-    a.out[(size_t)h * HD + d] = O / L;
+    if (back == 0 && tid == 0) a.counters[kvh] = ep;   // the next launch's epoch base (stream order)
 }
 
 __global__ void embed_kernel(const uint16_t* embed, const int* token, float* x, int hidden,
@@ -1749,11 +1854,14 @@ hipError_t launch_rope_kv(float* q, const float* k, const float* v, const RopeKV
     return hipGetLastError();
 }
 
-size_t attention_ws_floats(int n_kv, int max_splits, int group, int hd) {
-    return (size_t)n_kv * max_splits * group * (2 + hd);
+size_t attention_ws_bytes(int n_kv, int max_splits, int group, int hd) {
+    return (size_t)n_kv * max_splits * group * (2 + hd) * 8;
 }
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
+    // the merging block holds every split's (max, sum) in its 256-entry
+    // score buffer
+    if (a.max_splits < 1 || a.max_splits > 256 || a.chunk > 256 || !a.counters) return hipErrorInvalidValue;
     const dim3 grid(a.n_kv, a.max_splits);
     const int G = a.n_heads / a.n_kv;
 #define GSD_ATTN_G(HD)                                                                          \
@@ -1771,12 +1879,6 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
         default: return hipErrorInvalidValue;
     }
 #undef GSD_ATTN_G
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    // one split (contexts up to `chunk`): the attention kernel writes the
-    // output itself and no merge launch is needed
-    if (a.max_splits <= 1) return hipSuccess;
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(a.n_heads), dim3(a.hd), 0, st, a);
     return hipGetLastError();
 }
 
