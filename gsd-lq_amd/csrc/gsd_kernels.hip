@@ -993,7 +993,10 @@ __device__ __forceinline__ void mv4_publish(const HexArgs& a, int lead, float* s
 
 // TB > 0: every segment uses the same codebook of TB points, held at a
 // static LDS address; TB == 0: per-segment codebooks in dynamic LDS.
-template <int TB>
+// LR: some segment has rank-k terms (without them the rank-k machinery is not
+// compiled in: the epilogue code is inlined once per pipeline step of the
+// main loop).
+template <int TB, bool LR>
 __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) hexmv4_kernel(const HexArgs a) {
     __shared__ __attribute__((aligned(16))) uint32_t stab[TB > 0 ? TB * 64 : 1];
     __shared__ float red[2][kMv4MaxWaves][16];
@@ -1041,9 +1044,10 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
 
     // rank-k publishing blocks first
     int nlead = 0;
-    for (int g = 0; g < a.nseg; g++)
-        if (!a.seg[g].tmp_k && a.seg[g].k > 0) nlead += a.seg[g].k;
-    if ((int)blockIdx.x < nlead) {
+    if constexpr (LR)
+        for (int g = 0; g < a.nseg; g++)
+            if (!a.seg[g].tmp_k && a.seg[g].k > 0) nlead += a.seg[g].k;
+    if (LR && (int)blockIdx.x < nlead) {
         mv4_publish(a, (int)blockIdx.x, scratch);
         return;
     }
@@ -1188,7 +1192,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     }
     unsigned have = 0;   // epilogue lanes: rank-k values of segment g fetched
     using KF32 = const __attribute__((address_space(4))) float;
-    for (int g = 0; g < a.nseg; g++) {
+    for (int g = 0; g < (LR ? a.nseg : 0); g++) {
         if (kseg[g].k > 0 && kseg[g].tmp_k) {
             for (int j = 0; j < kseg[g].k; j++) {   // uniform index: scalar loads
                 const float v = ((KF32*)kseg[g].tmp_k)[j];
@@ -1260,7 +1264,9 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     };
 
     float pre = 0.f;                       // epilogue inputs of the current unit,
-    float2 pcs = make_float2(1.f, 0.f);    // fetched when the unit starts
+    float2 pcs = make_float2(1.f, 0.f);    // fetched when the unit starts (a load
+    uint32_t upf[2] = {0u, 0u};            // at the unit end would wait behind the
+                                           // code loads in flight: vmcnt is in order)
     auto prefetch = [&](int uu) {
         if (wid == 0 && lane < 16 && uu < nunits) {
             const int g = seg_of(uu);
@@ -1269,6 +1275,15 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                 if (a.epilogue == kEpiResidual) pre = a.resid[prow];
                 if (a.epilogue == kEpiRopeKV && g != 2)
                     pcs = a.rope.cs[(size_t)rpos * (a.rope.hd >> 1) + ((prow % a.rope.hd) >> 1)];
+                // the row's rank-k factors U[row][0..k) of each tensor of the
+                // unit, for k <= 2 (fp16 pair; U is 256-byte aligned)
+#pragma unroll
+                for (int gi = 0; gi < 2; gi++) {
+                    if (!LR || gi >= G) break;
+                    KSeg& sp = kseg[paired ? gi : g];
+                    if (sp.k == 2) upf[gi] = reinterpret_cast<const uint32_t*>(sp.U)[prow];
+                    else if (sp.k == 1) upf[gi] = sp.U[prow];
+                }
             }
         }
     };
@@ -1303,7 +1318,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                         const uint32_t e = sg.row_ptr[row + 1];
                         for (uint32_t i = sg.row_ptr[row]; i < e; i++) t += sg.kdel[i] * xnorm(a, sg.kcols[i], inv);
                     }
-                    if (sg.k > 0) {
+                    if (LR && sg.k > 0) {
                         if (!((have >> sg_i) & 1u)) {
                             // bounded wait for the published rank-k words of
                             // this segment (normally already there)
@@ -1323,8 +1338,18 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                             }
                             have |= 1u << sg_i;
                         }
-                        const uint16_t* up_ = sg.U + (size_t)row * sg.k;
-                        for (int jj = 0; jj < sg.k; jj++) t += h2f(up_[jj]) * tkl[sg_i][jj];
+                        if (sg.k <= 2) {   // prefetched factors, same order as below
+                            // (the asm keeps the use, and the wait for the
+                            // load, inside this branch: hoisted, it would wait
+                            // for the code loads in flight in every launch)
+                            uint32_t uw = gi == 0 ? upf[0] : upf[1];
+                            __asm__ volatile("" : "+v"(uw));
+                            t += h2f((uint16_t)(uw & 0xFFFFu)) * tkl[sg_i][0];
+                            if (sg.k == 2) t += h2f((uint16_t)(uw >> 16)) * tkl[sg_i][1];
+                        } else {
+                            const uint16_t* up_ = sg.U + (size_t)row * sg.k;
+                            for (int jj = 0; jj < sg.k; jj++) t += h2f(up_[jj]) * tkl[sg_i][jj];
+                        }
                     }
                 }
                 if (gi == 0) fin0 = t;
@@ -1678,19 +1703,19 @@ hipError_t launch_hexmv(const HexArgs& a, hipStream_t st) {
 #undef GSD_HEXMV_DISPATCH
 }
 
-template <int TB>
+template <int TB, bool LR>
 hipError_t launch_hexmv4_t(const HexArgs& a, hipStream_t st, int nw, size_t lds, int nunits, int nlead) {
     static int per_cu = 0;
     static size_t attr_lds = 0;
     if (lds > attr_lds) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&hexmv4_kernel<TB>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&hexmv4_kernel<TB, LR>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         attr_lds = lds;
         per_cu = 0;
     }
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, hexmv4_kernel<TB>, nw * 64, lds) != hipSuccess || n < 1)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, hexmv4_kernel<TB, LR>, nw * 64, lds) != hipSuccess || n < 1)
         return hipErrorInvalidConfiguration;
     per_cu = n;
     const int ncu = device_cu_count() > 0 ? device_cu_count() : 256;
@@ -1699,7 +1724,7 @@ hipError_t launch_hexmv4_t(const HexArgs& a, hipStream_t st, int nw, size_t lds,
     int grid = ncu * per_cu - nlead;
     if (grid < 1) grid = 1;
     if (grid > nunits) grid = nunits;
-    hipLaunchKernelGGL((hexmv4_kernel<TB>), dim3(grid + nlead), dim3(nw * 64), lds, st, a);
+    hipLaunchKernelGGL((hexmv4_kernel<TB, LR>), dim3(grid + nlead), dim3(nw * 64), lds, st, a);
     return hipGetLastError();
 }
 
@@ -1731,9 +1756,15 @@ hipError_t launch_hexmv4(const HexArgs& a, hipStream_t st) {
     while (wr > 1 && nc % wr != 0) wr >>= 1;
     const int nw = wr * G;
     const size_t xbytes = (size_t)G * nc * 512;   // every wave's own chunks of x
-    if (shared && a.seg[0].n_pts == 217) return launch_hexmv4_t<217>(a, st, nw, xbytes, nunits, nlead);
-    if (shared && a.seg[0].n_pts == 127) return launch_hexmv4_t<127>(a, st, nw, xbytes, nunits, nlead);
-    return launch_hexmv4_t<0>(a, st, nw, xbytes + (size_t)tab_bytes, nunits, nlead);
+    bool lr = false;
+    for (int g = 0; g < a.nseg; g++) lr = lr || a.seg[g].k > 0;
+#define GSD_MV4(T) \
+    return lr ? launch_hexmv4_t<T, true>(a, st, nw, xbytes + (T == 0 ? (size_t)tab_bytes : 0), nunits, nlead) \
+              : launch_hexmv4_t<T, false>(a, st, nw, xbytes + (T == 0 ? (size_t)tab_bytes : 0), nunits, nlead);
+    if (shared && a.seg[0].n_pts == 217) GSD_MV4(217)
+    if (shared && a.seg[0].n_pts == 127) GSD_MV4(127)
+    GSD_MV4(0)
+#undef GSD_MV4
 }
 
 size_t hexmm_xa_bytes(int M, int cols) {
