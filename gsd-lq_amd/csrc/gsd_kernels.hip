@@ -995,8 +995,9 @@ __device__ __forceinline__ void mv4_publish(const HexArgs& a, int lead, float* s
 // static LDS address; TB == 0: per-segment codebooks in dynamic LDS.
 // LR: some segment has rank-k terms (without them the rank-k machinery is not
 // compiled in: the epilogue code is inlined once per pipeline step of the
-// main loop).
-template <int TB, bool LR>
+// main loop, and a smaller kernel runs faster).  EPI: the epilogue (HexEpilogue),
+// or -1 to read it from the arguments.
+template <int TB, bool LR, int EPI>
 __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) hexmv4_kernel(const HexArgs a) {
     __shared__ __attribute__((aligned(16))) uint32_t stab[TB > 0 ? TB * 64 : 1];
     __shared__ float red[2][kMv4MaxWaves][16];
@@ -1037,9 +1038,10 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     unsigned bdim = blockDim.x;
     int cols0 = a.cols, epi0 = a.epilogue;
     __asm__ volatile("" : "+s"(bdim), "+s"(cols0), "+s"(epi0));
+    const int epi = EPI >= 0 ? EPI : epi0;
     const int NW = (int)(bdim >> 6);
     const int nc = (cols0 + 127) >> 7;
-    const bool paired = epi0 == kEpiSwiGLU;
+    const bool paired = epi == kEpiSwiGLU;
     const int G = paired ? 2 : 1, WR = NW / G, grp = wid / WR, wr = wid - grp * WR;
 
     // rank-k publishing blocks first
@@ -1114,7 +1116,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     // loads, which never wait behind the vector loads of the codes
     using KI32 = const __attribute__((address_space(4))) int;
     using KU32 = const __attribute__((address_space(4))) uint32_t;
-    const int rpos = a.epilogue == kEpiRopeKV ? (a.rope.pos_dev ? *(KI32*)a.rope.pos_dev : a.rope.pos) : 0;
+    const int rpos = epi == kEpiRopeKV ? (a.rope.pos_dev ? *(KI32*)a.rope.pos_dev : a.rope.pos) : 0;
     uint32_t* X32 = reinterpret_cast<uint32_t*>(dyn + tab_bytes) + (size_t)wid * P * 128;
     const uint4* Xw = reinterpret_cast<const uint4*>(X32);
     constexpr int kXP = 8;   // chunks of x per batch of loads
@@ -1272,8 +1274,8 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
             const int g = seg_of(uu);
             const int prow = (paired ? uu : uu - ubase(g)) * 16 + lane;
             if (prow < kseg[g].rows) {
-                if (a.epilogue == kEpiResidual) pre = a.resid[prow];
-                if (a.epilogue == kEpiRopeKV && g != 2)
+                if (epi == kEpiResidual) pre = a.resid[prow];
+                if (epi == kEpiRopeKV && g != 2)
                     pcs = a.rope.cs[(size_t)rpos * (a.rope.hd >> 1) + ((prow % a.rope.hd) >> 1)];
                 // the row's rank-k factors U[row][0..k) of each tensor of the
                 // unit, for k <= 2 (fp16 pair; U is 256-byte aligned)
@@ -1359,9 +1361,9 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
             const int row = (paired ? u : u - ubase(g)) * 16 + lane;
             if (paired) {
                 if (row < s0.rows) s0.out[row] = (fin0 / (1.0f + expf(-fin0))) * fin1;
-            } else if (a.epilogue == kEpiStore) {
+            } else if (epi == kEpiStore) {
                 if (row < s0.rows) s0.out[row] = fin0;
-            } else if (a.epilogue == kEpiResidual) {
+            } else if (epi == kEpiResidual) {
                 if (row < s0.rows) a.resid[row] = pre + fin0;
             } else {
                 // kEpiRopeKV: rows 2i, 2i+1 of a head are one rotation pair
@@ -1703,19 +1705,19 @@ hipError_t launch_hexmv(const HexArgs& a, hipStream_t st) {
 #undef GSD_HEXMV_DISPATCH
 }
 
-template <int TB, bool LR>
+template <int TB, bool LR, int EPI>
 hipError_t launch_hexmv4_t(const HexArgs& a, hipStream_t st, int nw, size_t lds, int nunits, int nlead) {
     static int per_cu = 0;
     static size_t attr_lds = 0;
     if (lds > attr_lds) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&hexmv4_kernel<TB, LR>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&hexmv4_kernel<TB, LR, EPI>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         attr_lds = lds;
         per_cu = 0;
     }
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, hexmv4_kernel<TB, LR>, nw * 64, lds) != hipSuccess || n < 1)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, hexmv4_kernel<TB, LR, EPI>, nw * 64, lds) != hipSuccess || n < 1)
         return hipErrorInvalidConfiguration;
     per_cu = n;
     const int ncu = device_cu_count() > 0 ? device_cu_count() : 256;
@@ -1724,7 +1726,7 @@ hipError_t launch_hexmv4_t(const HexArgs& a, hipStream_t st, int nw, size_t lds,
     int grid = ncu * per_cu - nlead;
     if (grid < 1) grid = 1;
     if (grid > nunits) grid = nunits;
-    hipLaunchKernelGGL((hexmv4_kernel<TB, LR>), dim3(grid + nlead), dim3(nw * 64), lds, st, a);
+    hipLaunchKernelGGL((hexmv4_kernel<TB, LR, EPI>), dim3(grid + nlead), dim3(nw * 64), lds, st, a);
     return hipGetLastError();
 }
 
@@ -1758,12 +1760,22 @@ hipError_t launch_hexmv4(const HexArgs& a, hipStream_t st) {
     const size_t xbytes = (size_t)G * nc * 512;   // every wave's own chunks of x
     bool lr = false;
     for (int g = 0; g < a.nseg; g++) lr = lr || a.seg[g].k > 0;
-#define GSD_MV4(T) \
-    return lr ? launch_hexmv4_t<T, true>(a, st, nw, xbytes + (T == 0 ? (size_t)tab_bytes : 0), nunits, nlead) \
-              : launch_hexmv4_t<T, false>(a, st, nw, xbytes + (T == 0 ? (size_t)tab_bytes : 0), nunits, nlead);
-    if (shared && a.seg[0].n_pts == 217) GSD_MV4(217)
-    if (shared && a.seg[0].n_pts == 127) GSD_MV4(127)
-    GSD_MV4(0)
+    // the shared-codebook kernels are specialised on the epilogue as well
+#define GSD_MV4(T, E) \
+    return lr ? launch_hexmv4_t<T, true, E>(a, st, nw, xbytes + (T == 0 ? (size_t)tab_bytes : 0), nunits, nlead) \
+              : launch_hexmv4_t<T, false, E>(a, st, nw, xbytes + (T == 0 ? (size_t)tab_bytes : 0), nunits, nlead);
+#define GSD_MV4E(T)                                          \
+    switch (a.epilogue) {                                    \
+        case kEpiStore: GSD_MV4(T, kEpiStore)                \
+        case kEpiResidual: GSD_MV4(T, kEpiResidual)          \
+        case kEpiSwiGLU: GSD_MV4(T, kEpiSwiGLU)              \
+        case kEpiRopeKV: GSD_MV4(T, kEpiRopeKV)              \
+        default: return hipErrorInvalidValue;                \
+    }
+    if (shared && a.seg[0].n_pts == 217) GSD_MV4E(217)
+    if (shared && a.seg[0].n_pts == 127) GSD_MV4E(127)
+    GSD_MV4(0, -1)
+#undef GSD_MV4E
 #undef GSD_MV4
 }
 
