@@ -52,6 +52,28 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0xB1, 0xF, 0xF, false)));
+    v = fmaxf(v, __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x4E, 0xF, 0xF, false)));
+    v = fmaxf(v, __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x141, 0xF, 0xF, false)));
+    v = fmaxf(v, __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x140, 0xF, 0xF, false)));
+    return v;
+}
+// Whole-wave sum / max in every lane, in VALU only (row DPP, then the
+// 16- and 32-lane swaps); all 64 lanes must be active.
+__device__ __forceinline__ float wave_sum_valu(float v) {
+    v = row16_sum(v);
+    v = swap_add16(v, v);
+    return swap_add32(v, v, false);
+}
+__device__ __forceinline__ float wave_max_valu(float v) {
+    v = row16_max(v);
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 __device__ __forceinline__ float dpp_sum8(float v) {    // sum within 8-lane half-rows
     v += __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0xB1, 0xF, 0xF, false));
     v += __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x4E, 0xF, 0xF, false));

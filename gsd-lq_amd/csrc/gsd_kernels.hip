@@ -993,15 +993,23 @@ __device__ __forceinline__ void mv4_publish(const HexArgs& a, int lead, float* s
 
 // TB > 0: every segment uses the same codebook of TB points, held at a
 // static LDS address; TB == 0: per-segment codebooks in dynamic LDS.
-// LR: some segment has rank-k terms (without them the rank-k machinery is not
-// compiled in: the epilogue code is inlined once per pipeline step of the
-// main loop, and a smaller kernel runs faster).  EPI: the epilogue (HexEpilogue),
-// or -1 to read it from the arguments.
-template <int TB, bool LR, int EPI>
+// LR: rank-k terms.  0: none (the rank-k machinery is not compiled in: the
+// epilogue code is inlined once per pipeline step of the main loop, and a
+// smaller kernel runs faster); 1: ranks <= 2, projections computed by every
+// block from its own staging of x (kLrSlots); 2: any rank, projections
+// published by leading blocks.  EPI: the epilogue (HexEpilogue), or -1 to
+// read it from the arguments.
+template <int TB, int LR, int EPI>
 __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) hexmv4_kernel(const HexArgs a) {
     __shared__ __attribute__((aligned(16))) uint32_t stab[TB > 0 ? TB * 64 : 1];
     __shared__ float red[2][kMv4MaxWaves][16];
     __shared__ float tkl[kMaxSeg][kMaxRank];
+    // LR == 1: each wave's partial rank-k dot products over its own columns
+    // (times S[j]), slot r = j (paired launch: the wave's group's segment) or
+    // 2 g + j, wave index last
+    constexpr int kVS = LR != 1 ? 1 : (EPI == kEpiResidual || EPI == kEpiSwiGLU ? 2 : 2 * kMaxSeg);
+    static_assert(LR != 1 || kVS == 2 || kVS == 2 * kMaxSeg, "rank-k slot counts");
+    __shared__ float vtp[kVS][LR == 1 ? kMv4MaxWaves : 1];
     __shared__ float scratch[32];
     __shared__ float ssq[kMv4MaxWaves];   // sum of x^2 over each wave's columns
     extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
@@ -1046,10 +1054,10 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
 
     // rank-k publishing blocks first
     int nlead = 0;
-    if constexpr (LR)
+    if constexpr (LR == 2)
         for (int g = 0; g < a.nseg; g++)
             if (!a.seg[g].tmp_k && a.seg[g].k > 0) nlead += a.seg[g].k;
-    if (LR && (int)blockIdx.x < nlead) {
+    if (LR == 2 && (int)blockIdx.x < nlead) {
         mv4_publish(a, (int)blockIdx.x, scratch);
         return;
     }
@@ -1119,17 +1127,61 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     const int rpos = epi == kEpiRopeKV ? (a.rope.pos_dev ? *(KI32*)a.rope.pos_dev : a.rope.pos) : 0;
     uint32_t* X32 = reinterpret_cast<uint32_t*>(dyn + tab_bytes) + (size_t)wid * P * 128;
     const uint4* Xw = reinterpret_cast<const uint4*>(X32);
-    constexpr int kXP = 8;   // chunks of x per batch of loads
+    // chunks of x per batch of loads (4 when the rank-k rows of three
+    // segments come with them: 24 more registers instead of 48)
+    constexpr int kXP = LR == 1 && kVS > 2 ? 4 : 8;
     float2 xv[kXP], wv[kXP];
+    // LR == 1: the rank-k rows Vt[j] of the wave's columns come with x (slot
+    // r of vmask: segment paired ? grp : r / 2, row paired ? r : r % 2), and
+    // dk[r] sums x'[c] * Vt[j][c] over them (x' without the RMSNorm factor)
+    auto slot_seg = [&](int r) { return paired ? grp : r >> 1; };
+    auto slot_row = [&](int r) { return paired ? r : r & 1; };
+    unsigned vmask = 0, emask = 0;   // emask: bit 2 g + j, segment g row j, for the epilogue
+    if constexpr (LR == 1) {
+        // (no short-circuit: seg[0..2] are all in the arguments, and one
+        // branch per test would wait for each scalar read in turn)
+#pragma unroll
+        for (int e = 0; e < 2 * kMaxSeg; e++)
+            emask |= (unsigned)(((e >> 1) < a.nseg) & (kseg[e >> 1].tmp_k == nullptr) & (kseg[e >> 1].k > (e & 1))) << e;
+        vmask = paired ? (emask >> (2 * grp)) & 3u : emask & ((1u << kVS) - 1u);
+    }
+    // Vt row of each slot (uniform); an unused slot reads the start of x
+    // instead (in bounds: 2 bytes per column against 4), so that the loads
+    // are unconditional and go out back to back
+    const uint16_t* vrow[kVS];
+#pragma unroll
+    for (int r = 0; r < kVS; r++)
+        vrow[r] = ((vmask >> r) & 1u) ? kseg[slot_seg(r)].Vt + (size_t)slot_row(r) * cols0
+                                      : reinterpret_cast<const uint16_t*>(a.x);
+    // S[j] of each slot, read with x as vector loads (a lane offset the
+    // compiler cannot prove uniform): they land with x, and take no scalar
+    // registers, of which the prologue has none to spare
+    float sv[kVS];
+    if constexpr (LR == 1) {
+        int z;
+        __asm__ volatile("v_mov_b32 %0, 0" : "=v"(z));
+#pragma unroll
+        for (int r = 0; r < kVS; r++) sv[r] = (((vmask >> r) & 1u) ? kseg[slot_seg(r)].S + slot_row(r) : a.x)[z];
+    }
+    uint32_t vt[kVS][kXP];
+    float dk[kVS];
+#pragma unroll
+    for (int r = 0; r < kVS; r++) dk[r] = 0.f;
     auto xload = [&](int p0) {
 #pragma unroll
         for (int i = 0; i < kXP; i++) {
             const int p = p0 + i, col = (wr + p * WR) * 128 + 2 * lane;
             xv[i] = make_float2(0.f, 0.f);
             wv[i] = make_float2(1.f, 1.f);
+#pragma unroll
+            for (int r = 0; r < kVS; r++) vt[r][i] = 0u;
             if (p < P && col < a.cols) {
                 xv[i] = *reinterpret_cast<const float2*>(a.x + col);
                 if (a.norm_w) wv[i] = *reinterpret_cast<const float2*>(a.norm_w + col);
+                if constexpr (LR == 1) {
+#pragma unroll
+                    for (int r = 0; r < kVS; r++) vt[r][i] = *reinterpret_cast<const uint32_t*>(vrow[r] + col);
+                }
             }
         }
     };
@@ -1147,6 +1199,14 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                 ss = fmaf(xv[i].x, xv[i].x, ss);
                 ss = fmaf(xv[i].y, xv[i].y, ss);
                 const float xa = xv[i].x * wv[i].x, xb = xv[i].y * wv[i].y;
+                if constexpr (LR == 1) {
+#pragma unroll
+                    for (int r = 0; r < kVS; r++)
+                        if ((vmask >> r) & 1u) {
+                            dk[r] = fmaf(xa, h2f((uint16_t)(vt[r][i] & 0xFFFFu)), dk[r]);
+                            dk[r] = fmaf(xb, h2f((uint16_t)(vt[r][i] >> 16)), dk[r]);
+                        }
+                }
                 const float u = xa, v = fmaf(kS32, xb, 0.5f * xa);
                 mx = fmaxf(mx, fmaxf(fabsf(u), fabsf(v)));
                 X32[p * 128 + xoff] = __float_as_uint(u);
@@ -1211,12 +1271,22 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
         xload(p0);
         xfirst(p0);
     }
+    // wave reductions in VALU (DPP and lane swaps): the LDS permutes of
+    // shuffles cost 16 waves x 6 steps per value
+    ss = wave_sum_valu(ss);
+    mx = wave_max_valu(mx);
+    if constexpr (LR == 1) {
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        ss += __shfl_xor(ss, o, 64);
-        mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        for (int r = 0; r < kVS; r++)
+            if ((vmask >> r) & 1u) dk[r] = wave_sum_valu(dk[r]);
     }
     if (lane == 0) ssq[wid] = ss;
+    if constexpr (LR == 1) {
+        if (lane == 0) {
+#pragma unroll
+            for (int r = 0; r < kVS; r++) vtp[r][wid] = ((vmask >> r) & 1u) ? dk[r] * sv[r] : 0.f;
+        }
+    }
     // power-of-two scale putting the wave's largest |u|, |v| near
     // [2^13, 2^14): fp16 high and low parts then hold them to 2^-22
     int ex = 0;
@@ -1281,7 +1351,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                 // unit, for k <= 2 (fp16 pair; U is 256-byte aligned)
 #pragma unroll
                 for (int gi = 0; gi < 2; gi++) {
-                    if (!LR || gi >= G) break;
+                    if (LR == 0 || gi >= G) break;
                     KSeg& sp = kseg[paired ? gi : g];
                     if (sp.k == 2) upf[gi] = reinterpret_cast<const uint32_t*>(sp.U)[prow];
                     else if (sp.k == 1) upf[gi] = sp.U[prow];
@@ -1304,6 +1374,23 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                 for (int w = 0; w < WR; w++) sx += ssq[w];
                 inv = 1.0f / sqrtf(sx / (float)a.cols + a.eps);
             }
+            if constexpr (LR == 1) {
+                // first unit end: rank-k values of the segments without tmp_k,
+                // inv * (sum of the S-scaled partials of the waves covering x)
+                // (gsd_lq_cpu_engine.c:110-127); lane l reads wave l's partial
+                if (!(have & 0x100u)) {
+#pragma unroll
+                    for (int e = 0; e < 2 * kMaxSeg; e++) {
+                        const int r = paired ? (e & 1) : e, w0 = paired ? (e >> 1) * WR : 0;
+                        if (r < kVS && ((emask >> e) & 1u)) {
+                            // (lanes 0-15 are one DPP row, all active here)
+                            const float v = row16_sum(lane < WR ? vtp[r][w0 + lane] : 0.f);
+                            tkl[e >> 1][e & 1] = v * inv;
+                        }
+                    }
+                    have |= 0x100u;
+                }
+            }
             float fin0 = 0.f, fin1 = 0.f;
 #pragma unroll
             for (int gi = 0; gi < 2; gi++) {
@@ -1320,8 +1407,8 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                         const uint32_t e = sg.row_ptr[row + 1];
                         for (uint32_t i = sg.row_ptr[row]; i < e; i++) t += sg.kdel[i] * xnorm(a, sg.kcols[i], inv);
                     }
-                    if (LR && sg.k > 0) {
-                        if (!((have >> sg_i) & 1u)) {
+                    if (LR > 0 && sg.k > 0) {
+                        if (LR == 2 && !((have >> sg_i) & 1u)) {
                             // bounded wait for the published rank-k words of
                             // this segment (normally already there)
                             int off = 0;
@@ -1340,7 +1427,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                             }
                             have |= 1u << sg_i;
                         }
-                        if (sg.k <= 2) {   // prefetched factors, same order as below
+                        if (LR == 1 || sg.k <= 2) {   // prefetched factors, same order as below
                             // (the asm keeps the use, and the wait for the
                             // load, inside this branch: hoisted, it would wait
                             // for the code loads in flight in every launch)
@@ -1705,7 +1792,7 @@ hipError_t launch_hexmv(const HexArgs& a, hipStream_t st) {
 #undef GSD_HEXMV_DISPATCH
 }
 
-template <int TB, bool LR, int EPI>
+template <int TB, int LR, int EPI>
 hipError_t launch_hexmv4_t(const HexArgs& a, hipStream_t st, int nw, size_t lds, int nunits, int nlead) {
     static int per_cu = 0;
     static size_t attr_lds = 0;
@@ -1721,8 +1808,9 @@ hipError_t launch_hexmv4_t(const HexArgs& a, hipStream_t st, int nw, size_t lds,
         return hipErrorInvalidConfiguration;
     per_cu = n;
     const int ncu = device_cu_count() > 0 ? device_cu_count() : 256;
-    // publishing blocks first (dispatched in order, they are resident before
-    // any matvec block waits on them), and all blocks resident at once
+    // publishing blocks (LR == 2) first (dispatched in order, they are
+    // resident before any matvec block waits on them), and all blocks
+    // resident at once
     int grid = ncu * per_cu - nlead;
     if (grid < 1) grid = 1;
     if (grid > nunits) grid = nunits;
@@ -1736,17 +1824,26 @@ hipError_t launch_hexmv4(const HexArgs& a, hipStream_t st) {
     const bool paired = a.epilogue == kEpiSwiGLU;
     if (paired && (a.nseg != 2 || a.seg[0].rows != a.seg[1].rows)) return hipErrorInvalidValue;
     if (a.epilogue == kEpiRopeKV && a.nseg != 3) return hipErrorInvalidValue;
-    bool shared = true;
+    bool shared = true, lr = false, inblock = a.epilogue != kEpiResidual || a.nseg == 1;
     int nlead = 0, nunits = 0, tab_bytes = 0;
     for (int g = 0; g < a.nseg; g++) {
         const HexSeg& s = a.seg[g];
         if (!s.codes_t || !s.scales_t || !s.fields || s.n_pts < 1 || s.n_pts > kTableSlots) return hipErrorInvalidValue;
         shared = shared && s.fields == a.seg[0].fields && s.n_pts == a.seg[0].n_pts;
-        if (!s.tmp_k && s.k > 0) nlead += s.k;
+        if (s.k > 0 && (!s.U || (!s.tmp_k && (!s.Vt || !s.S)))) return hipErrorInvalidValue;
+        lr = lr || s.k > 0;
+        if (!s.tmp_k && s.k > 0) {
+            nlead += s.k;
+            inblock = inblock && s.k <= 2;
+        }
         nunits += (s.rows + 15) / 16;
         tab_bytes += s.n_pts * 256;
     }
     if (paired) nunits = (a.seg[0].rows + 15) / 16;
+    // ranks <= 2 (every model tensor of the Precision mode): each block forms
+    // the projections from its own staging of x; otherwise leading blocks
+    // publish them (generic epilogue)
+    if (inblock) nlead = 0;
     if (nlead > 0 && (!a.pub || !a.err)) return hipErrorInvalidValue;
     if (nunits == 0) return hipSuccess;
     // waves per row-block: up to 16 (8 per group when paired), at most one
@@ -1758,12 +1855,14 @@ hipError_t launch_hexmv4(const HexArgs& a, hipStream_t st) {
     while (wr > 1 && nc % wr != 0) wr >>= 1;
     const int nw = wr * G;
     const size_t xbytes = (size_t)G * nc * 512;   // every wave's own chunks of x
-    bool lr = false;
-    for (int g = 0; g < a.nseg; g++) lr = lr || a.seg[g].k > 0;
     // the shared-codebook kernels are specialised on the epilogue as well
-#define GSD_MV4(T, E) \
-    return lr ? launch_hexmv4_t<T, true, E>(a, st, nw, xbytes + (T == 0 ? (size_t)tab_bytes : 0), nunits, nlead) \
-              : launch_hexmv4_t<T, false, E>(a, st, nw, xbytes + (T == 0 ? (size_t)tab_bytes : 0), nunits, nlead);
+#define GSD_MV4(T, E)                                                                           \
+    {                                                                                           \
+        const size_t lds = xbytes + (T == 0 ? (size_t)tab_bytes : 0);                           \
+        if (!lr) return launch_hexmv4_t<T, 0, E>(a, st, nw, lds, nunits, 0);                    \
+        if (inblock) return launch_hexmv4_t<T, 1, E>(a, st, nw, lds, nunits, 0);                \
+        return launch_hexmv4_t<T, 2, -1>(a, st, nw, lds, nunits, nlead);                        \
+    }
 #define GSD_MV4E(T)                                          \
     switch (a.epilogue) {                                    \
         case kEpiStore: GSD_MV4(T, kEpiStore)                \

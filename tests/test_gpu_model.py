@@ -85,6 +85,21 @@ def test_model_stepwise_vs_oracle(mode, kpr, il, shape, engine):
     gpu.close()
 
 
+@pytest.mark.parametrize("k_dim", [1, 3])
+def test_model_rank_sizes_vs_oracle(k_dim):
+    """Rank 1 runs the matvec's in-block projection with one row per tensor;
+    rank 3 the launches whose projections leading blocks publish (graph engine)."""
+    banner(f"stepwise model precision rank {k_dim} (graph)")
+    gpu, ref = _models(_spec(mode="precision", kinks_per_row=1, k_dim=k_dim))
+    rng = np.random.default_rng(11 + k_dim)
+    toks = rng.integers(0, gpu.vocab_size, 12).tolist()
+    for pos, t in enumerate(toks):
+        a = gpu.forward_token(t, pos)
+        b = ref.forward_token(t, pos)
+        assert rel_l2(a, b) < 1e-3, pos
+    gpu.close()
+
+
 @pytest.mark.parametrize("engine", ENGINES)
 def test_generate_greedy_matches_oracle(engine):
     banner(f"generate_greedy vs oracle ({engine})")
