@@ -691,13 +691,20 @@ int gsdh_model_set_hex(gsdh_model* m, int layer, int slot, int radius, int rows,
     HexDev& t = m->slot(layer, slot);
     if (t.block) { (void)hipFree(t.block); m->dev_bytes -= t.bytes; t = HexDev(); }
     auto al = [](size_t n) { return (n + 255) / 256 * 256; };
-    // tiled layout of the MFMA matvec: codes [nrb][nc][64 lanes][16 B] with
-    // lane l = row 16rb + (l & 15), bytes j = pairs 64c + 8(l >> 4) + j (j < 8)
-    // and 64c + 32 + 8(l >> 4) + j - 8 (j >= 8); scales [nrb][nc][16] as the
-    // fp16 pair of the chunk's two 64-weight blocks.  Padding: code 0, scale 0.
+    // tiled layout of the MFMA matvec: codes [nrb][nc][tile] where lane l of
+    // a tile holds 16 codes of row 16rb + (l & 15): code j = pair 64c +
+    // 8(l >> 4) + j (j < 8) or 64c + 32 + 8(l >> 4) + j - 8 (j >= 8).  A tile
+    // is 64 lanes x 16 bytes (one byte per code) for codebooks of more than
+    // 128 points, and 896 bytes for at most 128 (radius <= 6): 7 bits per
+    // code, lane pair i at bytes 28i .. 28i + 27, lane 2i's 16 codes as a
+    // 112-bit little-endian field at byte 28i (code j = bits 7j .. 7j + 6),
+    // lane 2i + 1's at byte 28i + 14.  Scales [nrb][nc][16] as the fp16 pair
+    // of the chunk's two 64-weight blocks.  Padding: code 0, scale 0.
     const size_t nrb = ((size_t)rows + 15) / 16, nc = ((size_t)cols + 127) / 128, nsb = (size_t)cols / 64;
     const size_t half = (size_t)cols / 2;
-    const size_t o_codes = 0, o_sc = o_codes + al(nrb * nc * 1024), o_rp = o_sc + al(nrb * nc * 64);
+    const bool b7 = n_pts <= 128;
+    const size_t tbytes = b7 ? 896 : 1024;
+    const size_t o_codes = 0, o_sc = o_codes + al(nrb * nc * tbytes), o_rp = o_sc + al(nrb * nc * 64);
     const size_t o_kc = o_rp + al((size_t)(rows + 1) * 4), o_kd = o_kc + al((size_t)nk * 2);
     const size_t o_u = o_kd + al((size_t)nk * 4), o_s = o_u + al((size_t)rows * k_dim * 2);
     const size_t o_vt = o_s + al((size_t)k_dim * 4), total = o_vt + al((size_t)k_dim * cols * 2);
@@ -709,18 +716,26 @@ int gsdh_model_set_hex(gsdh_model* m, int layer, int slot, int radius, int rows,
     t.kcols = (uint16_t*)(b + o_kc); t.kdel = (float*)(b + o_kd); t.U = (uint16_t*)(b + o_u);
     t.Sv = (float*)(b + o_s); t.Vt = (uint16_t*)(b + o_vt);
     {
-        std::vector<uint8_t> ct(nrb * nc * 1024, 0);
+        std::vector<uint8_t> ct(nrb * nc * tbytes, 0);
         std::vector<uint32_t> stl(nrb * nc * 16, 0);
         for (size_t rb = 0; rb < nrb; rb++)
             for (size_t c = 0; c < nc; c++) {
-                uint8_t* dst = ct.data() + (rb * nc + c) * 1024;
+                uint8_t* dst = ct.data() + (rb * nc + c) * tbytes;
                 for (int l = 0; l < 64; l++) {
                     const size_t row = rb * 16 + (size_t)(l & 15);
                     if (row >= (size_t)rows) continue;
                     const uint8_t* src = codes + row * half;
+                    uint8_t* ld = b7 ? dst + 28 * (l >> 1) + 14 * (l & 1) : dst + 16 * l;
                     for (int j = 0; j < 16; j++) {
                         const size_t p = 64 * c + (j < 8 ? 8 * (size_t)(l >> 4) + j : 32 + 8 * (size_t)(l >> 4) + (j - 8));
-                        if (p < half) dst[l * 16 + j] = src[p];
+                        const unsigned v = p < half ? src[p] : 0u;
+                        if (!b7) {
+                            ld[j] = (uint8_t)v;
+                        } else {   // bits 7j .. 7j + 6 of the lane's field
+                            const unsigned bit = 7u * (unsigned)j;
+                            ld[bit >> 3] |= (uint8_t)(v << (bit & 7));
+                            if ((bit & 7) > 1) ld[(bit >> 3) + 1] |= (uint8_t)(v >> (8 - (bit & 7)));
+                        }
                     }
                 }
                 for (int n = 0; n < 16; n++) {
@@ -833,6 +848,25 @@ int gsdh_generate_greedy(gsdh_model* m, const int* prompt, int n_prompt, int sta
     (void)hipStreamSynchronize(m->stream);
     (void)hipHostFree(ring);
     return rc;
+}
+
+int gsdh_model_read_codes(gsdh_model* m, int layer, int slot, uint8_t* codes_out) {
+    if (!m || !codes_out) return fail(-1, "read_codes: null argument");
+    if (slot < 0 || slot > GSDH_LM_HEAD) return fail(-1, "read_codes: slot %d", slot);
+    if (slot != GSDH_LM_HEAD && (layer < 0 || layer >= m->c.n_layers)) return fail(-1, "read_codes: layer %d", layer);
+    const HexDev& t = m->slot(layer, slot);
+    if (!t.set) return fail(-1, "read_codes: layer %d slot %d not set", layer, slot);
+    const size_t n = (size_t)t.rows * t.cols / 2;
+    void* d = nullptr;
+    HIPCHK(hipMalloc(&d, n));
+    HexSeg s{};
+    fill_seg(s, t, m, nullptr);
+    hipError_t e = launch_tile_codes(s, t.cols, static_cast<uint8_t*>(d), m->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+    if (e == hipSuccess) e = hipMemcpy(codes_out, d, n, hipMemcpyDeviceToHost);
+    (void)hipFree(d);
+    if (e != hipSuccess) return fail((int)e, "read_codes: %s", hipGetErrorString(e));
+    return 0;
 }
 
 int gsdh_model_matmul(gsdh_model* m, int layer, int slot, const uint16_t* X, int M, float* Y) {

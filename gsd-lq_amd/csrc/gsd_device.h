@@ -74,6 +74,50 @@ __device__ __forceinline__ float wave_max_valu(float v) {
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// Code tiles of the matrix-core matvec: a 16-row x 128-column tile of codes,
+// one 16-code word per lane (lane l: row l & 15).  Codebooks of more than 128
+// points (radius 7-8) use one byte per code: 1024 bytes, lane l at byte 16 l.
+// Codebooks of at most 128 points (radius <= 6) use 7 bits per code: 896
+// bytes, lane pair i owning bytes 28 i .. 28 i + 27, the 16 codes of lane 2 i
+// as a 112-bit little-endian field (code j = bits 7 j .. 7 j + 6) at byte
+// 28 i and those of lane 2 i + 1 at byte 28 i + 14.  Lane 2 i loads 16 bytes
+// at 28 i and lane 2 i + 1 at 28 i + 12 (4-byte aligned), so an odd lane's
+// field starts at bit 16 of its word until align7 shifts it down.
+constexpr int kTileU8 = 1024, kTile7 = 896;
+__device__ __forceinline__ int tile_bytes(bool b7) { return b7 ? kTile7 : kTileU8; }
+__device__ __forceinline__ uint32_t tile_lane_off(bool b7, int lane) {
+    return b7 ? 28u * (uint32_t)(lane >> 1) + 12u * (uint32_t)(lane & 1) : 16u * (uint32_t)lane;
+}
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+__device__ __forceinline__ uint4 tile_load(const unsigned char* p) {   // p = tile + tile_lane_off
+    const u32x4_a4 v = *reinterpret_cast<const u32x4_a4*>(p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+// 7-bit word with the lane's field moved to bit 0 (sh = 16 on odd lanes, 0 on even)
+__device__ __forceinline__ void align7(uint32_t (&w)[4], uint32_t sh) {
+    w[0] = __builtin_amdgcn_alignbit(w[1], w[0], sh);
+    w[1] = __builtin_amdgcn_alignbit(w[2], w[1], sh);
+    w[2] = __builtin_amdgcn_alignbit(w[3], w[2], sh);
+    w[3] = w[3] >> sh;
+}
+// code j (a constant after unrolling) of an aligned 7-bit word at bits 8 .. 14
+__device__ __forceinline__ uint32_t win7(const uint32_t (&w)[4], int j) {
+    if (j == 0) return w[0] << 8;
+    if (j == 1) return w[0] << 1;
+    const int s = 7 * j - 8, d = s >> 5, sh = s & 31;
+    return d == 3 ? w[3] >> sh : __builtin_amdgcn_alignbit(w[d + 1], w[d], sh);
+}
+// code j of a lane's word (u8 word, or 7-bit word after align7)
+__device__ __forceinline__ uint32_t code_of(const uint32_t (&w)[4], int j, bool b7) {
+    return b7 ? (win7(w, j) >> 8) & 0x7Fu : (w[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+}
+// LDS address code * 256 + lane * 4 of code j (lane_off = lane * 4): the
+// entry of the lane's own copy of the codebook
+__device__ __forceinline__ uint32_t code_addr(const uint32_t (&w)[4], int j, uint32_t lane_off, bool b7) {
+    return b7 ? ((win7(w, j) & 0x7F00u) | lane_off)
+              : __builtin_amdgcn_perm(w[j >> 2], lane_off, 0x0C0C0400u + ((uint32_t)(j & 3) << 8));
+}
+
 __device__ __forceinline__ float dpp_sum8(float v) {    // sum within 8-lane half-rows
     v += __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0xB1, 0xF, 0xF, false));
     v += __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x4E, 0xF, 0xF, false));

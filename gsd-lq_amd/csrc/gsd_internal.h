@@ -79,6 +79,16 @@ struct HexArgs {
     // be zero when the launch starts (each launch of a sequence has its own).
     unsigned long long* pub;
     unsigned* err;             // set to 1 when the wait exceeds its bound
+    // hexmv4 launch plan, filled in by launch_hexmv4 (callers leave it zero):
+    // per-launch constants the kernel would otherwise derive with integer
+    // divisions ahead of its first loads
+    struct Mv4Plan {
+        int P;                 // 128-column chunks per wave and unit
+        int wr_log2;           // log2 of the waves of a row-block group
+        int nunits;            // row-block units of the launch
+        int ub1, ub2;          // first units of segments 1 and 2
+        int units_q, units_r;  // units of matvec block b: units_q + (b < units_r)
+    } mv;
 };
 
 constexpr int kLeadMax = kMaxSeg * kMaxRank;   // publishing blocks per launch
@@ -179,6 +189,8 @@ hipError_t launch_unpack(const uint8_t* codes, int64_t n, int radius, int32_t* i
                          int8_t* r01, hipStream_t stream);
 
 hipError_t launch_copy(const void* src, void* dst, size_t nbytes, hipStream_t stream);
+// codes of a tensor's tiled layout back in file order (u8 [rows][cols / 2], device)
+hipError_t launch_tile_codes(const HexSeg& s, int cols, uint8_t* out, hipStream_t stream);
 
 int device_cu_count();
 

@@ -956,6 +956,9 @@ constexpr int kMv4MaxWaves = 16;
 // code steps (1 KB per wave each) in flight per wave: a CU streams about
 // (16 waves x depth KB) per load latency, so the depth sets its share of HBM
 constexpr int kMv4Depth = 4;
+// units per block whose epilogue inputs (residual, RoPE cos/sin, rank-k
+// factors) the prologue stages in LDS; the launcher keeps every block within it
+constexpr int kMv4PreUnits = 8;
 
 // x'[c] of the launch (RMSNorm applied when norm_w is set), as the reference
 // forms it: (x * inv) * w.
@@ -1012,6 +1015,11 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     __shared__ float vtp[kVS][LR == 1 ? kMv4MaxWaves : 1];
     __shared__ float scratch[32];
     __shared__ float ssq[kMv4MaxWaves];   // sum of x^2 over each wave's columns
+    // epilogue inputs of the block's units (written and read by the epilogue
+    // lanes, wave 0 lanes 0-15)
+    __shared__ float lpre[EPI == kEpiResidual || EPI < 0 ? kMv4PreUnits : 1][16];
+    __shared__ float2 lcs[EPI == kEpiRopeKV || EPI < 0 ? kMv4PreUnits : 1][16];
+    __shared__ uint32_t lup[LR > 0 ? kMv4PreUnits : 1][2][16];
     extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
 
     // wid in a scalar register: the segment selections below (seg_of) then
@@ -1045,12 +1053,17 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     // batch, so nothing waits for them before the batch is out)
     unsigned bdim = blockDim.x;
     int cols0 = a.cols, epi0 = a.epilogue;
-    __asm__ volatile("" : "+s"(bdim), "+s"(cols0), "+s"(epi0));
+    int P = a.mv.P, wrl = a.mv.wr_log2, nunits = a.mv.nunits, ub1 = a.mv.ub1, ub2 = a.mv.ub2;
+    int units_q = a.mv.units_q, units_r = a.mv.units_r;
+    __asm__ volatile("" : "+s"(bdim), "+s"(cols0), "+s"(epi0), "+s"(P), "+s"(wrl), "+s"(nunits), "+s"(ub1), "+s"(ub2),
+                     "+s"(units_q), "+s"(units_r));
     const int epi = EPI >= 0 ? EPI : epi0;
     const int NW = (int)(bdim >> 6);
     const int nc = (cols0 + 127) >> 7;
     const bool paired = epi == kEpiSwiGLU;
-    const int G = paired ? 2 : 1, WR = NW / G, grp = wid / WR, wr = wid - grp * WR;
+    // waves of a row-block group: a power of two dividing the chunk count
+    const int G = paired ? 2 : 1, WR = 1 << wrl, grp = wid >> wrl, wr = wid & (WR - 1);
+    using KU32 = const __attribute__((address_space(4))) uint32_t;
 
     // rank-k publishing blocks first
     int nlead = 0;
@@ -1064,12 +1077,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     const int nblk = (int)gridDim.x - nlead;
 
     // units: paired -> row-block rb of gate and up; else the row-blocks of
-    // the segments in order
-    // unit boundaries of the segments (scalars: no indexed private arrays)
-    const int nrb0 = (a.seg[0].rows + 15) >> 4;
-    const int ub1 = nrb0, ub2 = ub1 + (a.nseg > 1 ? (a.seg[1].rows + 15) >> 4 : 0);
-    const int ub3 = ub2 + (a.nseg > 2 ? (a.seg[2].rows + 15) >> 4 : 0);
-    const int nunits = paired ? nrb0 : ub3;
+    // the segments in order (first units ub1, ub2 of segments 1, 2)
     auto seg_of = [&](int u) {   // segment of a unit for this wave
         if (paired) return grp;
         return u >= ub2 ? 2 : (u >= ub1 ? 1 : 0);
@@ -1089,23 +1097,36 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     // the load cursor stays on that unit (valid addresses, unused data,
     // lines the block has just read: a shared unit there would have every
     // block's surplus loads meet on the same few HBM channels).
-    const int P = nc / WR;   // >= 1
+    // P >= 1 chunks per wave and unit (WR divides nc)
     const int u0 = (int)blockIdx.x - nlead;
-    const int my_units = u0 < nunits ? (nunits - 1 - u0) / nblk + 1 : 0;
+    const int my_units = u0 < nunits ? units_q + (u0 < units_r ? 1 : 0) : 0;
     const int nsteps = P * my_units;
-    int lk = 0, lj = 0;
-    const uint4* lcb = nullptr;
+    // code tiles: 7-bit for codebooks of at most 128 points (TB > 0: known
+    // here; TB == 0: per segment, bit g of b7m)
+    constexpr bool kB7 = TB > 0 && TB <= 128;
+    unsigned b7m = 0;
+    if constexpr (TB == 0)
+        for (int g = 0; g < a.nseg; g++) b7m |= (unsigned)(kseg[g].n_pts <= 128) << g;
+    auto seg_b7 = [&](int g) { return TB > 0 ? kB7 : ((b7m >> g) & 1u) != 0; };
+    const uint32_t lof8 = tile_lane_off(false, lane), lof7 = tile_lane_off(true, lane);
+    int lk = 0, lj = 0, lts = tile_bytes(kB7);
+    uint32_t lof = kB7 ? lof7 : lof8;
+    const unsigned char* lcb = nullptr;
     const uint32_t* lsb = nullptr;
     auto lset = [&](int k) {
         const int uu = min(u0 + min(k, max(my_units - 1, 0)) * nblk, nunits - 1);
         const int g = seg_of(uu);
         const int rb = paired ? uu : uu - ubase(g);
-        lcb = kseg[g].codes_t + (size_t)rb * nc * 64;
+        if constexpr (TB == 0) {
+            lts = tile_bytes(seg_b7(g));
+            lof = seg_b7(g) ? lof7 : lof8;
+        }
+        lcb = reinterpret_cast<const unsigned char*>(kseg[g].codes_t) + (size_t)rb * nc * lts;
         lsb = kseg[g].scales_t + (size_t)rb * nc * 16;
     };
     auto lissue = [&](uint4& cw, uint32_t& sw) {
         const int c = wr + lj * WR;
-        cw = lcb[c * 64 + lane];
+        cw = tile_load(lcb + (size_t)c * lts + lof);
         sw = lsb[c * 16 + (lane & 15)];
         if (++lj == P) {
             lj = 0;
@@ -1123,7 +1144,6 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     // codebook fields) are read through the constant address space: scalar
     // loads, which never wait behind the vector loads of the codes
     using KI32 = const __attribute__((address_space(4))) int;
-    using KU32 = const __attribute__((address_space(4))) uint32_t;
     const int rpos = epi == kEpiRopeKV ? (a.rope.pos_dev ? *(KI32*)a.rope.pos_dev : a.rope.pos) : 0;
     uint32_t* X32 = reinterpret_cast<uint32_t*>(dyn + tab_bytes) + (size_t)wid * P * 128;
     const uint4* Xw = reinterpret_cast<const uint4*>(X32);
@@ -1158,7 +1178,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     // registers, of which the prologue has none to spare
     float sv[kVS];
     if constexpr (LR == 1) {
-        int z;
+        int z;   // a zero the compiler cannot prove uniform: loads through it are vector loads
         __asm__ volatile("v_mov_b32 %0, 0" : "=v"(z));
 #pragma unroll
         for (int r = 0; r < kVS; r++) sv[r] = (((vmask >> r) & 1u) ? kseg[slot_seg(r)].S + slot_row(r) : a.x)[z];
@@ -1200,12 +1220,15 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                 ss = fmaf(xv[i].y, xv[i].y, ss);
                 const float xa = xv[i].x * wv[i].x, xb = xv[i].y * wv[i].y;
                 if constexpr (LR == 1) {
+                    // every slot, used or not: a loaded word no path consumes
+                    // stays pending, and a later reuse of its register then
+                    // waits for every load in flight (in the main loop's
+                    // header, on every pass)
 #pragma unroll
-                    for (int r = 0; r < kVS; r++)
-                        if ((vmask >> r) & 1u) {
-                            dk[r] = fmaf(xa, h2f((uint16_t)(vt[r][i] & 0xFFFFu)), dk[r]);
-                            dk[r] = fmaf(xb, h2f((uint16_t)(vt[r][i] >> 16)), dk[r]);
-                        }
+                    for (int r = 0; r < kVS; r++) {
+                        dk[r] = fmaf(xa, h2f((uint16_t)(vt[r][i] & 0xFFFFu)), dk[r]);
+                        dk[r] = fmaf(xb, h2f((uint16_t)(vt[r][i] >> 16)), dk[r]);
+                    }
                 }
                 const float u = xa, v = fmaf(kS32, xb, 0.5f * xa);
                 mx = fmaxf(mx, fmaxf(fabsf(u), fabsf(v)));
@@ -1220,6 +1243,50 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     // and vector loads complete in issue order, so the wait for x does not
     // wait for the codes, whose latency overlaps that of x
     xload(0);
+
+    // Epilogue inputs of every unit of the block, loaded now, behind x and
+    // ahead of the codes (the wait for x covers them), and kept in LDS.
+    // Loaded in the main loop instead, the wait for them at a unit end cannot
+    // be counted (the code loads issued in between depend on P), and the
+    // compiler's safe count drains most of the loads in flight.  Rank-k
+    // factors: one 32-bit load whatever k (k = 2: the fp16 pair; k = 1: the
+    // aligned pair holding U[row], half picked at the use; other k: a word
+    // of x).  Every loaded register is stored below on every path (a load no
+    // path consumes stays pending, and the next use of its register waits
+    // for every load in flight).
+    constexpr bool kHasPre = EPI == kEpiResidual || EPI < 0, kHasCs = EPI == kEpiRopeKV || EPI < 0;
+    float epre[kMv4PreUnits];
+    float2 ecs[kMv4PreUnits];
+    uint32_t eup[kMv4PreUnits][2];
+#pragma unroll
+    for (int k = 0; k < kMv4PreUnits; k++) {
+        epre[k] = 0.f;
+        ecs[k] = make_float2(1.f, 0.f);
+        eup[k][0] = eup[k][1] = 0u;
+    }
+    if (wid == 0 && lane < 16) {
+#pragma unroll
+        for (int k = 0; k < kMv4PreUnits; k++) {
+            if (k >= my_units) break;
+            const int uu = u0 + k * nblk;
+            const int g = seg_of(uu);
+            const int prow = (paired ? uu : uu - ubase(g)) * 16 + lane;
+            const int r0 = min(prow, kseg[g].rows - 1);
+            if (kHasPre && epi == kEpiResidual) epre[k] = a.resid[r0];
+            if (kHasCs && epi == kEpiRopeKV) ecs[k] = a.rope.cs[(size_t)rpos * (a.rope.hd >> 1) + ((r0 % a.rope.hd) >> 1)];
+#pragma unroll
+            for (int gi = 0; gi < 2; gi++) {
+                if (LR == 0 || gi >= G) break;
+                KSeg& sp = kseg[paired ? gi : g];
+                const int kk = sp.k, r = min(prow, sp.rows - 1);
+                const uint32_t* up = kk == 2   ? reinterpret_cast<const uint32_t*>(sp.U) + r
+                                     : kk == 1 ? reinterpret_cast<const uint32_t*>(sp.U + (r & ~1))
+                                               : reinterpret_cast<const uint32_t*>(a.x);
+                eup[k][gi] = *up;
+            }
+        }
+    }
+
     uint4 cw[kMv4Depth];
     uint32_t sw[kMv4Depth];
     lset(0);
@@ -1229,7 +1296,9 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     // codebook copies: entry e of lane l at byte e * 256 + l * 4.  Wave w
     // writes entries 16w .. 16w + 15 (waves 16 apart when fewer than 16
     // waves cover the table); their fields come in one 64-byte scalar read
-    // (the field tables are padded to 256 entries)
+    // (the field tables are padded to 256 entries), issued after the code
+    // loads: a scalar wait is for every scalar read in flight, so issued
+    // earlier it would hold up the reads of the code pointers
     uint32_t fv[16];
     if (TB > 0 && wid * 16 < TB) {
         KU32* fp = (KU32*)a.seg[0].fields + wid * 16;
@@ -1267,6 +1336,17 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     lds_barrier();
 
     xfirst(0);
+    if (wid == 0 && lane < 16) {   // x has landed, and with it the epilogue inputs
+#pragma unroll
+        for (int k = 0; k < kMv4PreUnits; k++) {
+            if constexpr (kHasPre) lpre[k][lane] = epre[k];
+            if constexpr (kHasCs) lcs[k][lane] = ecs[k];
+            if constexpr (LR > 0) {
+                lup[k][0][lane] = eup[k][0];
+                lup[k][1][lane] = eup[k][1];
+            }
+        }
+    }
     for (int p0 = kXP; p0 < P; p0 += kXP) {   // more than kXP chunks per wave
         xload(p0);
         xfirst(p0);
@@ -1284,7 +1364,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     if constexpr (LR == 1) {
         if (lane == 0) {
 #pragma unroll
-            for (int r = 0; r < kVS; r++) vtp[r][wid] = ((vmask >> r) & 1u) ? dk[r] * sv[r] : 0.f;
+            for (int r = 0; r < kVS; r++) vtp[r][wid] = dk[r] * sv[r];   // unused slots: never read
         }
     }
     // power-of-two scale putting the wave's largest |u|, |v| near
@@ -1303,9 +1383,12 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
 
     const uint32_t lane_off = (uint32_t)lane * 4u;
     const int m = lane & 15, lg = lane >> 4;
+    const uint32_t sh7 = (uint32_t)(lane & 1) * 16u;
     auto step = [&](int g, int p, const uint4 cw, const uint32_t sw, float& acc) {   // local chunk p
         const unsigned char* tb = TB > 0 ? reinterpret_cast<const unsigned char*>(stab) : dyn + toff(g);
-        const uint32_t w4[4] = {cw.x, cw.y, cw.z, cw.w};
+        const bool b7 = seg_b7(g);
+        uint32_t w4[4] = {cw.x, cw.y, cw.z, cw.w};
+        if (b7) align7(w4, sh7);
         // the block scales leave sw before the step's loads are reissued
         // (sw dead early: its next load lands in place instead of in a copy
         // whose move at the loop end would wait for every load in flight)
@@ -1321,11 +1404,10 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                 const uint4 xv = Xw[(((p * 2 + h) * 2 + t) * 4 + lg) * 2 + (m & 1)];
                 u32x4v aw;
                 aw[0] = xv.x; aw[1] = xv.y; aw[2] = xv.z; aw[3] = xv.w;
-                const uint32_t w = w4[2 * h + t];
                 u32x4v bw;
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    const uint32_t addr = __builtin_amdgcn_perm(w, lane_off, 0x0C0C0400u + (e << 8));
+                    const uint32_t addr = code_addr(w4, 4 * (2 * h + t) + e, lane_off, b7);
                     bw[e] = *reinterpret_cast<const uint32_t*>(tb + addr);
                 }
                 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, aw), __builtin_bit_cast(half8v, bw),
@@ -1335,31 +1417,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
         }
     };
 
-    float pre = 0.f;                       // epilogue inputs of the current unit,
-    float2 pcs = make_float2(1.f, 0.f);    // fetched when the unit starts (a load
-    uint32_t upf[2] = {0u, 0u};            // at the unit end would wait behind the
-                                           // code loads in flight: vmcnt is in order)
-    auto prefetch = [&](int uu) {
-        if (wid == 0 && lane < 16 && uu < nunits) {
-            const int g = seg_of(uu);
-            const int prow = (paired ? uu : uu - ubase(g)) * 16 + lane;
-            if (prow < kseg[g].rows) {
-                if (epi == kEpiResidual) pre = a.resid[prow];
-                if (epi == kEpiRopeKV && g != 2)
-                    pcs = a.rope.cs[(size_t)rpos * (a.rope.hd >> 1) + ((prow % a.rope.hd) >> 1)];
-                // the row's rank-k factors U[row][0..k) of each tensor of the
-                // unit, for k <= 2 (fp16 pair; U is 256-byte aligned)
-#pragma unroll
-                for (int gi = 0; gi < 2; gi++) {
-                    if (LR == 0 || gi >= G) break;
-                    KSeg& sp = kseg[paired ? gi : g];
-                    if (sp.k == 2) upf[gi] = reinterpret_cast<const uint32_t*>(sp.U)[prow];
-                    else if (sp.k == 1) upf[gi] = sp.U[prow];
-                }
-            }
-        }
-    };
-    int rbuf = 0;
+    int rbuf = 0, uk = 0;   // uk: the block's unit ordinal (epilogue input slot)
     auto unit_end = [&](int u, float& acc) {
         const int g = seg_of(u);
         if (lane < 16) red[rbuf][wid][lane] = acc * down;
@@ -1431,8 +1489,8 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                             // (the asm keeps the use, and the wait for the
                             // load, inside this branch: hoisted, it would wait
                             // for the code loads in flight in every launch)
-                            uint32_t uw = gi == 0 ? upf[0] : upf[1];
-                            __asm__ volatile("" : "+v"(uw));
+                            uint32_t uw = lup[uk][gi][lane];
+                            if (sg.k == 1) uw >>= 16 * (row & 1);   // U[row] of the aligned pair
                             t += h2f((uint16_t)(uw & 0xFFFFu)) * tkl[sg_i][0];
                             if (sg.k == 2) t += h2f((uint16_t)(uw >> 16)) * tkl[sg_i][1];
                         } else {
@@ -1451,7 +1509,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
             } else if (epi == kEpiStore) {
                 if (row < s0.rows) s0.out[row] = fin0;
             } else if (epi == kEpiResidual) {
-                if (row < s0.rows) a.resid[row] = pre + fin0;
+                if (row < s0.rows) a.resid[row] = lpre[kHasPre ? uk : 0][lane] + fin0;
             } else {
                 // kEpiRopeKV: rows 2i, 2i+1 of a head are one rotation pair
                 // (interleaved RoPE, gsd_lq_cpu_engine.c:213-256) in lanes
@@ -1466,7 +1524,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                     } else {
                         const bool odd = (lane & 1) != 0;
                         const float x0 = odd ? partner : fin0, x1 = odd ? fin0 : partner;
-                        const float2 cs = pcs;
+                        const float2 cs = lcs[kHasCs ? uk : 0][lane];
                         const float y = odd ? (x0 * cs.y + x1 * cs.x) : (x0 * cs.x - x1 * cs.y);
                         if (g == 0) s0.out[row] = y;
                         else r.k_cache[base + row] = f2h(y);
@@ -1475,10 +1533,9 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
             }
         }
         rbuf ^= 1;
-        prefetch(u + nblk);
+        uk = min(uk + 1, kMv4PreUnits - 1);   // (the launcher keeps my_units <= kMv4PreUnits)
     };
 
-    prefetch(u0);
     float acc = 0.f;
     int cj = 0, ck = 0, cu = u0;
     int cg = seg_of(min(u0, nunits - 1));
@@ -1596,13 +1653,18 @@ __global__ void __launch_bounds__(512) hexmm_kernel(const MatmulArgs a) {
     const int c0 = ks * cps, c1 = min(nc, c0 + cps);
     if (c0 >= c1) return;
 
-    // codes of this wave's row blocks for chunk c
+    // codes of this wave's row blocks for chunk c (7-bit tiles for
+    // codebooks of at most 128 points)
+    const bool b7 = TB > 0 ? TB <= 128 : a.w.n_pts <= 128;
+    const int tbytes = tile_bytes(b7);
+    const uint32_t lof = tile_lane_off(b7, lane), sh7 = (uint32_t)(lane & 1) * 16u;
+    const unsigned char* cbase = reinterpret_cast<const unsigned char*>(a.w.codes_t);
     auto load = [&](int c, uint4 (&cw)[RBW], uint32_t (&sw)[RBW]) {
         c = min(c, nc - 1);
 #pragma unroll
         for (int r = 0; r < RBW; r++) {
             const size_t i = (size_t)min(rb0 + r, nrb - 1) * nc + c;
-            cw[r] = a.w.codes_t[i * 64 + lane];
+            cw[r] = tile_load(cbase + i * tbytes + lof);
             sw[r] = a.w.scales_t[i * 16 + (lane & 15)];
         }
     };
@@ -1637,7 +1699,26 @@ __global__ void __launch_bounds__(512) hexmm_kernel(const MatmulArgs a) {
 #pragma unroll
         for (int g = 0; g < TG; g++) acc[r][g] = float4v{0.f, 0.f, 0.f, 0.f};
 
+    // the shared-codebook kernels decode their one tile format directly; the
+    // generic one turns 7-bit words into u8 words first (one decode path)
+    constexpr bool B7 = TB > 0 && TB <= 128;
     auto compute = [&](const uint4 (&cw)[RBW], const uint32_t (&sw)[RBW]) {
+        uint32_t w4[RBW][4];
+#pragma unroll
+        for (int r = 0; r < RBW; r++) {
+            w4[r][0] = cw[r].x; w4[r][1] = cw[r].y; w4[r][2] = cw[r].z; w4[r][3] = cw[r].w;
+            if constexpr (B7) align7(w4[r], sh7);
+            if constexpr (TB == 0) {
+                if (b7) {
+                    align7(w4[r], sh7);
+                    uint32_t u[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+                    for (int j = 0; j < 16; j++) u[j >> 2] |= code_of(w4[r], j, true) << (8 * (j & 3));
+#pragma unroll
+                    for (int i = 0; i < 4; i++) w4[r][i] = u[i];
+                }
+            }
+        }
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             float4v d[RBW][TG];
@@ -1650,12 +1731,9 @@ __global__ void __launch_bounds__(512) hexmm_kernel(const MatmulArgs a) {
                 u32x4v bw[RBW];
 #pragma unroll
                 for (int r = 0; r < RBW; r++) {
-                    const uint32_t w4[4] = {cw[r].x, cw[r].y, cw[r].z, cw[r].w};
-                    const uint32_t w = w4[2 * h + t];
 #pragma unroll
                     for (int e = 0; e < 4; e++)
-                        bw[r][e] = *reinterpret_cast<const uint32_t*>(
-                            tb + __builtin_amdgcn_perm(w, lane_off, 0x0C0C0400u + (e << 8)));
+                        bw[r][e] = *reinterpret_cast<const uint32_t*>(tb + code_addr(w4[r], 4 * (2 * h + t) + e, lane_off, B7));
                 }
 #pragma unroll
                 for (int g = 0; g < TG; g++) {
@@ -1793,7 +1871,7 @@ hipError_t launch_hexmv(const HexArgs& a, hipStream_t st) {
 }
 
 template <int TB, int LR, int EPI>
-hipError_t launch_hexmv4_t(const HexArgs& a, hipStream_t st, int nw, size_t lds, int nunits, int nlead) {
+hipError_t launch_hexmv4_t(const HexArgs& a0, hipStream_t st, int nw, size_t lds, int nunits, int nlead) {
     static int per_cu = 0;
     static size_t attr_lds = 0;
     if (lds > attr_lds) {
@@ -1814,6 +1892,12 @@ hipError_t launch_hexmv4_t(const HexArgs& a, hipStream_t st, int nw, size_t lds,
     int grid = ncu * per_cu - nlead;
     if (grid < 1) grid = 1;
     if (grid > nunits) grid = nunits;
+    // at most kMv4PreUnits units per block (more blocks than fit at once
+    // beyond 8 units per CU: the later ones start as earlier ones finish)
+    if (grid < (nunits + kMv4PreUnits - 1) / kMv4PreUnits) grid = (nunits + kMv4PreUnits - 1) / kMv4PreUnits;
+    HexArgs a = a0;
+    a.mv.units_q = nunits / grid;
+    a.mv.units_r = nunits % grid;
     hipLaunchKernelGGL((hexmv4_kernel<TB, LR, EPI>), dim3(grid + nlead), dim3(nw * 64), lds, st, a);
     return hipGetLastError();
 }
@@ -1851,17 +1935,26 @@ hipError_t launch_hexmv4(const HexArgs& a, hipStream_t st) {
     // waves per row-block: the largest power of two <= 16 / G dividing the
     // chunk count (so every wave has the same number of chunks per unit)
     const int G = paired ? 2 : 1;
-    int wr = kMv4MaxWaves / G;
-    while (wr > 1 && nc % wr != 0) wr >>= 1;
+    int wr = kMv4MaxWaves / G, wr_log2 = 4 - (G - 1);
+    while (wr > 1 && nc % wr != 0) {
+        wr >>= 1;
+        wr_log2--;
+    }
     const int nw = wr * G;
+    HexArgs ap = a;   // with the launch plan
+    ap.mv.P = nc / wr;
+    ap.mv.wr_log2 = wr_log2;
+    ap.mv.nunits = nunits;
+    ap.mv.ub1 = (a.seg[0].rows + 15) / 16;
+    ap.mv.ub2 = ap.mv.ub1 + (a.nseg > 1 ? (a.seg[1].rows + 15) / 16 : 0);
     const size_t xbytes = (size_t)G * nc * 512;   // every wave's own chunks of x
     // the shared-codebook kernels are specialised on the epilogue as well
 #define GSD_MV4(T, E)                                                                           \
     {                                                                                           \
         const size_t lds = xbytes + (T == 0 ? (size_t)tab_bytes : 0);                           \
-        if (!lr) return launch_hexmv4_t<T, 0, E>(a, st, nw, lds, nunits, 0);                    \
-        if (inblock) return launch_hexmv4_t<T, 1, E>(a, st, nw, lds, nunits, 0);                \
-        return launch_hexmv4_t<T, 2, -1>(a, st, nw, lds, nunits, nlead);                        \
+        if (!lr) return launch_hexmv4_t<T, 0, E>(ap, st, nw, lds, nunits, 0);                   \
+        if (inblock) return launch_hexmv4_t<T, 1, E>(ap, st, nw, lds, nunits, 0);               \
+        return launch_hexmv4_t<T, 2, -1>(ap, st, nw, lds, nunits, nlead);                       \
     }
 #define GSD_MV4E(T)                                          \
     switch (a.epilogue) {                                    \
@@ -2047,6 +2140,34 @@ hipError_t launch_fill_u32(unsigned* p, unsigned v, size_t n, hipStream_t st) {
 hipError_t launch_unpack(const uint8_t* codes, int64_t n, int radius, int32_t* idx, int8_t* r01, hipStream_t st) {
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(unpack_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, codes, n, radius, idx, r01);
+    return hipGetLastError();
+}
+
+// Codes of a tiled tensor back in file order (u8 [rows][cols / 2]), decoded
+// with the tile helpers the matvec kernels use: one wave per tile.
+__global__ void __launch_bounds__(64) tile_codes_kernel(const uint4* codes_t, int rows, int cols, int n_pts,
+                                                        uint8_t* out) {
+    const int lane = threadIdx.x;
+    const int nc = (cols + 127) >> 7, half = cols >> 1;
+    const int rb = (int)blockIdx.x / nc, c = (int)blockIdx.x % nc;
+    const bool b7 = n_pts <= 128;
+    const unsigned char* tile = reinterpret_cast<const unsigned char*>(codes_t) + ((size_t)rb * nc + c) * tile_bytes(b7);
+    const uint4 q = tile_load(tile + tile_lane_off(b7, lane));
+    uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    if (b7) align7(w, (uint32_t)(lane & 1) * 16u);
+    const int row = rb * 16 + (lane & 15);
+    if (row >= rows) return;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const int p = 64 * c + (j < 8 ? 8 * (lane >> 4) + j : 32 + 8 * (lane >> 4) + (j - 8));
+        if (p < half) out[(size_t)row * half + p] = (uint8_t)code_of(w, j, b7);
+    }
+}
+
+hipError_t launch_tile_codes(const HexSeg& s, int cols, uint8_t* out, hipStream_t st) {
+    if (!s.codes_t || !out || s.rows <= 0 || cols <= 0 || cols % 64) return hipErrorInvalidValue;
+    const size_t tiles = (size_t)((s.rows + 15) / 16) * ((cols + 127) / 128);
+    hipLaunchKernelGGL(tile_codes_kernel, dim3((unsigned)tiles), dim3(64), 0, st, s.codes_t, s.rows, cols, s.n_pts, out);
     return hipGetLastError();
 }
 

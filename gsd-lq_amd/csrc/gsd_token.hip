@@ -192,21 +192,25 @@ __device__ __forceinline__ void lin_phase(CArgs* a, const LinDesc& D, TokSmem<TB
     // weight ring: kRing chunk loads in flight per wave, the first ones issued
     // before the input vector is waited for (the cursor clamps to the last
     // unit, so loads past a wave's last step stay in bounds)
+    // code tiles: 7-bit for codebooks of at most 128 points
+    constexpr bool kB7 = TB <= 128;
+    constexpr int kTileB = kB7 ? kTile7 : kTileU8;
+    const uint32_t lof = tile_lane_off(kB7, lane);
     int lk = 0, lj = 0;
-    const uint4* lcb = nullptr;
+    const unsigned char* lcb = nullptr;
     const uint32_t* lsb = nullptr;
     auto lset = [&](int k) {
         const int uu = min(b + k * nblk, nunits - 1);
         const int g = seg_of(uu);
         const int rb = paired ? uu : uu - ubase(g);
         CSeg* sg = segp(g);
-        lcb = sg->codes_t + (size_t)rb * nc * 64;
+        lcb = reinterpret_cast<const unsigned char*>(sg->codes_t) + (size_t)rb * nc * kTileB;
         lsb = sg->scales_t + (size_t)rb * nc * 16;
     };
     const int wrl = active ? wr : 0;   // inactive waves load (and drop) in-bounds chunks
     auto lissue = [&](uint4& cw, uint32_t& sw) {
         const int c = wrl + lj * WR;
-        cw = lcb[c * 64 + lane];
+        cw = tile_load(lcb + (size_t)c * kTileB + lof);
         sw = lsb[c * 16 + (lane & 15)];
         if (++lj == P) {
             lj = 0;
@@ -475,9 +479,11 @@ __device__ __forceinline__ void lin_phase(CArgs* a, const LinDesc& D, TokSmem<TB
 
     const uint32_t lane_off = (uint32_t)lane * 4u;
     const int m = lane & 15, lg = lane >> 4;
+    const uint32_t sh7 = (uint32_t)(lane & 1) * 16u;
     auto step = [&](int c, const uint4 cw, const uint32_t sw, float& acc) {
         const unsigned char* tb = reinterpret_cast<const unsigned char*>(sm.stab);
-        const uint32_t w4[4] = {cw.x, cw.y, cw.z, cw.w};
+        uint32_t w4[4] = {cw.x, cw.y, cw.z, cw.w};
+        if constexpr (kB7) align7(w4, sh7);
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             float4v d = {0.f, 0.f, 0.f, 0.f};
@@ -486,11 +492,10 @@ __device__ __forceinline__ void lin_phase(CArgs* a, const LinDesc& D, TokSmem<TB
                 const uint4 xq = X[(((c * 2 + h) * 2 + t) * 4 + lg) * 2 + (m & 1)];
                 u32x4v aw;
                 aw[0] = xq.x; aw[1] = xq.y; aw[2] = xq.z; aw[3] = xq.w;
-                const uint32_t w = w4[2 * h + t];
                 u32x4v bw;
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    const uint32_t addr = __builtin_amdgcn_perm(w, lane_off, 0x0C0C0400u + (e << 8));
+                    const uint32_t addr = code_addr(w4, 4 * (2 * h + t) + e, lane_off, kB7);
                     bw[e] = *reinterpret_cast<const uint32_t*>(tb + addr);
                 }
                 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, aw), __builtin_bit_cast(half8v, bw),

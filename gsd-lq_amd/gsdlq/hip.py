@@ -43,6 +43,7 @@ SIGNATURES = {
     "gsdh_generate_greedy": [vp, vp, i32, i32, i32, vp, vp],
     "gsdh_model_run_linear": [vp, i32, i32],
     "gsdh_model_matmul": [vp, i32, i32, vp, i32, vp],
+    "gsdh_model_read_codes": [vp, i32, i32, vp],
     "gsdh_model_capture_begin": [vp],
     "gsdh_model_capture_end": [vp, ctypes.POINTER(vp)],
     "gsdh_graph_launch": [vp, vp, i32],

@@ -49,10 +49,11 @@ class SynthSpec:
     lr_iters: int = 2
     seed: int = 0
     sigma: float = 0.02
+    codebook_radius: Optional[int] = None   # overrides the mode's radius (1..8)
 
     @property
     def radius(self) -> int:
-        return MODES[self.mode]["radius"]
+        return MODES[self.mode]["radius"] if self.codebook_radius is None else int(self.codebook_radius)
 
     @property
     def rank(self) -> int:

@@ -184,6 +184,15 @@ int gsdh_generate_greedy(gsdh_model* m, const int* prompt, int n_prompt, int sta
  * calls (so a first call of a size is not graph-capturable). */
 int gsdh_model_matmul(gsdh_model* m, int layer, int slot, const uint16_t* X, int M, float* Y);
 
+/* The codes of packed tensor (layer, slot) as the device holds them, decoded
+ * back to the file's u8 [rows][cols/2] order on the device by the same tile
+ * decoding the matvec kernels use (one byte per code for radius 7-8, seven
+ * bits for radius <= 6) and copied to host `codes_out` (rows*cols/2 bytes);
+ * synchronous.  A check that decoding is bit-exact (the reference reads the
+ * u8 codes directly, run_gpu_native_chat.py:806, gsd_lq_cpu_runtime.py:191;
+ * no counterpart entry point). */
+int gsdh_model_read_codes(gsdh_model* m, int layer, int slot, uint8_t* codes_out);
+
 /* Benchmark hook: runs the model's matvec launches of `layer` (mask bit i =
  * launch i of {qkv, o, gate+up, down}) on the model stream with the current
  * activations, without attention or synchronisation. */

@@ -178,7 +178,7 @@ class OracleModel:
         self.max_seq_len = max_seq_len
         self.rope_interleaved = rope_interleaved
         self.embed = np.asarray(source.dense("token_embd.weight", np.float16)).astype(np.float32)
-        self.tables = {r: codebook(r) for r in (6, 8)}
+        self.tables = {r: codebook(r) for r in range(1, 9)}
         self.d16 = np.zeros(2, dtype=np.uint16)
         self.d32 = np.zeros(1, dtype=np.float32)
 

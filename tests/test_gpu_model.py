@@ -85,6 +85,53 @@ def test_model_stepwise_vs_oracle(mode, kpr, il, shape, engine):
     gpu.close()
 
 
+CODE_SHAPES = [
+    ("precision", dict()),
+    ("turbo", dict()),
+    # ragged: down has 1344 columns (a half-filled last chunk), lm_head 1000 rows
+    ("precision", dict(n_layers=1, hidden=512, ffn=1344, n_heads=8, n_kv_heads=2, head_dim=64, vocab=1000)),
+    ("turbo", dict(n_layers=1, codebook_radius=5)),
+    ("turbo", dict(n_layers=1, codebook_radius=7)),
+]
+
+
+@pytest.mark.parametrize("mode,shape", CODE_SHAPES)
+def test_device_codes_bit_exact(mode, shape):
+    """The codes the matvec kernels decode from the device tiles (7 bits per
+    code up to radius 6, one byte for radius 7-8) equal the file's u8 codes,
+    tensor by tensor."""
+    from gsdlq import synth, hip as _hip
+    import run_gpu_native_chat as chat
+    spec = _spec(mode=mode, kinks_per_row=1, **shape)
+    banner(f"device codes bit-exact {mode} {shape}")
+    src = synth.SynthSource(spec)
+    gpu = chat.GPUMistralV2Model(src, max_seq_len=64, verbose=False)
+    names = [(f"blk.{l}.{t}.weight", l, _hip.SLOTS[t]) for l in range(spec.n_layers)
+             for t in ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")]
+    names.append(("output.weight", 0, _hip.SLOTS["output"]))
+    for name, layer, slot in names:
+        want = np.ascontiguousarray(src.hex_field(name, "codes"), dtype=np.uint8)
+        got = np.full(want.shape, 0xFF, dtype=np.uint8)
+        gpu.cl.lib.gsdh_model_read_codes(gpu._m, layer, slot, _hip.ptr(got))
+        assert np.array_equal(got, want), name
+    gpu.close()
+
+
+@pytest.mark.parametrize("radius", [5, 7])
+def test_model_generic_codebook_vs_oracle(radius):
+    """Codebooks other than radius 6 / 8 run the generic-codebook matvec
+    (7-bit tiles at radius 5, u8 tiles at radius 7), graph engine."""
+    banner(f"stepwise model radius {radius} (graph)")
+    gpu, ref = _models(_spec(mode="precision", kinks_per_row=2, codebook_radius=radius))
+    rng = np.random.default_rng(30 + radius)
+    toks = rng.integers(0, gpu.vocab_size, 10).tolist()
+    for pos, t in enumerate(toks):
+        a = gpu.forward_token(t, pos)
+        b = ref.forward_token(t, pos)
+        assert rel_l2(a, b) < 1e-3, pos
+    gpu.close()
+
+
 @pytest.mark.parametrize("k_dim", [1, 3])
 def test_model_rank_sizes_vs_oracle(k_dim):
     """Rank 1 runs the matvec's in-block projection with one row per tensor;

@@ -83,6 +83,9 @@ def _small_model(spec):
     ("precision", 2, dict(), 33),
     ("turbo", 1, dict(hidden=320, ffn=448, n_heads=5, n_kv_heads=5, head_dim=64), 5),
     ("precision", 0, dict(hidden=384, ffn=704, n_heads=6, n_kv_heads=3, head_dim=64), 200),
+    # generic-codebook kernels: radius 5 (7-bit tiles), radius 7 (u8 tiles)
+    ("turbo", 1, dict(codebook_radius=5), 20),
+    ("precision", 0, dict(codebook_radius=7), 17),
 ])
 def test_matmul_small_vs_oracle(mode, kpr, shape, M):
     from gsdlq import synth
