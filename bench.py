@@ -9,12 +9,13 @@ down + residual).  Steps rotate over `--layers` distinct packed layers
 (> 256 MB) so the Infinity Cache cannot serve the weights, and are timed with
 HIP events around a captured HIP graph on the engine's stream.
 
-value = algorithmic bytes per step / time per step (GB/s), bytes as in the
-reference format: codes + fp16 scales + row_ptr + 6 B per kink + low-rank
-factors + x (4 B/col) + y (4 B/row), each stream counted once.
+value = algorithmic bytes per step / time per step (GB/s), bytes of the
+streams a matvec must read or write once: codes in the device format (one
+byte each for radius 8, seven bits for radius <= 6) + fp16 scales + row_ptr +
+6 B per kink + low-rank factors + x (4 B/col) + y (4 B/row).
 
-Also reported: the same for Precision mode (radius 6, rank 2; the file's u8
-codes), the dominant kernel's roofline (the fused gate/up launch, 2 x
+Also reported: the same for Precision mode (radius 6: 7-bit codes, rank 2),
+the dominant kernel's roofline (the fused gate/up launch, 2 x
 14336x4096), decode attention with RoPE + K/V append at contexts 512 / 2048 /
 8192 (GB/s of K/V cache read), end-to-end greedy decode tok/s of a 32-layer
 7B-shaped model, and the reference CPU engine timed on this host's cores on a
@@ -47,10 +48,17 @@ def layer_shapes():
             "ffn_gate": (F, H), "ffn_up": (F, H), "ffn_down": (H, F)}
 
 
+def code_bytes(f):
+    """Bytes of a tensor's codes in the device format: 7 bits per code for
+    codebooks of at most 128 points (radius <= 6), one byte otherwise."""
+    n = f["codes"].size
+    return (7 * n + 7) // 8 if f["radius"] <= 6 else n
+
+
 def alg_bytes(f):
     """Algorithmic bytes of one fused matvec over packed tensor f."""
     rows, cols, k = f["rows"], f["cols"], f["k_dim"]
-    b = f["codes"].nbytes + f["scales"].nbytes + f["row_ptr"].nbytes + 6 * f["nk"]
+    b = code_bytes(f) + f["scales"].nbytes + f["row_ptr"].nbytes + 6 * f["nk"]
     if k:
         b += 2 * rows * k + 2 * k * cols + 4 * k
     return b + 4 * cols + 4 * rows
@@ -417,7 +425,7 @@ def main():
         prec = LayerBank("precision", max(3, a.layers // 2))
         pg, pms, proof = bench_linear(prec, a.steps, a.warmup)
         extra["precision"] = {"value": round(pg, 1), "unit": "GB/s", "us_per_step": round(pms * 1e3, 2),
-                              "frac_hbm": round(pg / HBM_PEAK_GBS, 4), "codes": "u8 (file layout)",
+                              "frac_hbm": round(pg / HBM_PEAK_GBS, 4), "codes": "7-bit device tiles (radius 6)",
                               "gate_up_GBs": proof["achieved"], "bytes_per_step": prec.layer_bytes[0]}
         log(f"precision layer set: {pg:.1f} GB/s")
         if not a.no_decode:

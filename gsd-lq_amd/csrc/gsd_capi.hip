@@ -911,14 +911,16 @@ int gsdh_model_matmul(gsdh_model* m, int layer, int slot, const uint16_t* X, int
 
 int gsdh_model_run_linear(gsdh_model* m, int layer, int mask) {
     if (layer < 0 || layer >= m->c.n_layers) return fail(-1, "run_linear: layer %d", layer);
-    // a sequence of its own: its publication words (if any) start at zero
+    // a sequence of its own: its publication words (only launches with a rank
+    // above 2 publish their projections; smaller ranks are formed in every
+    // block) start at zero
     static const int slots[4][2] = {{GSDH_Q, GSDH_V}, {GSDH_O, GSDH_O}, {GSDH_GATE, GSDH_UP}, {GSDH_DOWN, GSDH_DOWN}};
-    bool lowrank = false;
+    bool publish = false;
     for (int i = 0; i < 4; i++)
         if (mask & (1 << i))
-            for (int s = slots[i][0]; s <= slots[i][1]; s++) lowrank = lowrank || m->slot(layer, s).k > 0;
+            for (int s = slots[i][0]; s <= slots[i][1]; s++) publish = publish || m->slot(layer, s).k > 2;
     m->pub_next = 0;
-    if (lowrank) HIPCHK(launch_fill_u32((unsigned*)m->pub, 0u, 2 * (size_t)4 * kLeadMax, m->stream));
+    if (publish) HIPCHK(launch_fill_u32((unsigned*)m->pub, 0u, 2 * (size_t)4 * kLeadMax, m->stream));
     return issue_linear(m, layer, mask);
 }
 

@@ -1020,6 +1020,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     __shared__ float lpre[EPI == kEpiResidual || EPI < 0 ? kMv4PreUnits : 1][16];
     __shared__ float2 lcs[EPI == kEpiRopeKV || EPI < 0 ? kMv4PreUnits : 1][16];
     __shared__ uint32_t lup[LR > 0 ? kMv4PreUnits : 1][2][16];
+    __shared__ float lsk[2 * kMaxSeg];   // LR == 1: S[j] of segment g at 2 g + j
     extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
 
     // wid in a scalar register: the segment selections below (seg_of) then
@@ -1173,16 +1174,6 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     for (int r = 0; r < kVS; r++)
         vrow[r] = ((vmask >> r) & 1u) ? kseg[slot_seg(r)].Vt + (size_t)slot_row(r) * cols0
                                       : reinterpret_cast<const uint16_t*>(a.x);
-    // S[j] of each slot, read with x as vector loads (a lane offset the
-    // compiler cannot prove uniform): they land with x, and take no scalar
-    // registers, of which the prologue has none to spare
-    float sv[kVS];
-    if constexpr (LR == 1) {
-        int z;   // a zero the compiler cannot prove uniform: loads through it are vector loads
-        __asm__ volatile("v_mov_b32 %0, 0" : "=v"(z));
-#pragma unroll
-        for (int r = 0; r < kVS; r++) sv[r] = (((vmask >> r) & 1u) ? kseg[slot_seg(r)].S + slot_row(r) : a.x)[z];
-    }
     uint32_t vt[kVS][kXP];
     float dk[kVS];
 #pragma unroll
@@ -1264,6 +1255,11 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
         ecs[k] = make_float2(1.f, 0.f);
         eup[k][0] = eup[k][1] = 0u;
     }
+    float esk = 0.f;   // LR == 1: lane 2 g + j of wave 0 holds S[j] of segment g
+    if (LR == 1 && wid == 0 && lane < 2 * kMaxSeg && ((emask >> lane) & 1u)) {
+        const float* sp = lane < 2 ? kseg[0].S : (lane < 4 ? kseg[1].S : kseg[2].S);
+        esk = sp[lane & 1];
+    }
     if (wid == 0 && lane < 16) {
 #pragma unroll
         for (int k = 0; k < kMv4PreUnits; k++) {
@@ -1337,6 +1333,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
 
     xfirst(0);
     if (wid == 0 && lane < 16) {   // x has landed, and with it the epilogue inputs
+        if (LR == 1 && lane < 2 * kMaxSeg) lsk[lane] = esk;
 #pragma unroll
         for (int k = 0; k < kMv4PreUnits; k++) {
             if constexpr (kHasPre) lpre[k][lane] = epre[k];
@@ -1355,16 +1352,22 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     // shuffles cost 16 waves x 6 steps per value
     ss = wave_sum_valu(ss);
     mx = wave_max_valu(mx);
-    if constexpr (LR == 1) {
-#pragma unroll
-        for (int r = 0; r < kVS; r++)
-            if ((vmask >> r) & 1u) dk[r] = wave_sum_valu(dk[r]);
-    }
     if (lane == 0) ssq[wid] = ss;
     if constexpr (LR == 1) {
-        if (lane == 0) {
-#pragma unroll
-            for (int r = 0; r < kVS; r++) vtp[r][wid] = dk[r] * sv[r];   // unused slots: never read
+        // the slots' partial sums reduced together: the 32-lane swaps pair
+        // slots, the 16-lane swaps put one slot in each 16-lane row, and one
+        // DPP row sum finishes them (unused slots hold values nobody reads)
+        if constexpr (kVS == 2) {
+            const float t = swap_add32(dk[0], dk[1], false);   // lanes 0-31: slot 0, 32-63: slot 1
+            const float u = row16_sum(swap_add16(t, t));
+            if ((lane & 31) == 0) vtp[lane >> 5][wid] = u;
+        } else {
+            const float t0 = swap_add32(dk[0], dk[1], false), t1 = swap_add32(dk[2], dk[3], false);
+            const float t2 = swap_add32(dk[4], dk[5], false);
+            const float u0 = row16_sum(swap_add16(t0, t1));   // rows 0-3: slots 0, 2, 1, 3
+            const float u1 = row16_sum(swap_add16(t2, t2));   // rows 0-1: slot 4, rows 2-3: slot 5
+            if ((lane & 15) == 0) vtp[((lane >> 4) & 1) * 2 + (lane >> 5)][wid] = u0;
+            if ((lane & 31) == 0) vtp[4 + (lane >> 5)][wid] = u1;
         }
     }
     // power-of-two scale putting the wave's largest |u|, |v| near
@@ -1434,7 +1437,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
             }
             if constexpr (LR == 1) {
                 // first unit end: rank-k values of the segments without tmp_k,
-                // inv * (sum of the S-scaled partials of the waves covering x)
+                // S[j] * inv * (sum of the partials of the waves covering x)
                 // (gsd_lq_cpu_engine.c:110-127); lane l reads wave l's partial
                 if (!(have & 0x100u)) {
 #pragma unroll
@@ -1443,7 +1446,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                         if (r < kVS && ((emask >> e) & 1u)) {
                             // (lanes 0-15 are one DPP row, all active here)
                             const float v = row16_sum(lane < WR ? vtp[r][w0 + lane] : 0.f);
-                            tkl[e >> 1][e & 1] = v * inv;
+                            tkl[e >> 1][e & 1] = lsk[e] * (v * inv);
                         }
                     }
                     have |= 0x100u;
