@@ -585,21 +585,25 @@ __global__ void rope_kv_kernel(float* q, const float* k, const float* v, const R
 
 constexpr int kAttnStage = 8192;   // floats of LDS staging for the merge (32 KB)
 
-template <int HD, int G>
-__global__ void __launch_bounds__(256) attn_kernel(const AttnArgs a) {
+// NW waves per block: 4 for split contexts (the merge below is written for
+// 256 threads), 16 for one split (contexts below 256 positions: a block per
+// KV head does all the work, and 16 waves spread its arithmetic over the
+// CU's four SIMDs instead of one wave each)
+template <int HD, int G, int NW>
+__global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
     constexpr int LPP = HD / 8;          // lanes per position
     constexpr int PPW = 64 / LPP;        // positions per wave per step
-    constexpr int PPB = 4 * PPW;         // positions per block per step
+    constexpr int PPB = NW * PPW;        // positions per block per step
     // steps whose loads are issued together: a whole chunk (256 positions at
     // most) of K and of V for HD <= 128, so one block has its 128 KB in
     // flight at once (a decode block is alone on its CU: it is latency, not
     // bandwidth, that a shallow issue depth runs into)
     constexpr int UNR = 256 / PPB < 16 ? 256 / PPB : 16;
     __shared__ float sc[G][256];
-    __shared__ float part[4][G][HD];
+    __shared__ float part[NW][G][HD];
     __shared__ float ml[2][G];
-    __shared__ float lsp[1][256];   // merging block: every split's exp-sum
-    __shared__ float stage[kAttnStage];   // merging block: a batch of the splits' outputs
+    __shared__ float lsp[1][NW == 4 ? 256 : 1];           // merging block: every split's exp-sum
+    __shared__ float stage[NW == 4 ? kAttnStage : 1];     // merging block: a batch of the splits' outputs
 
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int sub = lane % LPP, prow = lane / LPP;
@@ -656,6 +660,7 @@ __global__ void __launch_bounds__(256) attn_kernel(const AttnArgs a) {
         if (s0 > 0) kload(s0);
 #pragma unroll
         for (int u = 0; u < UNR; u++) {
+            if ((s0 + u) * PPB >= cn) break;   // steps past the context (their loads were clamped)
             const int tl = (s0 + u) * PPB + wid * PPW + prow;
             float kf[8];
             unpack8(kw[u], kf);
@@ -670,8 +675,8 @@ __global__ void __launch_bounds__(256) attn_kernel(const AttnArgs a) {
         }
     }
     __syncthreads();
-    // phase B: per head max and exp-sum over the chunk (wave w: heads w, w+4)
-    for (int g = wid; g < G; g += 4) {
+    // phase B: per head max and exp-sum over the chunk (wave w: heads w, w + NW, ...)
+    for (int g = wid; g < G; g += NW) {
         float m = -INFINITY;
         for (int i = lane; i < cn; i += 64) m = fmaxf(m, sc[g][i]);
         m = wave_allmax(m);
@@ -721,13 +726,28 @@ __global__ void __launch_bounds__(256) attn_kernel(const AttnArgs a) {
     __syncthreads();
     const int group_base = kvh * G;
     if (nsplit == 1) {
-        for (int i = tid; i < G * HD; i += 256) {
+        for (int i = tid; i < G * HD; i += NW * 64) {
             const int g = i / HD, d = i % HD;
-            const float o = (part[0][g][d] + part[1][g][d]) + (part[2][g][d] + part[3][g][d]);
+            float o;
+            if constexpr (NW == 4) {
+                o = (part[0][g][d] + part[1][g][d]) + (part[2][g][d] + part[3][g][d]);
+            } else {
+                float q[NW / 4];
+#pragma unroll
+                for (int w = 0; w < NW / 4; w++)
+                    q[w] = (part[4 * w][g][d] + part[4 * w + 1][g][d]) + (part[4 * w + 2][g][d] + part[4 * w + 3][g][d]);
+                o = q[0];
+#pragma unroll
+                for (int w = 1; w < NW / 4; w++) o += q[w];
+            }
             a.out[(size_t)(group_base + g) * HD + d] = o * (1.0f / ml[1][g]);
         }
         return;
     }
+    if constexpr (NW != 4) {   // launched for one split only
+        if (tid == 0 && a.err) *a.err = 1u;
+        return;
+    } else {
     // partials [kvh][split][g][2+HD] as epoch-tagged words (every block, all
     // G heads); query head g is merged by the block of split nsplit - 1 - g
     // (g mod nsplit when there are fewer splits than heads): no merge launch,
@@ -844,6 +864,7 @@ __global__ void __launch_bounds__(256) attn_kernel(const AttnArgs a) {
         if (tid < HD) a.out[(size_t)(group_base + g) * HD + tid] = O / L;
     }
     if (back == 0 && tid == 0) a.counters[kvh] = ep;   // the next launch's epoch base (stream order)
+    }
 }
 
 __global__ void embed_kernel(const uint16_t* embed, const int* token, float* x, int hidden,
@@ -2102,13 +2123,19 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
     if (a.max_splits < 1 || a.max_splits > 256 || a.chunk > 256 || !a.counters) return hipErrorInvalidValue;
     const dim3 grid(a.n_kv, a.max_splits);
     const int G = a.n_heads / a.n_kv;
-#define GSD_ATTN_G(HD)                                                                          \
-    switch (G) {                                                                                \
-        case 1: hipLaunchKernelGGL((attn_kernel<HD, 1>), grid, dim3(256), 0, st, a); break;     \
-        case 2: hipLaunchKernelGGL((attn_kernel<HD, 2>), grid, dim3(256), 0, st, a); break;     \
-        case 4: hipLaunchKernelGGL((attn_kernel<HD, 4>), grid, dim3(256), 0, st, a); break;     \
-        case 8: hipLaunchKernelGGL((attn_kernel<HD, 8>), grid, dim3(256), 0, st, a); break;     \
-        default: return hipErrorInvalidValue;                                                   \
+    // one split (the whole context in one block per KV head): 16 waves, for
+    // up to 4 query heads per KV head (8 would not fit the registers of 16)
+    const bool one = a.max_splits == 1;
+#define GSD_ATTN_L(HD, GG)                                                                            \
+    if (GG <= 4 && one) hipLaunchKernelGGL((attn_kernel<HD, GG, GG <= 4 ? 16 : 4>), grid, dim3(GG <= 4 ? 1024 : 256), 0, st, a); \
+    else hipLaunchKernelGGL((attn_kernel<HD, GG, 4>), grid, dim3(256), 0, st, a);
+#define GSD_ATTN_G(HD)                                          \
+    switch (G) {                                                \
+        case 1: GSD_ATTN_L(HD, 1) break;                        \
+        case 2: GSD_ATTN_L(HD, 2) break;                        \
+        case 4: GSD_ATTN_L(HD, 4) break;                        \
+        case 8: GSD_ATTN_L(HD, 8) break;                        \
+        default: return hipErrorInvalidValue;                   \
     }
     switch (a.hd) {
         case 64: GSD_ATTN_G(64) break;
@@ -2117,6 +2144,7 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
         default: return hipErrorInvalidValue;
     }
 #undef GSD_ATTN_G
+#undef GSD_ATTN_L
     return hipGetLastError();
 }
 
