@@ -1959,7 +1959,13 @@ hipError_t launch_hexmv4(const HexArgs& a, hipStream_t st) {
     // waves per row-block: the largest power of two <= 16 / G dividing the
     // chunk count (so every wave has the same number of chunks per unit)
     const int G = paired ? 2 : 1;
-    int wr = kMv4MaxWaves / G, wr_log2 = 4 - (G - 1);
+    // 8 waves instead of 16 when every block has one unit and the wave's
+    // chunks still fit one batch of x loads (o: 4096 x 4096): the prologue,
+    // which every wave runs and four waves per SIMD issue in turn, then
+    // reaches the code loads sooner (measured: o 7.6 -> 6.7 us); two units or
+    // more per block (q/k/v) measured slower
+    const bool few = nunits <= device_cu_count() && nc <= 64;
+    int wr = (few ? kMv4MaxWaves / 2 : kMv4MaxWaves) / G, wr_log2 = (few ? 3 : 4) - (G - 1);
     while (wr > 1 && nc % wr != 0) {
         wr >>= 1;
         wr_log2--;
