@@ -1963,7 +1963,9 @@ hipError_t launch_hexmv4(const HexArgs& a, hipStream_t st) {
     // chunks still fit one batch of x loads (o: 4096 x 4096): the prologue,
     // which every wave runs and four waves per SIMD issue in turn, then
     // reaches the code loads sooner (measured: o 7.6 -> 6.7 us); two units or
-    // more per block (q/k/v) measured slower
+    // more per block (q/k/v) measured slower, and so did down with 8 waves
+    // and all its x in one batch (8 waves x 4 steps hold half the bytes in
+    // flight that a 31 MB launch needs at the HBM rate)
     const bool few = nunits <= device_cu_count() && nc <= 64;
     int wr = (few ? kMv4MaxWaves / 2 : kMv4MaxWaves) / G, wr_log2 = (few ? 3 : 4) - (G - 1);
     while (wr > 1 && nc % wr != 0) {
