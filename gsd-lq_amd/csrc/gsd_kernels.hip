@@ -879,17 +879,25 @@ __global__ void __launch_bounds__(1024) argmax_kernel(const float* logits, int n
                                                       float* gen_margin, int advance) {
     __shared__ Top2 sw[16];
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    // the step state thread 0 updates at the end, read before the logits (a
+    // read there would cost one more memory round trip)
+    int c0 = 0, p0 = 0;
+    if (tid == 0) {
+        c0 = st->gen_count;
+        p0 = st->pos;
+    }
     Top2 t{-INFINITY, -INFINITY, 0x7FFFFFFF};
-    // 16 independent coalesced loads per thread per round
-    for (int base = tid; base < n; base += 1024 * 16) {
-        float v[16];
+    // 32 independent coalesced loads per thread per round: one round for a
+    // 32768-entry vocabulary
+    for (int base = tid; base < n; base += 1024 * 32) {
+        float v[32];
 #pragma unroll
-        for (int u = 0; u < 16; u++) {
+        for (int u = 0; u < 32; u++) {
             const int i = base + u * 1024;
             v[u] = i < n ? logits[i] : -INFINITY;
         }
 #pragma unroll
-        for (int u = 0; u < 16; u++) {
+        for (int u = 0; u < 32; u++) {
             const int i = base + u * 1024;
             if (i < n) t = merge(t, Top2{clean(v[u]), -INFINITY, i});
         }
@@ -907,12 +915,11 @@ __global__ void __launch_bounds__(1024) argmax_kernel(const float* logits, int n
         const float margin = r.v1 - r.v2;
         st->token = r.i1;
         if (gen_tok) {
-            const int c = st->gen_count;
-            gen_tok[c] = r.i1;
-            gen_margin[c] = margin;
-            st->gen_count = c + 1;
+            gen_tok[c0] = r.i1;
+            gen_margin[c0] = margin;
+            st->gen_count = c0 + 1;
         }
-        if (advance) st->pos = st->pos + 1;
+        if (advance) st->pos = p0 + 1;
         st->margin_bits = __float_as_int(margin);
     }
 }
