@@ -585,10 +585,10 @@ __global__ void rope_kv_kernel(float* q, const float* k, const float* v, const R
 
 constexpr int kAttnStage = 8192;   // floats of LDS staging for the merge (32 KB)
 
-// NW waves per block: 4 for split contexts (the merge below is written for
-// 256 threads), 16 for one split (contexts below 256 positions: a block per
-// KV head does all the work, and 16 waves spread its arithmetic over the
-// CU's four SIMDs instead of one wave each)
+// NW waves per block (NT = 64 NW threads): 16 spread a block's arithmetic
+// over the CU's four SIMDs (one split: a block per KV head does all the work;
+// split contexts: the partial sums and the merge); 4 where 16 would not fit
+// the registers (8 query heads per KV head)
 template <int HD, int G, int NW>
 __global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
     constexpr int LPP = HD / 8;          // lanes per position
@@ -602,8 +602,9 @@ __global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
     __shared__ float sc[G][256];
     __shared__ float part[NW][G][HD];
     __shared__ float ml[2][G];
-    __shared__ float lsp[1][NW == 4 ? 256 : 1];           // merging block: every split's exp-sum
-    __shared__ float stage[NW == 4 ? kAttnStage : 1];     // merging block: a batch of the splits' outputs
+    constexpr int NT = NW * 64;
+    __shared__ float lsp[1][256];          // merging block: every split's exp-sum
+    __shared__ float stage[kAttnStage];    // merging block: a batch of the splits' outputs
 
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int sub = lane % LPP, prow = lane / LPP;
@@ -725,29 +726,21 @@ __global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
     }
     __syncthreads();
     const int group_base = kvh * G;
+    // the block's output for head g, dim d: its waves' partial sums in a fixed order
+    auto psum = [&](int g, int d) {
+        float o = (part[0][g][d] + part[1][g][d]) + (part[2][g][d] + part[3][g][d]);
+#pragma unroll
+        for (int w = 4; w < NW; w += 4)
+            o += (part[w][g][d] + part[w + 1][g][d]) + (part[w + 2][g][d] + part[w + 3][g][d]);
+        return o;
+    };
     if (nsplit == 1) {
-        for (int i = tid; i < G * HD; i += NW * 64) {
+        for (int i = tid; i < G * HD; i += NT) {
             const int g = i / HD, d = i % HD;
-            float o;
-            if constexpr (NW == 4) {
-                o = (part[0][g][d] + part[1][g][d]) + (part[2][g][d] + part[3][g][d]);
-            } else {
-                float q[NW / 4];
-#pragma unroll
-                for (int w = 0; w < NW / 4; w++)
-                    q[w] = (part[4 * w][g][d] + part[4 * w + 1][g][d]) + (part[4 * w + 2][g][d] + part[4 * w + 3][g][d]);
-                o = q[0];
-#pragma unroll
-                for (int w = 1; w < NW / 4; w++) o += q[w];
-            }
-            a.out[(size_t)(group_base + g) * HD + d] = o * (1.0f / ml[1][g]);
+            a.out[(size_t)(group_base + g) * HD + d] = psum(g, d) * (1.0f / ml[1][g]);
         }
         return;
     }
-    if constexpr (NW != 4) {   // launched for one split only
-        if (tid == 0 && a.err) *a.err = 1u;
-        return;
-    } else {
     // partials [kvh][split][g][2+HD] as epoch-tagged words (every block, all
     // G heads); query head g is merged by the block of split nsplit - 1 - g
     // (g mod nsplit when there are fewer splits than heads): no merge launch,
@@ -757,9 +750,9 @@ __global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
     unsigned long long* wsk = a.ws + (size_t)kvh * a.max_splits * G * (2 + HD);
     {
         unsigned long long* wsb = wsk + (size_t)split * G * (2 + HD);
-        for (int i = tid; i < G * HD; i += 256) {
+        for (int i = tid; i < G * HD; i += NT) {
             const int g = i / HD, d = i % HD;
-            const float o = (part[0][g][d] + part[1][g][d]) + (part[2][g][d] + part[3][g][d]);
+            const float o = psum(g, d);
             __hip_atomic_store(wsb + g * (2 + HD) + 2 + d, tag | __float_as_uint(o), __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -796,7 +789,7 @@ __global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
         return (v >> 32) == ep ? __uint_as_float((unsigned)v) : wait_word(w);
     };
     constexpr int SB = kAttnStage / HD;       // splits per staging batch
-    constexpr int MAXI = kAttnStage / 256;    // staged words per thread
+    constexpr int MAXI = kAttnStage / NT;     // staged words per thread
     for (int g = back; g < G; g += nsplit) {
         __syncthreads();   // (LDS reuse across heads)
         // one round trip: the (max, sum) words of every split and the first
@@ -806,7 +799,7 @@ __global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
             const int sn = min(SB, nsplit - s0);
 #pragma unroll
             for (int j = 0; j < MAXI; j++) {
-                const int i = tid + 256 * j, sp = s0 + i / HD, d = i % HD;
+                const int i = tid + NT * j, sp = s0 + i / HD, d = i % HD;
                 v[j] = ld(i < sn * HD ? (sp * G + g) * (2 + HD) + 2 + d : -1);
             }
         };
@@ -814,23 +807,21 @@ __global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
             const int sn = min(SB, nsplit - s0);
 #pragma unroll
             for (int j = 0; j < MAXI; j++) {
-                const int i = tid + 256 * j, sp = s0 + i / HD, d = i % HD;
-                if (i < sn * HD)
-                    stage[i] = sp == split ? (part[0][g][d] + part[1][g][d]) + (part[2][g][d] + part[3][g][d])
-                                           : value(v[j], (sp * G + g) * (2 + HD) + 2 + d);
+                const int i = tid + NT * j, sp = s0 + i / HD, d = i % HD;
+                if (i < sn * HD) stage[i] = sp == split ? psum(g, d) : value(v[j], (sp * G + g) * (2 + HD) + 2 + d);
             }
         };
         const int wm = (tid * G + g) * (2 + HD);   // (valid for tid < nsplit)
         const unsigned long long vm = ld(tid < nsplit ? wm : -1), vl = ld(tid < nsplit ? wm + 1 : -1);
         stage_issue(0);
-        for (int sp = tid; sp < nsplit; sp += 256) {
+        for (int sp = tid; sp < nsplit; sp += NT) {
             if (sp == split) {
                 sc[0][sp] = ml[0][g];
                 lsp[0][sp] = ml[1][g];
             } else if (sp == tid) {
                 sc[0][sp] = value(vm, wm);
                 lsp[0][sp] = value(vl, wm + 1);
-            } else {   // (more than 256 splits: not launched, kept general)
+            } else {   // (more splits than threads: not launched, kept general)
                 const int w = (sp * G + g) * (2 + HD);
                 sc[0][sp] = wait_word(w);
                 lsp[0][sp] = wait_word(w + 1);
@@ -864,7 +855,6 @@ __global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
         if (tid < HD) a.out[(size_t)(group_base + g) * HD + tid] = O / L;
     }
     if (back == 0 && tid == 0) a.counters[kvh] = ep;   // the next launch's epoch base (stream order)
-    }
 }
 
 __global__ void embed_kernel(const uint16_t* embed, const int* token, float* x, int hidden,
@@ -2138,12 +2128,10 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
     if (a.max_splits < 1 || a.max_splits > 256 || a.chunk > 256 || !a.counters) return hipErrorInvalidValue;
     const dim3 grid(a.n_kv, a.max_splits);
     const int G = a.n_heads / a.n_kv;
-    // one split (the whole context in one block per KV head): 16 waves, for
-    // up to 4 query heads per KV head (8 would not fit the registers of 16)
-    const bool one = a.max_splits == 1;
-#define GSD_ATTN_L(HD, GG)                                                                            \
-    if (GG <= 4 && one) hipLaunchKernelGGL((attn_kernel<HD, GG, GG <= 4 ? 16 : 4>), grid, dim3(GG <= 4 ? 1024 : 256), 0, st, a); \
-    else hipLaunchKernelGGL((attn_kernel<HD, GG, 4>), grid, dim3(256), 0, st, a);
+    // 16 waves for up to 4 query heads per KV head (8 would not fit the
+    // registers of 16), else 4
+#define GSD_ATTN_L(HD, GG) \
+    hipLaunchKernelGGL((attn_kernel<HD, GG, GG <= 4 ? 16 : 4>), grid, dim3(GG <= 4 ? 1024 : 256), 0, st, a);
 #define GSD_ATTN_G(HD)                                          \
     switch (G) {                                                \
         case 1: GSD_ATTN_L(HD, 1) break;                        \
