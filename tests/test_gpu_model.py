@@ -147,6 +147,29 @@ def test_model_rank_sizes_vs_oracle(k_dim):
     gpu.close()
 
 
+@pytest.mark.parametrize("mode", ["turbo", "precision"])
+@pytest.mark.parametrize("shape", [
+    # gate/up: 272 units of 16 rows on 256 blocks (16 blocks with two units)
+    dict(hidden=2048, ffn=4352, n_heads=16, n_kv_heads=4, head_dim=128),
+    # q/k/v: 384 units, gate/up 288 units (7B hidden size, one layer)
+    dict(hidden=4096, ffn=4608, n_heads=32, n_kv_heads=8, head_dim=128),
+])
+def test_model_uneven_units_vs_oracle(mode, shape):
+    """Launches with more row-block units than blocks, not a multiple of them
+    (blocks with one unit more than others), graph engine."""
+    banner(f"stepwise model {mode} {shape} uneven units (graph)")
+    gpu, ref = _models(_spec(mode=mode, kinks_per_row=2, n_layers=1, vocab=1000, **shape), max_seq=64)
+    rng = np.random.default_rng(41)
+    toks = rng.integers(0, gpu.vocab_size, 8).tolist()
+    for pos, t in enumerate(toks):
+        a = gpu.forward_token(t, pos)
+        b = ref.forward_token(t, pos)
+        assert rel_l2(a, b) < 1e-3, pos
+    # the same token twice: same bits
+    assert np.array_equal(gpu.forward_token(toks[3], 3), gpu.forward_token(toks[3], 3))
+    gpu.close()
+
+
 @pytest.mark.parametrize("engine", ENGINES)
 def test_generate_greedy_matches_oracle(engine):
     banner(f"generate_greedy vs oracle ({engine})")
