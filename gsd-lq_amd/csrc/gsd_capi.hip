@@ -6,6 +6,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -16,9 +17,10 @@
 using namespace gsd;
 
 namespace {
-
 thread_local std::string g_err;
+}
 
+namespace gsd {
 int fail(int code, const char* fmt, ...) {
     char buf[512];
     va_list ap;
@@ -28,6 +30,10 @@ int fail(int code, const char* fmt, ...) {
     g_err = buf;
     return code ? code : -1;
 }
+}  // namespace gsd
+
+namespace {
+
 
 #define HIPCHK(expr)                                                                        \
     do {                                                                                    \
@@ -83,26 +89,18 @@ __attribute__((noinline)) void rope_cs(float theta, int hd, int pos, float* out 
     }
 }
 
-// Scratch of the attention twin: partial words + per-KV-head launch counters
-// (both zeroed when allocated).
-struct AttnScratch {
-    std::mutex mu;
+// Workspaces of the attention twin, one per stream (calls on different
+// streams may overlap; calls on one stream run in order): the partial words
+// and the epoch of the stream's last launch.  Every launch takes the next
+// epoch, so words a launch of another shape left behind never match.
+struct AttnWs {
     unsigned long long* ws = nullptr;
-    size_t ws_bytes = 0;
-    unsigned* counters = nullptr;
-    size_t n_counters = 0;
-} g_attn;
+    size_t bytes = 0;
+    unsigned epoch = 0;
+};
+std::mutex g_attn_mu;
+std::map<hipStream_t, AttnWs> g_attn_ws;
 
-// Positions per attention split: enough splits to spread long contexts over
-// the chip (n_kv * splits ~ 256 blocks), at least 64 and at most 256
-// positions each (256 is the kernel's LDS score buffer).
-int choose_chunk(int n_ctx, int n_kv) {
-    int c = (n_ctx * n_kv + 255) / 256;
-    c = (c + 63) / 64 * 64;
-    if (c < 64) c = 64;
-    if (c > 256) c = 256;
-    return c;
-}
 
 }  // namespace
 
@@ -222,28 +220,28 @@ int gsdh_gqa_attention(void* stream, const float* q, const uint16_t* k_cache, co
     a.q = q; a.k_cache = k_cache; a.v_cache = v_cache; a.out = attn_out; a.pos_dev = nullptr; a.pos = pos;
     a.layer = layer_idx; a.n_heads = n_heads; a.n_kv = n_kv_heads; a.hd = head_dim; a.max_seq = max_seq_len;
     a.sm_scale = sm_scale;
-    a.chunk = choose_chunk(n, n_kv_heads);
+    a.chunk = attention_chunk(n, n_kv_heads);
     a.max_splits = (n + a.chunk - 1) / a.chunk;
-    std::lock_guard<std::mutex> lk(g_attn.mu);
     const size_t need = attention_ws_bytes(n_kv_heads, a.max_splits, G, head_dim);
-    if (need > g_attn.ws_bytes) {
-        if (g_attn.ws) HIPCHK(hipFree(g_attn.ws));
-        g_attn.ws = nullptr;
-        g_attn.ws_bytes = 0;
-        HIPCHK(hipMalloc(&g_attn.ws, need));
-        HIPCHK(launch_fill_u32(reinterpret_cast<unsigned*>(g_attn.ws), 0u, need / 4, S(stream)));
-        g_attn.ws_bytes = need;
+    std::lock_guard<std::mutex> lk(g_attn_mu);
+    AttnWs& w = g_attn_ws[S(stream)];
+    if (need > w.bytes || w.epoch >= 0xFFFFFFF0u) {
+        // a larger workspace (the stream's earlier launches finish first),
+        // or the epoch about to wrap: words start at zero, epochs at 1
+        if (need > w.bytes) {
+            HIPCHK(hipStreamSynchronize(S(stream)));
+            if (w.ws) HIPCHK(hipFree(w.ws));
+            w.ws = nullptr;
+            w.bytes = 0;
+            HIPCHK(hipMalloc(&w.ws, need));
+            w.bytes = need;
+        }
+        HIPCHK(launch_fill_u32(reinterpret_cast<unsigned*>(w.ws), 0u, w.bytes / 4, S(stream)));
+        w.epoch = 0;
     }
-    if ((size_t)n_kv_heads > g_attn.n_counters) {
-        if (g_attn.counters) HIPCHK(hipFree(g_attn.counters));
-        g_attn.counters = nullptr;
-        g_attn.n_counters = 0;
-        HIPCHK(hipMalloc(&g_attn.counters, (size_t)n_kv_heads * sizeof(unsigned)));
-        HIPCHK(launch_fill_u32(g_attn.counters, 0u, (size_t)n_kv_heads, S(stream)));
-        g_attn.n_counters = (size_t)n_kv_heads;
-    }
-    a.ws = g_attn.ws;
-    a.counters = g_attn.counters;
+    a.ws = w.ws;
+    a.counters = nullptr;
+    a.epoch = ++w.epoch;
     HIPCHK(launch_attention(a, S(stream)));
     return 0;
 }
@@ -251,6 +249,13 @@ int gsdh_gqa_attention(void* stream, const float* q, const uint16_t* k_cache, co
 int gsdh_unpack_codes(void* stream, const uint8_t* codes, int64_t n, int radius, int32_t* idx_out, int8_t* r01_out) {
     if (radius < 1 || radius > 8) return fail(-1, "unpack: radius %d outside 1..8", radius);
     HIPCHK(launch_unpack(codes, n, radius, idx_out, r01_out, S(stream)));
+    return 0;
+}
+
+int gsdh_greedy_argmax(void* stream, const float* logits, int n, int* token_out, float* margin_out) {
+    if (n <= 0) return fail(-1, "argmax: n %d", n);
+    if (!logits || !token_out || !margin_out) return fail(-1, "argmax: null argument");
+    HIPCHK(launch_argmax(logits, n, nullptr, token_out, margin_out, 0, S(stream)));
     return 0;
 }
 
@@ -407,6 +412,22 @@ int issue_linear(gsdh_model* m, int l, int mask) {
     return 0;
 }
 
+// Final RMSNorm + lm_head (run_gpu_native_chat.py:962-968) and, with
+// `greedy`, the device argmax that appends the token and advances the step.
+int issue_head(gsdh_model* m, bool greedy) {
+    const auto& c = m->c;
+    HexArgs a{};
+    a.nseg = 1;
+    fill_seg(a.seg[0], m->slot(0, GSDH_LM_HEAD), m, m->logits);
+    a.x = m->x; a.norm_w = m->norm(-1, 0); a.eps = c.rms_eps; a.cols = c.hidden; a.epilogue = kEpiStore;
+    a.scale_t = 1;
+    int rc = prep_lowrank(m, a);
+    if (rc) return rc;
+    HIPCHK(launch_hexmv4(a, m->stream));
+    if (greedy) HIPCHK(launch_argmax(m->logits, c.vocab, m->st, m->gen_tok, m->gen_margin, 1, m->stream));
+    return 0;
+}
+
 // The per-token launch sequence (run_gpu_native_chat.py:892-969, fused).
 int issue_token(gsdh_model* m, bool with_head, bool short_ctx) {
     const auto& c = m->c;
@@ -436,17 +457,7 @@ int issue_token(gsdh_model* m, bool with_head, bool short_ctx) {
         rc = issue_linear(m, l, 2 | 4 | 8);
         if (rc) return rc;
     }
-    if (with_head) {
-        HexArgs a{};
-        a.nseg = 1;
-        fill_seg(a.seg[0], m->slot(0, GSDH_LM_HEAD), m, m->logits);
-        a.x = m->x; a.norm_w = m->norm(-1, 0); a.eps = c.rms_eps; a.cols = c.hidden; a.epilogue = kEpiStore;
-        a.scale_t = 1;
-        int rc = prep_lowrank(m, a);
-        if (rc) return rc;
-        HIPCHK(launch_hexmv4(a, m->stream));
-        HIPCHK(launch_argmax(m->logits, c.vocab, m->st, m->gen_tok, m->gen_margin, 1, m->stream));
-    }
+    if (with_head) return issue_head(m, true);
     return 0;
 }
 
@@ -572,7 +583,7 @@ int gsdh_model_create(const gsdh_model_config* cfg, gsdh_model** out) {
     A((void**)&m->norms, ((size_t)c.n_layers * 2 + 1) * c.hidden * 4);
     A((void**)&m->embed, (size_t)c.vocab * c.hidden * 2);
     A((void**)&m->cs, (size_t)c.max_seq_len * (c.head_dim / 2) * sizeof(float2));
-    m->chunk = choose_chunk(c.max_seq_len, c.n_kv_heads);
+    m->chunk = attention_chunk(c.max_seq_len, c.n_kv_heads);
     m->max_splits = (c.max_seq_len + m->chunk - 1) / m->chunk;
     A((void**)&m->ws, attention_ws_bytes(c.n_kv_heads, m->max_splits, c.n_heads / c.n_kv_heads, c.head_dim));
     A((void**)&m->counters, (size_t)c.n_kv_heads * 4);
@@ -644,11 +655,13 @@ int gsdh_model_destroy(gsdh_model* m) {
 }
 
 int gsdh_model_set_embedding(gsdh_model* m, const uint16_t* embed) {
+    if (m->finalized) return fail(-1, "set_embedding: the model is finalized (its token graphs hold the tensors)");
     HIPCHK(hipMemcpy(m->embed, embed, (size_t)m->c.vocab * m->c.hidden * 2, hipMemcpyHostToDevice));
     return 0;
 }
 
 int gsdh_model_set_norm(gsdh_model* m, int layer, int which, const float* w) {
+    if (m->finalized) return fail(-1, "set_norm: the model is finalized (its token graphs hold the tensors)");
     if (layer >= m->c.n_layers || which < 0 || which > 1) return fail(-1, "set_norm: layer %d which %d", layer, which);
     HIPCHK(hipMemcpy(m->norm(layer, which), w, (size_t)m->c.hidden * 4, hipMemcpyHostToDevice));
     return 0;
@@ -659,6 +672,7 @@ int gsdh_model_set_hex(gsdh_model* m, int layer, int slot, int radius, int rows,
                        const uint16_t* kink_cols, const float* kink_deltas, int64_t nk, const uint16_t* U,
                        const float* Sv, const uint16_t* Vt) {
     const auto& c = m->c;
+    if (m->finalized) return fail(-1, "set_hex: the model is finalized (its token graphs hold the tensors)");
     if (slot < 0 || slot > GSDH_LM_HEAD) return fail(-1, "set_hex: slot %d", slot);
     if (slot != GSDH_LM_HEAD && (layer < 0 || layer >= c.n_layers)) return fail(-1, "set_hex: layer %d", layer);
     const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
@@ -910,6 +924,15 @@ int gsdh_model_matmul(gsdh_model* m, int layer, int slot, const uint16_t* X, int
 }
 
 int gsdh_model_run_linear(gsdh_model* m, int layer, int mask) {
+    if (!m) return fail(-1, "run_linear: null model");
+    if (mask & ~31) return fail(-1, "run_linear: mask 0x%x", mask);
+    if (mask == 16) {   // the head alone: final norm + lm_head, no argmax
+        const bool publish = m->slot(0, GSDH_LM_HEAD).k > 2;
+        m->pub_next = 0;
+        if (publish) HIPCHK(launch_fill_u32((unsigned*)m->pub, 0u, 2 * (size_t)kLeadMax, m->stream));
+        return issue_head(m, false);
+    }
+    if (mask & 16) return fail(-1, "run_linear: the head (mask 16) runs alone");
     if (layer < 0 || layer >= m->c.n_layers) return fail(-1, "run_linear: layer %d", layer);
     // a sequence of its own: its publication words (only launches with a rank
     // above 2 publish their projections; smaller ranks are formed in every
@@ -969,5 +992,51 @@ int gsdh_graph_destroy(void* ge) {
 }
 
 void* gsdh_model_stream(gsdh_model* m) { return m ? (void*)m->stream : nullptr; }
+
+int gsdh_model_vector(gsdh_model* m, int which, int write, void* host, uint64_t nbytes) {
+    if (!m || !host) return fail(-1, "model_vector: null argument");
+    const auto& c = m->c;
+    float* d = nullptr;
+    size_t n = 0;
+    switch (which) {
+        case GSDH_VEC_X: d = m->x; n = c.hidden; break;
+        case GSDH_VEC_Q: d = m->q; n = (size_t)c.n_heads * c.head_dim; break;
+        case GSDH_VEC_K: d = m->k; n = (size_t)c.n_kv_heads * c.head_dim; break;
+        case GSDH_VEC_V: d = m->v; n = (size_t)c.n_kv_heads * c.head_dim; break;
+        case GSDH_VEC_ATTN: d = m->attn; n = (size_t)c.n_heads * c.head_dim; break;
+        case GSDH_VEC_H: d = m->h; n = c.ffn; break;
+        case GSDH_VEC_LOGITS: d = m->logits; n = c.vocab; break;
+        default: return fail(-1, "model_vector: unknown vector %d", which);
+    }
+    if (nbytes != n * 4) return fail(-1, "model_vector: %llu bytes, vector %d holds %zu", (unsigned long long)nbytes, which, n * 4);
+    HIPCHK(hipStreamSynchronize(m->stream));
+    HIPCHK(hipMemcpy(write ? (void*)d : host, write ? host : (const void*)d, nbytes,
+                     write ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost));
+    return 0;
+}
+
+int gsdh_model_set_step(gsdh_model* m, int token_id, int pos) {
+    if (!m) return fail(-1, "set_step: null model");
+    if (token_id < 0 || token_id >= m->c.vocab) return fail(-1, "set_step: token %d outside vocab %d", token_id, m->c.vocab);
+    if (pos < 0 || pos >= m->c.max_seq_len) return fail(-1, "set_step: pos %d outside 0..%d", pos, m->c.max_seq_len - 1);
+    HIPCHK(hipStreamSynchronize(m->stream));
+    StepState* h = m->st_host;
+    *h = StepState{};
+    h->token = token_id; h->pos = pos;
+    HIPCHK(hipMemcpy(m->st, h, sizeof(StepState), hipMemcpyHostToDevice));
+    return 0;
+}
+
+int gsdh_model_read_kv(gsdh_model* m, int layer, int pos, uint16_t* k_out, uint16_t* v_out) {
+    if (!m || !k_out || !v_out) return fail(-1, "read_kv: null argument");
+    const auto& c = m->c;
+    if (layer < 0 || layer >= c.n_layers) return fail(-1, "read_kv: layer %d", layer);
+    if (pos < 0 || pos >= c.max_seq_len) return fail(-1, "read_kv: pos %d outside 0..%d", pos, c.max_seq_len - 1);
+    const size_t kvd = (size_t)c.n_kv_heads * c.head_dim, off = ((size_t)layer * c.max_seq_len + pos) * kvd;
+    HIPCHK(hipStreamSynchronize(m->stream));
+    HIPCHK(hipMemcpy(k_out, m->kc + off, kvd * 2, hipMemcpyDeviceToHost));
+    HIPCHK(hipMemcpy(v_out, m->vc + off, kvd * 2, hipMemcpyDeviceToHost));
+    return 0;
+}
 
 }  // extern "C"

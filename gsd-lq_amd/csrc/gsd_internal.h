@@ -156,13 +156,31 @@ struct AttnArgs {
     // head) to the block of the last split as 64-bit words, epoch << 32 |
     // float bits, one relaxed device-scope store each: a word read with the
     // launch's epoch is that launch's value, so there is no fence and no
-    // clearing.  counters[kvh] counts the head's launches (the epoch is the
-    // count + 1); the merging block advances it.  Zero both at allocation.
+    // clearing.  Epoch source: `epoch` when nonzero (chosen by the host,
+    // different for every launch on a workspace: words left by launches of
+    // another shape then never match), else counters[kvh], the head's launch
+    // count (the epoch is the count + 1, advanced by the merging block; for
+    // graph replays of one shape).  Zero ws and counters at allocation.
     unsigned long long* ws;   // [n_kv][max_splits][group][2 + hd]
-    unsigned* counters;       // [n_kv]
+    unsigned* counters;       // [n_kv] (epoch == 0 only)
     unsigned* err;            // set to 1 when a wait for a partial runs out (may be null)
+    unsigned epoch;
 };
 hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
+// Positions per attention split for a context of n_ctx positions: enough
+// splits to spread long contexts over the chip (n_kv * splits ~ 256 blocks),
+// at least 64 and at most 256 positions each (256 is the kernel's LDS score
+// buffer).
+inline int attention_chunk(int n_ctx, int n_kv) {
+    int c = (n_ctx * n_kv + 255) / 256;
+    c = (c + 63) / 64 * 64;
+    if (c < 64) c = 64;
+    if (c > 256) c = 256;
+    return c;
+}
+// Sets the calling thread's error text (gsdh_last_error) and returns code,
+// or -1 for code 0.
+int fail(int code, const char* fmt, ...);
 size_t attention_ws_bytes(int n_kv, int max_splits, int group, int hd);
 
 // embedding row of *token_dev to fp32 x; also zeroes clear[0..nclear) (the
@@ -171,9 +189,10 @@ hipError_t launch_embed(const uint16_t* embed, const int* token_dev, float* x, i
                         unsigned long long* clear, int nclear, hipStream_t stream);
 
 // Greedy argmax with the reference's nan_to_num (gsd_lq_cpu_runtime.py:423);
-// writes token to *tok_out, margin top1-top2 to *margin_out and, when
-// gen != null, appends both to gen arrays at *gen_count and advances the
-// step state (token_dev = argmax, pos_dev += 1).
+// with a step state st it writes the token and the margin top1-top2 there
+// and, when gen_tokens != null, appends both to the gen arrays at
+// st->gen_count (advance: st->pos += 1); with st == null it writes them to
+// gen_tokens[0] and gen_margins[0] only.
 struct StepState {
     int token;
     int pos;

@@ -614,7 +614,7 @@ __global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
     const int split = blockIdx.y;
     if (split >= nsplit) return;
     const int kvh = blockIdx.x;
-    const unsigned ep0 = a.counters[kvh];   // launches of this KV head so far (used at the end)
+    const unsigned ep0 = a.epoch ? a.epoch - 1u : a.counters[kvh];   // (used at the end)
     const int t0 = split * a.chunk;
     const int t1 = min(n, t0 + a.chunk);
     const int cn = t1 - t0;
@@ -854,7 +854,7 @@ __global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
         }
         if (tid < HD) a.out[(size_t)(group_base + g) * HD + tid] = O / L;
     }
-    if (back == 0 && tid == 0) a.counters[kvh] = ep;   // the next launch's epoch base (stream order)
+    if (back == 0 && tid == 0 && !a.epoch) a.counters[kvh] = ep;   // the next launch's epoch base (stream order)
 }
 
 __global__ void embed_kernel(const uint16_t* embed, const int* token, float* x, int hidden,
@@ -872,7 +872,7 @@ __global__ void __launch_bounds__(1024) argmax_kernel(const float* logits, int n
     // the step state thread 0 updates at the end, read before the logits (a
     // read there would cost one more memory round trip)
     int c0 = 0, p0 = 0;
-    if (tid == 0) {
+    if (tid == 0 && st) {
         c0 = st->gen_count;
         p0 = st->pos;
     }
@@ -903,6 +903,11 @@ __global__ void __launch_bounds__(1024) argmax_kernel(const float* logits, int n
         Top2 r = sw[0];
         for (int w = 1; w < (int)(blockDim.x >> 6); w++) r = merge(r, sw[w]);
         const float margin = r.v1 - r.v2;
+        if (!st) {   // stand-alone call: the token and margin only
+            gen_tok[0] = r.i1;
+            gen_margin[0] = margin;
+            return;
+        }
         st->token = r.i1;
         if (gen_tok) {
             gen_tok[c0] = r.i1;
@@ -2125,7 +2130,8 @@ size_t attention_ws_bytes(int n_kv, int max_splits, int group, int hd) {
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
     // the merging block holds every split's (max, sum) in its 256-entry
     // score buffer
-    if (a.max_splits < 1 || a.max_splits > 256 || a.chunk > 256 || !a.counters) return hipErrorInvalidValue;
+    if (a.max_splits < 1 || a.max_splits > 256 || a.chunk > 256 || (!a.counters && !a.epoch) || !a.ws)
+        return hipErrorInvalidValue;
     const dim3 grid(a.n_kv, a.max_splits);
     const int G = a.n_heads / a.n_kv;
     // 16 waves for up to 4 query heads per KV head (8 would not fit the

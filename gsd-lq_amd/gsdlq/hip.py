@@ -49,6 +49,10 @@ SIGNATURES = {
     "gsdh_graph_launch": [vp, vp, i32],
     "gsdh_graph_destroy": [vp],
     "gsdh_graph_time": [vp, vp, i32, ctypes.POINTER(f32)],
+    "gsdh_greedy_argmax": [vp, vp, i32, vp, vp],
+    "gsdh_model_vector": [vp, i32, i32, vp, u64],
+    "gsdh_model_set_step": [vp, i32, i32],
+    "gsdh_model_read_kv": [vp, i32, i32, vp, vp],
 }
 RESTYPES = {"gsdh_model_device_bytes": (u64, [vp]), "gsdh_model_stream": (vp, [vp]),
             "gsdh_model_engine": (i32, [vp]),
@@ -60,6 +64,8 @@ class GsdModelConfig(ctypes.Structure):
                 ("n_kv_heads", i32), ("head_dim", i32), ("vocab", i32), ("max_seq_len", i32),
                 ("rope_interleaved", i32), ("rms_eps", f32), ("rope_theta", f32)]
 
+
+VECTORS = {"x": 0, "q": 1, "k": 2, "v": 3, "attn": 4, "h": 5, "logits": 6}
 
 SLOTS = {"attn_q": 0, "attn_k": 1, "attn_v": 2, "attn_output": 3, "ffn_gate": 4, "ffn_up": 5,
          "ffn_down": 6, "output": 7}

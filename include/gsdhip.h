@@ -101,6 +101,13 @@ int gsdh_gqa_attention(void* stream, const float* q, const uint16_t* k_cache,
 int gsdh_unpack_codes(void* stream, const uint8_t* codes, int64_t n, int radius,
                       int32_t* idx_out, int8_t* r01_out);
 
+/* Greedy branch of sample_token (gsd_lq_cpu_runtime.py:422-425):
+ * nan_to_num(nan=-1e4, posinf=100, neginf=-1e4), then the first index of the
+ * maximum.  logits: device f32 [n]; writes the token to device *token_out and
+ * the top1 - top2 margin of the cleaned values to device *margin_out.  The
+ * same kernel ends every greedy step of the model context. */
+int gsdh_greedy_argmax(void* stream, const float* logits, int n, int* token_out, float* margin_out);
+
 /* ------------------------------------------------------------------------ */
 /* 2. Model context (replaces GPUMistralV2Model's device side)              */
 /* ------------------------------------------------------------------------ */
@@ -121,7 +128,8 @@ int gsdh_model_create(const gsdh_model_config* cfg, gsdh_model** out);
 int gsdh_model_destroy(gsdh_model* m);
 
 /* Dense tensors from host memory.  embed: fp16 bits [vocab, hidden];
- * norms: f32 [hidden]; layer = -1 for output_norm. */
+ * norms: f32 [hidden]; layer = -1 for output_norm.  These and
+ * gsdh_model_set_hex fail once the model is finalized. */
 int gsdh_model_set_embedding(gsdh_model* m, const uint16_t* embed_f16);
 int gsdh_model_set_norm(gsdh_model* m, int layer, int which /*0 attn, 1 ffn*/, const float* w);
 
@@ -193,10 +201,33 @@ int gsdh_model_matmul(gsdh_model* m, int layer, int slot, const uint16_t* X, int
  * no counterpart entry point). */
 int gsdh_model_read_codes(gsdh_model* m, int layer, int slot, uint8_t* codes_out);
 
-/* Benchmark hook: runs the model's matvec launches of `layer` (mask bit i =
- * launch i of {qkv, o, gate+up, down}) on the model stream with the current
- * activations, without attention or synchronisation. */
+/* Runs the model's fused matvec launches of `layer` on the model stream with
+ * the current activations, without attention or synchronisation.  Mask bit i
+ * = launch i of {qkv, o, gate+up, down}:
+ *   1: q, k, v of rmsnorm(x) * attn_norm, RoPE(q) -> q, fp16 RoPE(k) and v
+ *      appended to the cache at the step position (run_gpu_native_chat.py:
+ *      899-925);  2: x += W_o attn;  4: h = silu(W_gate x') * (W_up x') with
+ *      x' = rmsnorm(x) * ffn_norm;  8: x += W_down h (chat.py:927-956).
+ * mask 16 alone runs the head instead: logits = W_lm rmsnorm(x) * out_norm
+ * (chat.py:962-968), layer ignored.  Used by the benchmark and by the
+ * full-shape parity tests of each launch. */
 int gsdh_model_run_linear(gsdh_model* m, int layer, int mask);
+
+/* Activation vectors of the model context (f32): x [hidden], q [n_heads*hd],
+ * k / v [n_kv*hd], attn [n_heads*hd], h [ffn], logits [vocab].  write = 1
+ * copies host -> device, 0 device -> host; nbytes must be the vector's size.
+ * Synchronous (waits for the model stream first).  With gsdh_model_set_step
+ * and gsdh_model_read_kv they let a harness feed one launch of
+ * gsdh_model_run_linear and read its result, as the reference's ctypes
+ * harness feeds NumPy buffers to each gsd_cpu_* call
+ * (gsd_lq_cpu_runtime.py:316-404).  No counterpart in the reference. */
+enum { GSDH_VEC_X = 0, GSDH_VEC_Q, GSDH_VEC_K, GSDH_VEC_V, GSDH_VEC_ATTN, GSDH_VEC_H, GSDH_VEC_LOGITS };
+int gsdh_model_vector(gsdh_model* m, int which, int write, void* host, uint64_t nbytes);
+/* Step state read by the launches: token id and position (RoPE angle and
+ * KV slot of the qkv launch).  Synchronous. */
+int gsdh_model_set_step(gsdh_model* m, int token_id, int pos);
+/* The fp16 K and V cache rows [n_kv*hd] of (layer, pos) to host memory. */
+int gsdh_model_read_kv(gsdh_model* m, int layer, int pos, uint16_t* k_out, uint16_t* v_out);
 
 /* Graph capture of an arbitrary sequence of the model's own launches on its
  * stream, for timing: begin, issue calls, end -> replay n times. */

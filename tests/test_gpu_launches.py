@@ -1,0 +1,176 @@
+"""Full-shape parity of every fused matvec launch the decode runs (and the
+benchmark times), one launch at a time, against the oracle on the same inputs.
+
+The model is one layer of the Mistral-7B shape (hidden 4096, ffn 14336,
+32 query / 8 KV heads of 128, vocab 32768), packed like the benchmark's layers
+in Turbo mode (radius 8, u8 codes) and Precision mode (radius 6, 7-bit device
+codes, rank 2).  Each launch reads the activation vectors a test writes and
+its result is read back (gsdh_model_vector / gsdh_model_read_kv):
+
+  qkv      q' = RoPE(Wq xn), K' = fp16(RoPE(Wk xn)), V = fp16(Wv xn),
+           xn = rmsnorm(x) * attn_norm        (gsd_lq_cpu_runtime.py:316-340)
+  o        x + Wo attn                         (gsd_lq_cpu_runtime.py:376-378)
+  gate/up  silu(Wg xn) * (Wu xn), xn = rmsnorm(x) * ffn_norm   (:384-396)
+  down     x + Wd h                            (:398-404)
+  head     Wlm (rmsnorm(x) * out_norm)         (:414-419)
+
+Bar: 1e-3 relative L2 (the tolerance of the matvec's fp32 accumulation in
+another order).  The measured error of every launch is printed; the matrix-core
+kernel represents x as fp16 high + low parts (about 2^-22 relative), so it is
+also held to 1e-4, a regression guard two orders under the bar."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import rel_l2
+from gpu_util import banner
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+GUARD = 1e-4
+
+
+@pytest.fixture(scope="module", params=["turbo", "precision"])
+def layer7b(request):
+    from gsdlq import synth
+    import run_gpu_native_chat as chat
+    mode = request.param
+    banner(f"packing one 7B-shaped layer + 32768-row head ({mode})")
+    src = synth.SynthSource(synth.SynthSpec(n_layers=1, mode=mode))
+    gpu = chat.GPUMistralV2Model(src, max_seq_len=64, verbose=False)
+    ref = O.OracleModel(src, kind="port", max_seq_len=64)
+    yield mode, gpu, ref
+    gpu.close()
+
+
+def _put(gpu, name, a):
+    from gsdlq import hip
+    a = np.ascontiguousarray(a, np.float32)
+    gpu.cl.lib.gsdh_model_vector(gpu._m, hip.VECTORS[name], 1, hip.ptr(a), a.nbytes)
+
+
+def _get(gpu, name, n):
+    from gsdlq import hip
+    a = np.empty(n, np.float32)
+    gpu.cl.lib.gsdh_model_vector(gpu._m, hip.VECTORS[name], 0, hip.ptr(a), a.nbytes)
+    return a
+
+
+def _check(label, got, want, tol=TOL):
+    e = rel_l2(got, want)
+    print(f"[launch-parity] {label}: rel L2 {e:.3e}", flush=True)
+    assert e < tol, (label, e)
+    assert e < GUARD, (label, e)
+    return e
+
+
+def _rmsnorm(ref, x, w):
+    out = np.empty_like(x)
+    ref.lib.gsd_cpu_rmsnorm(O.P(x), O.P(w), O.P(out), x.size, float(ref.rms_eps))
+    return out
+
+
+def test_qkv_launch_full_shape(layer7b):
+    mode, gpu, ref = layer7b
+    rng = np.random.default_rng(101)
+    x = rng.standard_normal(gpu.hidden).astype(np.float32)
+    pos = 37
+    _put(gpu, "x", x)
+    gpu.cl.lib.gsdh_model_set_step(gpu._m, 0, pos)
+    gpu.cl.lib.gsdh_model_run_linear(gpu._m, 0, 1)
+    q = _get(gpu, "q", gpu.n_heads * gpu.head_dim)
+    kvd = gpu.n_kv_heads * gpu.head_dim
+    kr, vr = np.empty(kvd, np.uint16), np.empty(kvd, np.uint16)
+    from gsdlq import hip
+    gpu.cl.lib.gsdh_model_read_kv(gpu._m, 0, pos, hip.ptr(kr), hip.ptr(vr))
+
+    ly = ref.layers[0]
+    xb = _rmsnorm(ref, x, ly["attn_norm"])
+    ref.matvec(xb, ly["q"], ref.q)
+    ref.matvec(xb, ly["k"], ref.k)
+    ref.matvec(xb, ly["v"], ref.v)
+    ref.lib.gsd_cpu_rope_and_store_kv(O.P(ref.q), O.P(ref.k), O.P(ref.v), O.P(ref.k_cache), O.P(ref.v_cache),
+                                      0, pos, ref.n_heads, ref.n_kv_heads, ref.head_dim, ref.max_seq_len,
+                                      float(ref.rope_theta), 1)
+    _check(f"{mode} q (4096x4096, RoPE pos {pos})", q, ref.q)
+    _check(f"{mode} K cache row (1024x4096, RoPE, fp16)", O.f16_to_f32(kr),
+           O.f16_to_f32(ref.k_cache[0, pos].reshape(-1)))
+    _check(f"{mode} V cache row (1024x4096, fp16)", O.f16_to_f32(vr), O.f16_to_f32(ref.v_cache[0, pos].reshape(-1)))
+
+
+def test_o_launch_full_shape(layer7b):
+    mode, gpu, ref = layer7b
+    rng = np.random.default_rng(102)
+    x = rng.standard_normal(gpu.hidden).astype(np.float32)
+    att = rng.standard_normal(gpu.n_heads * gpu.head_dim).astype(np.float32)
+    _put(gpu, "x", x)
+    _put(gpu, "attn", att)
+    gpu.cl.lib.gsdh_model_run_linear(gpu._m, 0, 2)
+    got = _get(gpu, "x", gpu.hidden)
+    y = np.empty(gpu.hidden, np.float32)
+    ref.matvec(att, ref.layers[0]["o"], y)
+    _check(f"{mode} o (4096x4096) without residual", got - x, y)
+    _check(f"{mode} o + residual", got, x + y)
+
+
+def test_gate_up_launch_full_shape(layer7b):
+    """The launch the benchmark's roofline figure times: 2 x 14336 x 4096."""
+    mode, gpu, ref = layer7b
+    rng = np.random.default_rng(103)
+    x = rng.standard_normal(gpu.hidden).astype(np.float32)
+    _put(gpu, "x", x)
+    gpu.cl.lib.gsdh_model_run_linear(gpu._m, 0, 4)
+    got = _get(gpu, "h", gpu.ffn_size)
+    ly = ref.layers[0]
+    xb = _rmsnorm(ref, x, ly["ffn_norm"])
+    g = np.empty(gpu.ffn_size, np.float32)
+    u = np.empty(gpu.ffn_size, np.float32)
+    ref.matvec(xb, ly["gate"], g)
+    ref.matvec(xb, ly["up"], u)
+    ref.lib.gsd_cpu_swiglu(O.P(g), O.P(u), O.P(g), gpu.ffn_size)
+    _check(f"{mode} gate/up (2x14336x4096) + SwiGLU", got, g)
+
+
+def test_down_launch_full_shape(layer7b):
+    mode, gpu, ref = layer7b
+    rng = np.random.default_rng(104)
+    x = rng.standard_normal(gpu.hidden).astype(np.float32)
+    h = rng.standard_normal(gpu.ffn_size).astype(np.float32)
+    _put(gpu, "x", x)
+    _put(gpu, "h", h)
+    gpu.cl.lib.gsdh_model_run_linear(gpu._m, 0, 8)
+    got = _get(gpu, "x", gpu.hidden)
+    y = np.empty(gpu.hidden, np.float32)
+    ref.matvec(h, ref.layers[0]["down"], y)
+    _check(f"{mode} down (4096x14336) without residual", got - x, y)
+    _check(f"{mode} down + residual", got, x + y)
+
+
+def test_head_launch_full_shape(layer7b):
+    mode, gpu, ref = layer7b
+    rng = np.random.default_rng(105)
+    x = rng.standard_normal(gpu.hidden).astype(np.float32)
+    _put(gpu, "x", x)
+    gpu.cl.lib.gsdh_model_run_linear(gpu._m, 0, 16)
+    got = _get(gpu, "logits", gpu.vocab_size)
+    xb = _rmsnorm(ref, x, ref.final_norm)
+    want = np.empty(gpu.vocab_size, np.float32)
+    ref.matvec(xb, ref.lm_head, want)
+    _check(f"{mode} lm_head (32768x4096)", got, want)
+
+
+def test_launches_repeat_bit_identical(layer7b):
+    """A launch run twice on the same inputs gives the same bits (fixed
+    reduction order; no state carried between launches)."""
+    mode, gpu, _ = layer7b
+    rng = np.random.default_rng(106)
+    x = rng.standard_normal(gpu.hidden).astype(np.float32)
+    outs = []
+    for _ in range(2):
+        _put(gpu, "x", x)
+        gpu.cl.lib.gsdh_model_run_linear(gpu._m, 0, 4)
+        outs.append(_get(gpu, "h", gpu.ffn_size))
+    assert np.array_equal(outs[0], outs[1])

@@ -266,3 +266,46 @@ def test_greedy_7b_precision_128_steps():
     for i, v in top:
         assert abs(lg[i] - v) <= 1e-3 * max(1.0, abs(v))
     gpu.close()
+
+
+_LONG = {}
+
+
+def _long_oracle():
+    """Oracle greedy run through positions 0 .. 4113 of an 8192-position model
+    (computed once for both engines)."""
+    if not _LONG:
+        from gsdlq import synth
+        spec = _spec(mode="precision", kinks_per_row=1, n_layers=1)
+        ref = O.OracleModel(synth.SynthSource(spec), kind="port", max_seq_len=8192)
+        rng = np.random.default_rng(LONG_SEED)
+        prompt = rng.integers(0, spec.vocab, 4090).tolist()
+        toks, margins = ref.generate_greedy(prompt, 24)
+        rewrites = {}
+        for pos in (2047, 2048, 4095, 4096, 4113):
+            rewrites[pos] = ref.forward_token(toks[0], pos)
+        _LONG.update(spec=spec, prompt=prompt, toks=toks, margins=margins, rewrites=rewrites)
+    return _LONG
+
+
+LONG_SEED = 5
+
+
+@pytest.mark.parametrize("engine", ENGINES)
+def test_decode_past_2048_to_4096(engine):
+    """A model with an 8192-position cache decodes through positions 2048
+    (the reference's fixed cache size) and 4096: 4090 prompt tokens, then 24
+    greedy steps equal to the oracle's (heap score buffer), and forward_token
+    on both sides of each boundary within 1e-3."""
+    from gsdlq import synth
+    import run_gpu_native_chat as chat
+    L = _long_oracle()
+    banner(f"decode to position 4113 of an 8192-position cache ({engine})")
+    gpu = chat.GPUMistralV2Model(synth.SynthSource(L["spec"]), max_seq_len=8192, verbose=False)
+    gpu.set_engine(engine)
+    toks, margins = gpu.generate_greedy(L["prompt"], 24)
+    assert toks == L["toks"]
+    assert np.allclose(margins, L["margins"], rtol=1e-2, atol=1e-4)
+    for pos, want in L["rewrites"].items():
+        assert rel_l2(gpu.forward_token(L["toks"][0], pos), want) < 1e-3, pos
+    gpu.close()

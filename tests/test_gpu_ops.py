@@ -160,3 +160,101 @@ def test_attention_vs_oracle(lib, ctx, nh, nkv, hd, layers):
         lib.gsdh_gqa_attention(None, p(dq), p(dk), p(dv), p(out), layer, ctx - 1, nh, nkv, hd, ms,
                                1.0 / float(np.sqrt(hd)))
         assert rel_l2(H(out, np.float32, nh * hd), want) < TOL
+
+
+# head_dim 256 with 4 query heads per KV head (16 waves), 2 query heads per KV
+# head at hd 128 and 64
+@pytest.mark.parametrize("ctx,nh,nkv,hd", [(777, 8, 2, 256), (1500, 16, 8, 128), (3000, 8, 4, 64), (300, 8, 2, 256)])
+def test_attention_group_sizes_vs_oracle(lib, ctx, nh, nkv, hd):
+    banner(f"attention ctx {ctx} heads {nh}/{nkv} hd {hd}")
+    _attention_case(lib, ctx, nh, nkv, hd, seed=ctx + hd)
+
+
+def _attention_case(lib, ctx, nh, nkv, hd, seed, ms=None):
+    from gsdlq import pack
+    ms = ms or ctx + 3
+    kc = pack.synth_f16(seed, ctx, ms * nkv * hd, 1.0)
+    vc = pack.synth_f16(seed + 1, ctx, ms * nkv * hd, 1.0)
+    q = np.random.default_rng(seed).standard_normal(nh * hd).astype(np.float32)
+    want = np.zeros(nh * hd, np.float32)
+    O.load("port").gsd_cpu_gqa_attention(O.P(q), O.P(kc), O.P(vc), O.P(want), 0, ctx - 1, nh, nkv, hd, ms,
+                                         1.0 / float(np.sqrt(hd)))
+    out, dk, dv, dq = E(nh * hd * 4), D(kc), D(vc), D(q)
+    lib.gsdh_gqa_attention(None, p(dq), p(dk), p(dv), p(out), 0, ctx - 1, nh, nkv, hd, ms, 1.0 / float(np.sqrt(hd)))
+    got = H(out, np.float32, nh * hd)
+    assert rel_l2(got, want) < TOL, (ctx, nh, nkv, hd)
+
+
+def test_attention_shape_changes_between_calls(lib):
+    """One call per shape, in an order whose split-word regions overlap: 8 KV
+    heads, then 2 KV heads of 256 dims, then 8 KV heads again (a word left by
+    an earlier call of another shape must never be taken for this call's)."""
+    banner("attention: 8 KV heads -> 2 KV heads (hd 256) -> 8 KV heads")
+    _attention_case(lib, 2048, 32, 8, 128, seed=61)
+    _attention_case(lib, 1200, 8, 2, 256, seed=62)
+    _attention_case(lib, 2048, 32, 8, 128, seed=63)
+    _attention_case(lib, 5000, 32, 8, 128, seed=64)
+    _attention_case(lib, 700, 16, 2, 64, seed=65)
+    _attention_case(lib, 2048, 32, 8, 128, seed=66)
+
+
+@pytest.mark.parametrize("pos", [2048, 4095, 8191])
+@pytest.mark.parametrize("il", [1, 0])
+def test_rope_kv_bitexact_long_positions(lib, pos, il):
+    """RoPE + K/V append past the reference's 2048-position cache, up to the
+    last slot of an 8192-position cache, bit-exact against the oracle (the
+    same C library cos/sin)."""
+    ms, nh, nkv, hd = 8192, 32, 8, 128
+    rng = np.random.default_rng(pos + il)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k = rng.standard_normal(nkv * hd).astype(np.float32)
+    v = rng.standard_normal(nkv * hd).astype(np.float32)
+    qr, kcr, vcr = q.copy(), np.zeros((ms, nkv, hd), np.uint16), np.zeros((ms, nkv, hd), np.uint16)
+    O.load("port").gsd_cpu_rope_and_store_kv(O.P(qr), O.P(k), O.P(v), O.P(kcr), O.P(vcr), 0, pos, nh, nkv, hd, ms,
+                                             1e6, il)
+    dq, dk, dv = D(q), D(k), D(v)
+    kc, vc = E(ms * nkv * hd * 2), E(ms * nkv * hd * 2)
+    lib.gsdh_rope_and_store_kv(None, p(dq), p(dk), p(dv), p(kc), p(vc), 0, pos, nh, nkv, hd, ms, 1e6, il)
+    assert np.array_equal(H(dq, np.uint32, nh * hd), qr.view(np.uint32))
+    assert np.array_equal(H(kc, np.uint16, ms * nkv * hd).reshape(ms, nkv, hd)[pos], kcr[pos])
+    assert np.array_equal(H(vc, np.uint16, ms * nkv * hd).reshape(ms, nkv, hd)[pos], vcr[pos])
+
+
+def _argmax_cases():
+    rng = np.random.default_rng(7)
+    n = 32768
+    base = rng.standard_normal(n).astype(np.float32) * 5
+    cases = {}
+    a = base.copy(); a[[3, 900, 20000]] = np.nan; cases["nan"] = a
+    a = base.copy(); a[:] = np.nan; cases["all_nan"] = a
+    a = base.copy(); a[12345] = np.inf; cases["posinf"] = a
+    a = base.copy(); a[12345] = np.inf; a[77] = 150.0; cases["posinf_below_finite"] = a
+    a = base.copy(); a[500] = np.inf; a[40] = 100.0; cases["posinf_ties_100"] = a
+    a = base.copy(); a[9] = np.inf; a[10] = np.inf; cases["two_posinf"] = a
+    a = base.copy(); a[:] = -np.inf; a[31000] = -3.0; cases["neginf"] = a
+    a = base.copy(); a[:] = -np.inf; cases["all_neginf"] = a
+    a = np.zeros(n, np.float32); cases["all_equal"] = a
+    a = base.copy(); m = a.max() + 1; a[[25000, 7000, 7001, 31999]] = m; cases["ties_first_index"] = a
+    a = base.copy(); a[0] = a.max() + 2; a[n - 1] = a[0]; cases["ties_ends"] = a
+    a = base.copy(); a[5] = np.nan; a[6] = -1e4; a[:] = -1e5; a[5] = np.nan; cases["nan_is_minus_1e4"] = a
+    cases["n1"] = np.array([-2.5], np.float32)
+    a = rng.standard_normal(1000).astype(np.float32); a[999] = 40; cases["n1000"] = a
+    a = rng.standard_normal(100003).astype(np.float32); a[70001] = 9; a[100002] = 9; cases["n100003_two_rounds"] = a
+    return cases
+
+
+@pytest.mark.parametrize("name", sorted(_argmax_cases()))
+def test_greedy_argmax_special_values(lib, name):
+    """The device greedy step against gsd_lq_cpu_runtime.py:422-425:
+    nan_to_num(nan=-1e4, posinf=100, neginf=-1e4), then the first index of
+    the maximum; the margin is top1 - top2 of the cleaned values."""
+    lg = _argmax_cases()[name]
+    want = O.OracleModel.greedy(lg)
+    clean = np.nan_to_num(lg, nan=-1e4, posinf=100.0, neginf=-1e4)
+    srt = np.sort(clean)
+    want_margin = np.float32(srt[-1] - (srt[-2] if clean.size > 1 else -np.inf))
+    d = D(lg)
+    tok, mg = E(4), E(4)
+    lib.gsdh_greedy_argmax(None, p(d), lg.size, p(tok), p(mg))
+    assert int(H(tok, np.int32, 1)[0]) == want, name
+    assert H(mg, np.float32, 1)[0] == want_margin, name
