@@ -94,6 +94,22 @@ int gsdh_gqa_attention(void* stream, const float* q, const uint16_t* k_cache,
                        const uint16_t* v_cache, float* attn_out, int layer_idx, int pos,
                        int n_heads, int n_kv_heads, int head_dim, int max_seq_len, float sm_scale);
 
+/* gsd_cpu_gqa_attention for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference.  Same arguments and results as
+ * gsdh_gqa_attention, but the split partials live in a static 8 MiB device
+ * array of the library (one per GPU, kept until the process ends), so the
+ * call allocates nothing.  Limit: n_kv_heads * splits * (n_heads/n_kv_heads)
+ * * (head_dim + 2) * 8 bytes <= 8 MiB, splits = ceil((pos+1) / chunk) with
+ * chunk = clamp(round_up((pos+1) * n_kv_heads / 256, 64), 64, 256); e.g. 8 KV
+ * heads x 4 x 128 dims up to 32 splits (context 8192) use 1.1 MB.  Larger
+ * calls fail with an error.  All calls on one GPU share the array: calls
+ * that overlap on one GPU (different streams, or threads) race. */
+int gsdh_gqa_attention_noalloc(void* stream, const float* q, const uint16_t* k_cache,
+                               const uint16_t* v_cache, float* attn_out, int layer_idx, int pos,
+                               int n_heads, int n_kv_heads, int head_dim, int max_seq_len,
+                               float sm_scale);
+
 /* Bit-exact unpack of codes: idx[i] = codes[i], r01[2i..2i+1] = integer
  * lattice fields (r0, r1) of codeword idx[i] in the radius-R enumeration.
  * Used to check the device decode path (no reference counterpart; the
