@@ -21,7 +21,7 @@ the dominant kernel's roofline (the fused gate/up launch, 2 x
 7B-shaped model, and the reference CPU engine timed on this host's cores on a
 bounded sample.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 3]
+    python bench.py [--gpus 1] [--steps 100] [--warmup 3]
 """
 import argparse
 import ctypes
@@ -129,34 +129,81 @@ def time_graph(model, ge, n):
 
 
 def bench_linear(bank, steps, warmup):
-    """GB/s of the layer linear set; returns (gbs, ms_per_step, roofline dict)."""
+    """GB/s of the layer linear set; returns (gbs, ms_per_step, roofline dict).
+    Step i runs the four launches of distinct layer i % layers; the warm-up
+    steps and the timed steps are each one captured graph, so exactly
+    `steps` steps lie between the two timing events."""
     model = build_model(bank, bank.n)
     lib = model.cl.lib
     model.forward_token(1, 0)   # realistic activations in every buffer
     L = bank.n
-    ge = capture(model, lambda: [lib.gsdh_model_run_linear(model._m, l, 15) for l in range(L)])
-    time_graph(model, ge, max(1, warmup))
-    reps = max(1, steps // L)
-    ms = time_graph(model, ge, reps)
-    n_steps = reps * L
-    ms_step = ms / n_steps
-    gbs = sum(bank.layer_bytes) * reps / (ms * 1e-3) / 1e9
-    # dominant kernel: fused gate+up (2 x 14336 x 4096), timed alone
-    gu = capture(model, lambda: [lib.gsdh_model_run_linear(model._m, l, 4) for l in range(L)])
-    time_graph(model, gu, 2)
-    gms = time_graph(model, gu, reps)
-    per_launch_ms = gms / (reps * L)
+    if warmup > 0:
+        gw = capture(model, lambda: [lib.gsdh_model_run_linear(model._m, i % L, 15) for i in range(warmup)])
+        time_graph(model, gw, 1)
+        lib.gsdh_graph_destroy(gw)
+    ge = capture(model, lambda: [lib.gsdh_model_run_linear(model._m, i % L, 15) for i in range(steps)])
+    ms = time_graph(model, ge, 1)
+    ms_step = ms / steps
+    gbs = sum(bank.layer_bytes[i % L] for i in range(steps)) / (ms * 1e-3) / 1e9
+    # dominant kernel: fused gate+up (2 x 14336 x 4096), timed alone over
+    # 128 launches rotating the distinct layers
+    ng = 128
+    gu = capture(model, lambda: [lib.gsdh_model_run_linear(model._m, i % L, 4) for i in range(ng)])
+    time_graph(model, gu, 1)
+    gms = time_graph(model, gu, 1)
+    per_launch_ms = gms / ng
     gu_bytes = sum(alg_bytes(bank.packed[(l, t)]) for l in range(L) for t in ("ffn_gate", "ffn_up")) / L
     gu_bytes -= 4 * H   # gate and up read the same x once
     ach = gu_bytes / (per_launch_ms * 1e-3) / 1e9
     roof = {"kernel": "hexmv4_kernel (MFMA fused RMSNorm + gate/up matvec + SwiGLU, 2x14336x4096)",
             "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(),
-            "launch_us": round(per_launch_ms * 1e3, 2), "alg_bytes_per_launch": int(gu_bytes)}
+            "launch_us": round(per_launch_ms * 1e3, 2), "alg_bytes_per_launch": int(gu_bytes),
+            "launches_timed": ng}
     for g in (ge, gu):
         lib.gsdh_graph_destroy(g)
     model.close()
     return gbs, ms_step, roof
+
+
+class C1Source(BankSource):
+    """A Turbo model whose 4096x4096 o projections are all distinct (seeded
+    per layer), the other tensors the bank's: C1's matvec rotated over more
+    weights than the Infinity Cache holds."""
+
+    def __init__(self, bank, n_layers):
+        from gsdlq import synth
+        super().__init__(bank, n_layers)
+        self.o = [synth.pack_synth(synth.SynthSpec(n_layers=n_layers, mode="turbo"), f"blk.{l}.attn_output.weight")
+                  for l in range(n_layers)]
+
+    def hex_field(self, name, field):
+        parts = name.split(".")
+        if name != "output.weight" and parts[2] == "attn_output":
+            return self.o[int(parts[1])][field]
+        return super().hex_field(name, field)
+
+
+def bench_c1(bank, n=48, reps=4):
+    """C1: one fused unpack-matvec of a 4096x4096 Turbo tensor (the o
+    projection launch: x += W attn), over n distinct tensors (n x 9 MB beyond
+    the 256 MB Infinity Cache), graph-captured back to back."""
+    import run_gpu_native_chat as chat
+    src = C1Source(bank, n)
+    model = chat.GPUMistralV2Model(src, max_seq_len=16, verbose=False)
+    lib = model.cl.lib
+    model.forward_token(1, 0)
+    ge = capture(model, lambda: [lib.gsdh_model_run_linear(model._m, l, 2) for l in range(n)])
+    time_graph(model, ge, 1)
+    ms = time_graph(model, ge, reps)
+    lib.gsdh_graph_destroy(ge)
+    us = ms * 1e3 / (reps * n)
+    b = sum(alg_bytes(f) for f in src.o) / n
+    model.close()
+    gbs = b / (us * 1e-6) / 1e9
+    return {"us_per_matvec": round(us, 3), "alg_bytes": int(b), "GBs": round(gbs, 1),
+            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "distinct_tensors": n,
+            "workload": "4096x4096 Turbo (R=8) fused unpack-matvec + residual (o launch), batch 1"}
 
 
 MFMA_F16_PEAK_TFLOPS = 2500.0   # MI355X dense fp16 / bf16 matrix peak
@@ -241,13 +288,31 @@ def bench_decode(bank, n_prompt=64, n_new=128):
     return out
 
 
+def host_cpu():
+    """CPU model and core count of this host (reported with every CPU figure)."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"model": model, "nproc": os.cpu_count() or 1,
+            "omp_threads": int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))}
+
+
+def _oracle():
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    return O, ("reference" if O.have_reference() else "port")
+
+
 def cpu_baseline(bank, seconds=12.0):
     """The reference CPU engine (built from its source into oracle/_ref; the
     oracle restatement if absent) on one Turbo layer's 7 matvecs, repeated for
     a bounded time on all host cores."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import oracle as O
-    kind = "reference" if O.have_reference() else "port"
+    O, kind = _oracle()
     x = np.random.default_rng(1).standard_normal(F).astype(np.float32)
     fs = [bank.packed[(0, t)] for t in layer_shapes()]
     for f in fs:   # warm
@@ -259,18 +324,84 @@ def cpu_baseline(bank, seconds=12.0):
             O.hex2d_matvec(x[:f["cols"]], f, kind=kind)
         n += 1
     dt = time.time() - t0
+    cpu = host_cpu()
     return {"value": round(bank.layer_bytes[0] * n / dt / 1e9, 3), "unit": "GB/s",
-            "cores": int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)), "kind": kind,
+            "cores": cpu["omp_threads"], "kind": kind, "cpu": cpu["model"], "nproc": cpu["nproc"],
             "sample": f"{n} passes over one Turbo 7B layer's 7 matvecs ({dt:.1f}s), gsd_cpu_hex2d_matvec "
                       f"built with the reference flags (clang -O3 -fopenmp)"}
 
 
-def probe(kind: str, n: int):
+def cpu_attention(ctxs=(512, 2048, 8192), seconds=2.0):
+    """C3 on the CPU: per layer one gsd_cpu_rope_and_store_kv and one
+    gsd_cpu_gqa_attention (32 / 8 heads x 128) at pos = ctx - 1, repeated for
+    a bounded time.  The reference engine keeps its scores in a fixed
+    2048-entry stack array (gsd_lq_cpu_engine.c:292), so contexts beyond 2048
+    run the oracle restatement (heap scores, same loops)."""
+    O, kind = _oracle()
+    nh, nkv, hd = 32, 8, 128
+    rng = np.random.default_rng(3)
+    out = {}
+    for ctx in ctxs:
+        k2 = kind if ctx <= 2048 else "port"
+        lib = O.load(k2)
+        kc = rng.standard_normal(ctx * nkv * hd, dtype=np.float32).astype(np.float16).view(np.uint16)
+        vc = rng.standard_normal(ctx * nkv * hd, dtype=np.float32).astype(np.float16).view(np.uint16)
+        q0 = rng.standard_normal(nh * hd, dtype=np.float32)
+        k = rng.standard_normal(nkv * hd, dtype=np.float32)
+        v = rng.standard_normal(nkv * hd, dtype=np.float32)
+        o = np.zeros(nh * hd, np.float32)
+        n, t0 = 0, time.time()
+        while time.time() - t0 < seconds or n < 3:
+            q = q0.copy()
+            lib.gsd_cpu_rope_and_store_kv(O.P(q), O.P(k), O.P(v), O.P(kc), O.P(vc), 0, ctx - 1, nh, nkv, hd, ctx,
+                                          1e6, 1)
+            lib.gsd_cpu_gqa_attention(O.P(q), O.P(kc), O.P(vc), O.P(o), 0, ctx - 1, nh, nkv, hd, ctx,
+                                      float(1.0 / np.sqrt(hd)))
+            n += 1
+        us = (time.time() - t0) * 1e6 / n
+        out[f"ctx{ctx}"] = {"us_per_layer": round(us, 1), "kind": k2, "calls": n}
+    out["cpu"] = host_cpu()
+    return out
+
+
+def cpu_decode(bank, n_prompt=2, n_new=6):
+    """C4 on the CPU: greedy decode of the 32-layer 7B Precision model
+    (the bank's distinct layers repeated) by the reference engine through the
+    reference's forward order (gsd_lq_cpu_runtime.py:302-420), a bounded
+    sample of n_prompt + n_new tokens."""
+    O, kind = _oracle()
+    src = BankSource(bank, 32)
+    ref = O.OracleModel(src, kind=kind, max_seq_len=64)
+    prompt = np.random.default_rng(4).integers(0, V, n_prompt).tolist()
+    logits = None
+    for pos, t in enumerate(prompt):
+        logits = ref.forward_token(int(t), pos, return_logits=pos == len(prompt) - 1)
+    t0 = time.time()
+    pos = len(prompt)
+    for _ in range(n_new):
+        logits = ref.forward_token(ref.greedy(logits), pos)
+        pos += 1
+    dt = time.time() - t0
+    return {"decode_tok_s": round(n_new / dt, 3), "kind": kind, "cpu": host_cpu(),
+            "sample": f"{n_prompt}-token prompt, then {n_new} greedy tokens ({dt:.1f}s)"}
+
+
+def probe(kind: str, n: int, ctx: int = 8192, m: int = 128):
     """Launch one kernel repeatedly for counter collection under rocprofv3:
     'gateup' = the fused gate/up matvec over 8 rotated Turbo layers,
-    'copy' = a 256 MiB device copy (the calibration of FETCH/WRITE_SIZE)."""
+    'copy' = a 256 MiB device copy (the calibration of FETCH/WRITE_SIZE),
+    'attn' = RoPE + K/V append and decode attention at context `ctx`,
+    'prefill' = the batched projection of 8 Turbo layer sets for `m` tokens."""
     from gsdlq import hip
     lib = hip.lib()
+    if kind == "attn":
+        r = bench_attention(ctxs=(ctx,), reps=n)
+        print(f"[probe] attention ctx {ctx}: {r}", flush=True)
+        return
+    if kind == "prefill":
+        r = bench_prefill(LayerBank("turbo", 8), ms=(m,), reps=n)
+        print(f"[probe] prefill M {m}: {r}", flush=True)
+        return
     if kind == "copy":
         nbytes = 256 << 20
         a, b = ctypes.c_void_p(), ctypes.c_void_p()
@@ -390,7 +521,7 @@ def traffic_from_profile():
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=40)
+    ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=8, help="distinct packed layers rotated (Turbo)")
     ap.add_argument("--no-precision", action="store_true")
@@ -398,10 +529,14 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-attention", action="store_true")
-    ap.add_argument("--probe", choices=["gateup", "copy"], help="run one kernel for rocprofv3 counters")
+    ap.add_argument("--no-c1", action="store_true")
+    ap.add_argument("--probe", choices=["gateup", "copy", "attn", "prefill"],
+                    help="run one kernel for rocprofv3 counters")
+    ap.add_argument("--ctx", type=int, default=8192, help="--probe attn: context length")
+    ap.add_argument("--m", type=int, default=128, help="--probe prefill: tokens")
     a = ap.parse_args()
     if a.probe:
-        probe(a.probe, max(a.steps, 1))
+        probe(a.probe, max(a.steps, 1), a.ctx, a.m)
         return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the decode path has no multi-GPU mode in this build "
@@ -418,6 +553,9 @@ def main():
     if not a.no_prefill:
         extra["prefill_turbo"] = dict(bench_prefill(turbo), workload="Turbo 7B layer set (7 tensors), X bf16 "
                                       "[M][cols] -> Y fp32, fp16 MFMA with fp32 accumulation")
+    if not a.no_c1:
+        extra["c1_matvec_4096"] = bench_c1(turbo)
+        log(f"C1 matvec: {extra['c1_matvec_4096']}")
     if not a.no_attention:
         extra["attention_c3"] = bench_attention()
         log(f"attention: {extra['attention_c3']}")
@@ -431,13 +569,19 @@ def main():
         if not a.no_decode:
             extra["decode_7b_precision"] = bench_decode(prec)
             log(f"decode: {extra['decode_7b_precision']}")
+        if not a.no_cpu_baseline and not a.no_decode:
+            extra["cpu_c4_decode"] = cpu_decode(prec)
+            log(f"CPU C4: {extra['cpu_c4_decode']}")
     cpu = None if a.no_cpu_baseline else cpu_baseline(turbo)
+    if not a.no_cpu_baseline and not a.no_attention:
+        extra["cpu_c3_attention"] = cpu_attention()
+        log(f"CPU C3: {extra['cpu_c3_attention']}")
     out = {
         "metric": "fused unpack-matvec GB/s (% HBM peak); batch-1 decode tok/s, 7B shape",
         "value": round(gbs, 1),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": max(1, a.steps // a.layers) * a.layers,
+        "steps": a.steps,
         "warmup": a.warmup,
         "ms_per_step": round(ms_step, 5),
         "higher_is_better": True,
