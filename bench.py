@@ -284,6 +284,23 @@ def bench_decode(bank, n_prompt=64, n_new=128):
             first = toks
         else:
             out["engines_agree"] = toks == first
+    # the 64-token prompt alone: batched prefill vs one decode step per token
+    model.set_engine("graph")
+    for batched, key in ((True, "prefill_batched"), (False, "prefill_token_by_token")):
+        model.set_prefill(batched)
+        model.prefill(prompt, 0, return_logits=False) if batched else None
+        t0 = time.time()
+        reps = 5
+        for _ in range(reps):
+            if batched:
+                model.prefill(prompt, 0)
+            else:
+                for pos, t in enumerate(prompt):
+                    model.forward_token(t, pos, return_logits=pos == n_prompt - 1)
+        dt = (time.time() - t0) / reps
+        out[key + "_ms"] = round(dt * 1e3, 2)
+        out[key + "_tok_s"] = round(n_prompt / dt, 1)
+    model.set_prefill(True)
     model.close()
     return out
 

@@ -264,6 +264,12 @@ int gsdh_greedy_argmax(void* stream, const float* logits, int n, int* token_out,
 // ---------------------------------------------------------------------------
 // model runtime
 // ---------------------------------------------------------------------------
+namespace {
+constexpr int kMatmulMaxM = 512;    // tokens per gsdh_model_matmul call
+constexpr int kPrefillChunk = 128;  // prompt tokens per batched prefill pass
+constexpr int kPrefillAttnChunk = 256;   // positions per attention split in prefill
+}  // namespace
+
 struct HexDev {
     int set = 0, radius = 0, rows = 0, cols = 0, k = 0;
     int64_t nk = 0;
@@ -292,8 +298,27 @@ struct gsdh_model {
     float2* cs = nullptr;
     unsigned long long* ws = nullptr;   // attention partial words
     unsigned* counters = nullptr;
-    void* mm_ws = nullptr;          // prefill staging (A fragments | descales | rank-k values)
+    // batched work, allocated at finalize (the calls allocate nothing):
+    // gsdh_model_matmul staging (A fragments | descales | rank-k values |
+    // split partials) for up to kMatmulMaxM tokens, and the prefill buffers
+    // for chunks of up to kPrefillChunk prompt tokens
+    void* mm_ws = nullptr;
     size_t mm_ws_bytes = 0;
+    struct Prefill {
+        int* tok = nullptr;                       // [chunk] token ids
+        float *X = nullptr, *Q = nullptr, *K = nullptr, *V = nullptr, *A = nullptr, *G = nullptr, *U = nullptr;
+        float* xn = nullptr;                      // prepared input [chunk][max cols]
+        uint4* xa = nullptr;                      // hi/lo MFMA fragments
+        float* xs = nullptr;                      // per-token descales
+        float* tmp = nullptr;                     // rank-k values [kMaxSeg][chunk][kMaxRank]
+        float* part = nullptr;                    // split partials
+        size_t part_bytes = 0;
+        unsigned long long* ws = nullptr;         // attention split words [chunk][n_kv][splits][G][2 + hd]
+        size_t ws_bytes = 0;
+        unsigned epoch = 0;                       // last attention epoch on ws
+        int chunk = 0, splits = 0;
+        bool batched = true;                      // generate_greedy prefills in batches
+    } pf;
     unsigned long long* pub = nullptr;   // rank-k publication words, one range per matvec launch
     int pub_words = 0, pub_next = 0;
     int chunk = 64, max_splits = 1;
@@ -530,6 +555,193 @@ int setup_token_kernel(gsdh_model* m) {
     return 0;
 }
 
+// Staging bytes of one gsdh_model_matmul call (bf16 X, single fp16 operand
+// rounding): A fragments, descales, rank-k values, split partials.
+size_t matmul_ws_need(int M, int rows, int cols) {
+    const size_t xa = (hexmm_xa_bytes(M, cols) + 255) / 256 * 256;
+    const size_t xs = ((size_t)(M + 15) / 16 * 16 * 4 + 255) / 256 * 256;
+    const size_t tk = ((size_t)M * kMaxRank * 4 + 255) / 256 * 256;
+    const MatmulPlan plan = hexmm_plan(M, rows, cols);
+    const size_t pt = plan.nsplit > 1 ? (size_t)plan.nsplit * ((M + 15) / 16 * 16) * rows * 4 : 0;
+    return xa + xs + tk + pt;
+}
+
+size_t split_part_bytes(int M, int rows, int cols) {
+    const MatmulPlan plan = hexmm_plan(M, rows, cols);
+    return plan.nsplit > 1 ? (size_t)plan.nsplit * ((M + 15) / 16 * 16) * rows * 4 : 0;
+}
+
+// The batched workspaces, sized for every tensor shape of the model and every
+// batch size up to the limits, so no later call allocates.
+int setup_batched(gsdh_model* m) {
+    const auto& c = m->c;
+    const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
+    const int shapes[5][2] = {{qd, c.hidden}, {kvd, c.hidden}, {c.hidden, qd}, {c.ffn, c.hidden}, {c.hidden, c.ffn}};
+    size_t mm = 0, part = 0;
+    for (int M = 1; M <= kMatmulMaxM; M++) {
+        for (const auto& sh : shapes) {
+            mm = std::max(mm, matmul_ws_need(M, sh[0], sh[1]));
+            if (M <= kPrefillChunk) part = std::max(part, split_part_bytes(M, sh[0], sh[1]));
+        }
+        mm = std::max(mm, matmul_ws_need(M, c.vocab, c.hidden));
+    }
+    auto& P = m->pf;
+    const int Mc = kPrefillChunk, Mp = (Mc + 15) / 16 * 16;
+    const int maxc = std::max(std::max(c.hidden, c.ffn), qd);
+    P.chunk = Mc;
+    P.splits = (c.max_seq_len + kPrefillAttnChunk - 1) / kPrefillAttnChunk;
+    P.ws_bytes = attention_ws_bytes(c.n_kv_heads, P.splits, c.n_heads / c.n_kv_heads, c.head_dim) * Mc;
+    P.part_bytes = part;
+    int rc = 0;
+    auto A = [&](void** p, size_t n) { if (!rc) rc = dalloc(m, p, n); };
+    A(&m->mm_ws, mm);
+    m->mm_ws_bytes = mm;
+    A((void**)&P.tok, (size_t)Mc * 4);
+    A((void**)&P.X, (size_t)Mc * c.hidden * 4);
+    A((void**)&P.Q, (size_t)Mc * qd * 4);
+    A((void**)&P.K, (size_t)Mc * kvd * 4);
+    A((void**)&P.V, (size_t)Mc * kvd * 4);
+    A((void**)&P.A, (size_t)Mc * qd * 4);
+    A((void**)&P.G, (size_t)Mc * c.ffn * 4);
+    A((void**)&P.U, (size_t)Mc * c.ffn * 4);
+    A((void**)&P.xn, (size_t)Mp * maxc * 4);
+    A((void**)&P.xa, hexmm_xa_bytes(Mc, maxc, 1));
+    A((void**)&P.xs, (size_t)Mp * 4);
+    A((void**)&P.tmp, (size_t)kMaxSeg * Mc * kMaxRank * 4);
+    A((void**)&P.part, part);
+    A((void**)&P.ws, P.ws_bytes);
+    if (rc) return rc;
+    HIPCHK(launch_fill_u32(reinterpret_cast<unsigned*>(P.ws), 0u, P.ws_bytes / 4, m->stream));
+    P.epoch = 0;
+    return 0;
+}
+
+// One batched projection of the prepared operands (launch_batch_prep) into Y
+// [M][rows]: y, or Y += y with accumulate.
+int issue_mm(gsdh_model* m, const HexDev& t, int M, int cols, const float* tmp, float* Y, bool accumulate) {
+    auto& P = m->pf;
+    MatmulArgs a{};
+    fill_seg(a.w, t, m, nullptr);
+    const MatmulPlan plan = hexmm_plan(M, t.rows, cols);
+    if (plan.nsplit > 1 && split_part_bytes(M, t.rows, cols) > P.part_bytes)
+        return fail(-1, "prefill: split partials of %d tokens exceed the workspace", M);
+    a.xa = P.xa; a.xs = P.xs; a.Xf = P.xn; a.hl = 1; a.accumulate = accumulate ? 1 : 0;
+    a.tmp_k = t.k > 0 ? tmp : nullptr; a.Y = Y; a.M = M; a.cols = cols;
+    a.nsplit = plan.nsplit; a.tg = plan.tg; a.rbw = plan.rbw; a.part = plan.nsplit > 1 ? P.part : nullptr;
+    HIPCHK(launch_hexmm_prepared(a, m->stream));
+    return 0;
+}
+
+// Operands of the batched projections reading X [M][cols] (norm: RMSNorm
+// weights or null), with the rank-k projections of tensors t[0..n).
+int issue_prep(gsdh_model* m, const float* X, int M, int cols, const float* norm_w, const HexDev* const* t, int n) {
+    auto& P = m->pf;
+    BatchPrep b{};
+    b.X = X; b.ldx = cols; b.norm_w = norm_w; b.eps = m->c.rms_eps; b.M = M; b.cols = cols;
+    b.xa = P.xa; b.xs = P.xs; b.xn = P.xn;
+    for (int g = 0; g < n; g++) {
+        if (t[g]->k > 0) {
+            b.Vt[g] = t[g]->Vt; b.S[g] = t[g]->Sv; b.k[g] = t[g]->k;
+            b.tmp[g] = P.tmp + (size_t)g * P.chunk * kMaxRank;
+        }
+    }
+    HIPCHK(launch_batch_prep(b, m->stream));
+    return 0;
+}
+
+// Prompt tokens P.tok[0..M) at positions p0.. through every layer as batched
+// projections on the matrix cores (run_gpu_native_chat.py:892-956 per
+// token, computed for M tokens at once), K/V appended for every position,
+// causal attention over the cache; the last token's hidden state is left in
+// x for the head.
+int issue_prefill(gsdh_model* m, int M, int p0) {
+    const auto& c = m->c;
+    auto& P = m->pf;
+    const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
+    int rc = 0;
+    HIPCHK(launch_embed_rows(m->embed, P.tok, M, P.X, c.hidden, m->stream));
+    for (int l = 0; l < c.n_layers; l++) {
+        const HexDev *tq = &m->slot(l, GSDH_Q), *tk = &m->slot(l, GSDH_K), *tv = &m->slot(l, GSDH_V);
+        const HexDev *to = &m->slot(l, GSDH_O), *tg = &m->slot(l, GSDH_GATE), *tu = &m->slot(l, GSDH_UP);
+        const HexDev* td = &m->slot(l, GSDH_DOWN);
+        const float* tmp0 = P.tmp;
+        const float* tmp1 = P.tmp + (size_t)P.chunk * kMaxRank;
+        const float* tmp2 = P.tmp + (size_t)2 * P.chunk * kMaxRank;
+        {   // q, k, v of rmsnorm(x) * attn_norm
+            const HexDev* ts[3] = {tq, tk, tv};
+            if ((rc = issue_prep(m, P.X, M, c.hidden, m->norm(l, 0), ts, 3))) return rc;
+            if ((rc = issue_mm(m, *tq, M, c.hidden, tmp0, P.Q, false))) return rc;
+            if ((rc = issue_mm(m, *tk, M, c.hidden, tmp1, P.K, false))) return rc;
+            if ((rc = issue_mm(m, *tv, M, c.hidden, tmp2, P.V, false))) return rc;
+        }
+        RopeKV r{};
+        r.cs = m->cs; r.pos_dev = nullptr; r.pos = p0; r.k_cache = m->kc; r.v_cache = m->vc; r.layer = l;
+        r.n_heads = c.n_heads; r.n_kv = c.n_kv_heads; r.hd = c.head_dim; r.max_seq = c.max_seq_len;
+        r.interleaved = c.rope_interleaved;
+        HIPCHK(launch_rope_kv_rows(P.Q, P.K, P.V, r, M, m->stream));
+        {   // causal attention of the M tokens over the cache
+            AttnArgs a{};
+            a.q = P.Q; a.k_cache = m->kc; a.v_cache = m->vc; a.out = P.A; a.pos_dev = nullptr; a.pos = p0;
+            a.layer = l; a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.hd = c.head_dim; a.max_seq = c.max_seq_len;
+            a.sm_scale = 1.0f / (float)std::sqrt((double)c.head_dim);
+            a.chunk = kPrefillAttnChunk;
+            a.max_splits = (p0 + M + kPrefillAttnChunk - 1) / kPrefillAttnChunk;
+            a.ws = P.ws; a.counters = nullptr; a.err = &m->st->err; a.ntok = M;
+            if (P.epoch >= 0xFFFFFFF0u) {
+                HIPCHK(launch_fill_u32(reinterpret_cast<unsigned*>(P.ws), 0u, P.ws_bytes / 4, m->stream));
+                P.epoch = 0;
+            }
+            a.epoch = ++P.epoch;
+            HIPCHK(launch_attention(a, m->stream));
+        }
+        {   // x += W_o attn
+            const HexDev* ts[1] = {to};
+            if ((rc = issue_prep(m, P.A, M, qd, nullptr, ts, 1))) return rc;
+            if ((rc = issue_mm(m, *to, M, qd, tmp0, P.X, true))) return rc;
+        }
+        {   // h = silu(W_gate x') * (W_up x'), x' = rmsnorm(x) * ffn_norm
+            const HexDev* ts[2] = {tg, tu};
+            if ((rc = issue_prep(m, P.X, M, c.hidden, m->norm(l, 1), ts, 2))) return rc;
+            if ((rc = issue_mm(m, *tg, M, c.hidden, tmp0, P.G, false))) return rc;
+            if ((rc = issue_mm(m, *tu, M, c.hidden, tmp1, P.U, false))) return rc;
+            HIPCHK(launch_swiglu(P.G, P.U, P.G, M * c.ffn, m->stream));
+        }
+        {   // x += W_down h
+            const HexDev* ts[1] = {td};
+            if ((rc = issue_prep(m, P.G, M, c.ffn, nullptr, ts, 1))) return rc;
+            if ((rc = issue_mm(m, *td, M, c.ffn, tmp0, P.X, true))) return rc;
+        }
+    }
+    (void)kvd;
+    // the last token's residual stream for the head
+    HIPCHK(hipMemcpyAsync(m->x, P.X + (size_t)(M - 1) * c.hidden, (size_t)c.hidden * 4, hipMemcpyDeviceToDevice,
+                          m->stream));
+    return 0;
+}
+
+// Prompt prompt[0..n) at positions start.. in batches of the prefill chunk;
+// with `head`, the last token's logits and the greedy step (the step state
+// then holds the first generated token at position start + n, gen_count 1).
+// `ring`: pinned host staging of >= ceil(n / chunk) step states (read by
+// the copies until the stream is synchronised).
+int run_prefill(gsdh_model* m, const int* prompt, int n, int start, bool head, int* tok_stage, StepState* st_stage) {
+    auto& P = m->pf;
+    for (int b0 = 0; b0 < n; b0 += P.chunk) {
+        const int M = std::min(P.chunk, n - b0);
+        int* ts = tok_stage + b0;
+        for (int i = 0; i < M; i++) ts[i] = prompt[b0 + i];
+        HIPCHK(hipMemcpyAsync(P.tok, ts, (size_t)M * 4, hipMemcpyHostToDevice, m->stream));
+        int rc = issue_prefill(m, M, start + b0);
+        if (rc) return rc;
+    }
+    *st_stage = StepState{};
+    st_stage->token = prompt[n - 1];
+    st_stage->pos = start + n - 1;
+    HIPCHK(hipMemcpyAsync(m->st, st_stage, sizeof(StepState), hipMemcpyHostToDevice, m->stream));
+    if (head) return issue_head(m, true);
+    return 0;
+}
+
 int capture(gsdh_model* m, bool with_head, bool short_ctx, hipGraphExec_t* out) {
     hipGraph_t g = nullptr;
     HIPCHK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
@@ -647,7 +859,6 @@ int gsdh_model_destroy(gsdh_model* m) {
     for (auto& t : m->hex)
         if (t.block) (void)hipFree(t.block);
     for (void* p : m->allocs) (void)hipFree(p);
-    if (m->mm_ws) (void)hipFree(m->mm_ws);
     if (m->st_host) (void)hipHostFree(m->st_host);
     if (m->stream) (void)hipStreamDestroy(m->stream);
     delete m;
@@ -787,7 +998,9 @@ int gsdh_model_finalize(gsdh_model* m) {
     if (!rc) rc = capture(m, true, true, &m->g_full_s);
     if (!rc) rc = capture(m, false, true, &m->g_prefill_s);
     if (!rc) rc = setup_token_kernel(m);
+    if (!rc) rc = setup_batched(m);
     if (rc) return rc;
+    HIPCHK(hipStreamSynchronize(m->stream));
     m->finalized = true;
     return 0;
 }
@@ -836,14 +1049,18 @@ int gsdh_generate_greedy(gsdh_model* m, const int* prompt, int n_prompt, int sta
     for (int i = 0; i < n_prompt; i++)
         if (prompt[i] < 0 || prompt[i] >= m->c.vocab) return fail(-1, "generate: prompt token %d outside vocab", prompt[i]);
     StepState* ring = nullptr;
-    HIPCHK(hipHostMalloc((void**)&ring, sizeof(StepState) * (size_t)n_prompt, 0));
+    HIPCHK(hipHostMalloc((void**)&ring, sizeof(StepState) * (size_t)n_prompt + sizeof(int) * (size_t)n_prompt, 0));
     int rc = 0;
-    for (int i = 0; i < n_prompt && !rc; i++) {
-        ring[i] = StepState{};
-        ring[i].token = prompt[i]; ring[i].pos = start_pos + i;
-        hipError_t e = hipMemcpyAsync(m->st, &ring[i], sizeof(StepState), hipMemcpyHostToDevice, m->stream);
-        if (e == hipSuccess) e = hipGraphLaunch(token_graph(m, i == n_prompt - 1, start_pos + i), m->stream);
-        if (e != hipSuccess) rc = fail((int)e, "generate prefill: %s", hipGetErrorString(e));
+    if (m->pf.batched) {
+        rc = run_prefill(m, prompt, n_prompt, start_pos, true, reinterpret_cast<int*>(ring + n_prompt), ring);
+    } else {
+        for (int i = 0; i < n_prompt && !rc; i++) {
+            ring[i] = StepState{};
+            ring[i].token = prompt[i]; ring[i].pos = start_pos + i;
+            hipError_t e = hipMemcpyAsync(m->st, &ring[i], sizeof(StepState), hipMemcpyHostToDevice, m->stream);
+            if (e == hipSuccess) e = hipGraphLaunch(token_graph(m, i == n_prompt - 1, start_pos + i), m->stream);
+            if (e != hipSuccess) rc = fail((int)e, "generate prefill: %s", hipGetErrorString(e));
+        }
     }
     for (int i = 1; i < n_new && !rc; i++) {
         // the device advances the position: this launch runs the token at
@@ -862,6 +1079,40 @@ int gsdh_generate_greedy(gsdh_model* m, const int* prompt, int n_prompt, int sta
     (void)hipStreamSynchronize(m->stream);
     (void)hipHostFree(ring);
     return rc;
+}
+
+int gsdh_model_prefill(gsdh_model* m, const int* tokens, int n, int start_pos, int want_logits, float* logits_host,
+                       int* argmax_out) {
+    if (!m || !tokens) return fail(-1, "prefill: null argument");
+    if (!m->finalized) return fail(-1, "prefill: model not finalized");
+    if (n <= 0) return fail(-1, "prefill: n %d", n);
+    if (start_pos < 0 || start_pos + n > m->c.max_seq_len)
+        return fail(-1, "prefill: positions %d..%d exceed max_seq_len %d", start_pos, start_pos + n - 1, m->c.max_seq_len);
+    for (int i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= m->c.vocab) return fail(-1, "prefill: token %d outside vocab %d", tokens[i], m->c.vocab);
+    StepState* ring = nullptr;
+    HIPCHK(hipHostMalloc((void**)&ring, sizeof(StepState) * 2 + sizeof(int) * (size_t)n, 0));
+    int rc = run_prefill(m, tokens, n, start_pos, want_logits != 0, reinterpret_cast<int*>(ring + 2), ring);
+    if (!rc && want_logits && logits_host) {
+        hipError_t e = hipMemcpyAsync(logits_host, m->logits, (size_t)m->c.vocab * 4, hipMemcpyDeviceToHost, m->stream);
+        if (e != hipSuccess) rc = fail((int)e, "prefill: %s", hipGetErrorString(e));
+    }
+    if (!rc) {
+        hipError_t e = hipMemcpyAsync(ring + 1, m->st, sizeof(StepState), hipMemcpyDeviceToHost, m->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+        if (e != hipSuccess) rc = fail((int)e, "prefill: %s", hipGetErrorString(e));
+        else if (ring[1].err) rc = fail(-2, "prefill: an in-kernel wait timed out");
+        else if (want_logits && argmax_out) *argmax_out = ring[1].token;
+    }
+    (void)hipStreamSynchronize(m->stream);
+    (void)hipHostFree(ring);
+    return rc;
+}
+
+int gsdh_model_set_prefill(gsdh_model* m, int batched) {
+    if (!m) return fail(-1, "set_prefill: null model");
+    m->pf.batched = batched != 0;
+    return 0;
 }
 
 int gsdh_model_read_codes(gsdh_model* m, int layer, int slot, uint8_t* codes_out) {
@@ -890,20 +1141,15 @@ int gsdh_model_matmul(gsdh_model* m, int layer, int slot, const uint16_t* X, int
     if (M <= 0) return fail(-1, "matmul: M %d", M);
     const HexDev& t = m->slot(layer, slot);
     if (!t.set) return fail(-1, "matmul: layer %d slot %d not set", layer, slot);
+    if (!m->finalized) return fail(-1, "matmul: model not finalized");
+    if (M > kMatmulMaxM) return fail(-1, "matmul: M %d > %d tokens per call (split the batch)", M, kMatmulMaxM);
     const size_t xa = (hexmm_xa_bytes(M, t.cols) + 255) / 256 * 256;
     const size_t xs = ((size_t)(M + 15) / 16 * 16 * 4 + 255) / 256 * 256;
     const size_t tk = ((size_t)M * kMaxRank * 4 + 255) / 256 * 256;
     const MatmulPlan plan = hexmm_plan(M, t.rows, t.cols);
     const int nsplit = plan.nsplit;
-    const size_t pt = nsplit > 1 ? (size_t)nsplit * ((M + 15) / 16 * 16) * t.rows * 4 : 0;
-    if (xa + xs + tk + pt > m->mm_ws_bytes) {
-        HIPCHK(hipStreamSynchronize(m->stream));
-        if (m->mm_ws) (void)hipFree(m->mm_ws);
-        m->mm_ws = nullptr;
-        m->mm_ws_bytes = 0;
-        HIPCHK(hipMalloc(&m->mm_ws, xa + xs + tk + pt));
-        m->mm_ws_bytes = xa + xs + tk + pt;
-    }
+    if (matmul_ws_need(M, t.rows, t.cols) > m->mm_ws_bytes)
+        return fail(-1, "matmul: staging for %d tokens exceeds the model's workspace", M);
     char* w = static_cast<char*>(m->mm_ws);
     MatmulArgs a{};
     fill_seg(a.w, t, m, nullptr);

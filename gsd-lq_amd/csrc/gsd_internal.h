@@ -106,7 +106,7 @@ hipError_t launch_hexmv4(const HexArgs& a, hipStream_t stream);
 // (null when k == 0).
 struct MatmulArgs {
     HexSeg w;                  // codes_t, scales_t, fields, rows, n_pts, kinks, U, k
-    const uint16_t* X;
+    const uint16_t* X;         // bf16 input (hl == 0; the kink terms read it)
     uint4* xa;
     float* xs;
     const float* tmp_k;
@@ -115,8 +115,42 @@ struct MatmulArgs {
     int M, cols;
     int nsplit;                // column splits (1: blocks write Y directly)
     int tg, rbw;               // tiling (hexmm_plan)
+    // hl = 1: xa holds each token's (u, v) as fp16 high + low parts (about
+    // 2^-22 relative, as the batch-1 matvec) prepared by launch_batch_prep,
+    // two MFMAs per step; the kink terms read Xf (fp32 [M][cols], the
+    // prepared input).  accumulate = 1: Y[m][row] += y (residual add).
+    int hl;
+    const float* Xf;
+    int accumulate;
 };
-size_t hexmm_xa_bytes(int M, int cols);
+size_t hexmm_xa_bytes(int M, int cols, int hl = 0);
+// Operands of M tokens for the batched projections that share one input
+// (q/k/v, gate/up, o, down): x' = rmsnorm(x) * norm_w (as
+// gsd_lq_cpu_engine.c:66-82; norm_w null: x' = x) into xn (fp32 [M][cols]),
+// the hi/lo fp16 MFMA fragments of (u, v) = (x'a, x'a / 2 + x'b sqrt(3) / 2)
+// after a per-token power-of-two prescale (xa, descale xs), and the rank-k
+// projections tmp[g][m * k[g] + j] = S_g[j] * sum_c x'[c] Vt_g[j][c] of up to
+// kMaxSeg tensors (gsd_lq_cpu_engine.c:110-127).
+struct BatchPrep {
+    const float* X;
+    int ldx;                   // row stride of X (floats)
+    const float* norm_w;
+    float eps;
+    int M, cols;
+    uint4* xa;
+    float* xs;
+    float* xn;
+    const uint16_t* Vt[kMaxSeg];
+    const float* S[kMaxSeg];
+    int k[kMaxSeg];
+    float* tmp[kMaxSeg];
+};
+hipError_t launch_batch_prep(const BatchPrep& p, hipStream_t stream);
+// hexmm over operands launch_batch_prep made (a.hl = 1): no operand prep here
+hipError_t launch_hexmm_prepared(const MatmulArgs& a, hipStream_t stream);
+// X[m][:] = fp16 embedding row of tokens[m] (fp32 [M][hidden])
+hipError_t launch_embed_rows(const uint16_t* embed, const int* tokens, int M, float* X, int hidden,
+                             hipStream_t stream);
 // Tiling of a batched projection: token groups per block (tg: 1, 2, 4, 8),
 // row blocks per wave (rbw) and column splits (nsplit), chosen so the grid
 // fills the chip with the fewest re-decodes of the weights.
@@ -136,6 +170,10 @@ hipError_t launch_vec_add(float* y, const float* a, const float* b, int dim, hip
 hipError_t launch_swiglu(const float* g, const float* u, float* out, int dim, hipStream_t stream);
 hipError_t launch_rope_kv(float* q, const float* k, const float* v, const RopeKV& r,
                           const float2* cs_inline, hipStream_t stream);
+// The same for M consecutive tokens: q [M][n_heads*hd] in place, k / v
+// [M][n_kv*hd], token m at position r.pos + m (r.cs holds every position).
+hipError_t launch_rope_kv_rows(float* q, const float* k, const float* v, const RopeKV& r, int M,
+                               hipStream_t stream);
 
 // Contexts up to this length run attention as one block per KV head (the
 // score buffer of attn_kernel holds 256 positions).
@@ -165,6 +203,10 @@ struct AttnArgs {
     unsigned* counters;       // [n_kv] (epoch == 0 only)
     unsigned* err;            // set to 1 when a wait for a partial runs out (may be null)
     unsigned epoch;
+    // ntok > 1: a batch of consecutive query tokens (prefill; causal): token
+    // z = grid.z index at position pos + z, q / out rows z * n_heads * hd, its
+    // words at ws + z * n_kv * max_splits * group * (2 + hd); needs epoch.
+    int ntok;
 };
 hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
 // Positions per attention split for a context of n_ctx positions: enough

@@ -546,7 +546,12 @@ __global__ void rope_kv_kernel(float* q, const float* k, const float* v, const R
                                int use_inline) {
 #pragma clang fp contract(off)
     const int half = r.hd >> 1;
-    const int pos = r.pos_dev ? *r.pos_dev : r.pos;
+    // token blockIdx.y of a batch (one token: 0): its rows and position
+    const int tok = blockIdx.y;
+    q += (size_t)tok * r.n_heads * r.hd;
+    k += (size_t)tok * r.n_kv * r.hd;
+    v += (size_t)tok * r.n_kv * r.hd;
+    const int pos = (r.pos_dev ? *r.pos_dev : r.pos) + tok;
     const float2* cs = use_inline ? csi.v : r.cs + (size_t)pos * half;
     const int gid = blockIdx.x * blockDim.x + threadIdx.x;
     const size_t base = ((size_t)r.layer * r.max_seq + (size_t)pos) * (size_t)r.n_kv * r.hd;
@@ -608,12 +613,16 @@ __global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
 
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int sub = lane % LPP, prow = lane / LPP;
-    const int pos = a.pos_dev ? *a.pos_dev : a.pos;
+    // token z of a batch (prefill; decode: z = 0) at position pos + z
+    const int z = blockIdx.z;
+    const int pos = (a.pos_dev ? *a.pos_dev : a.pos) + z;
     const int n = pos + 1;
     const int nsplit = (n + a.chunk - 1) / a.chunk;
     const int split = blockIdx.y;
     if (split >= nsplit) return;
     const int kvh = blockIdx.x;
+    const float* qz = a.q + (size_t)z * a.n_heads * HD;
+    float* outz = a.out + (size_t)z * a.n_heads * HD;
     const unsigned ep0 = a.epoch ? a.epoch - 1u : a.counters[kvh];   // (used at the end)
     const int t0 = split * a.chunk;
     const int t1 = min(n, t0 + a.chunk);
@@ -625,7 +634,7 @@ __global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
     float qv[G][8];
 #pragma unroll
     for (int g = 0; g < G; g++) {
-        const float4* qp = reinterpret_cast<const float4*>(a.q + (size_t)(kvh * G + g) * HD + sub * 8);
+        const float4* qp = reinterpret_cast<const float4*>(qz + (size_t)(kvh * G + g) * HD + sub * 8);
         const float4 q0 = qp[0], q1 = qp[1];
         qv[g][0] = q0.x; qv[g][1] = q0.y; qv[g][2] = q0.z; qv[g][3] = q0.w;
         qv[g][4] = q1.x; qv[g][5] = q1.y; qv[g][6] = q1.z; qv[g][7] = q1.w;
@@ -737,7 +746,7 @@ __global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
     if (nsplit == 1) {
         for (int i = tid; i < G * HD; i += NT) {
             const int g = i / HD, d = i % HD;
-            a.out[(size_t)(group_base + g) * HD + d] = psum(g, d) * (1.0f / ml[1][g]);
+            outz[(size_t)(group_base + g) * HD + d] = psum(g, d) * (1.0f / ml[1][g]);
         }
         return;
     }
@@ -747,7 +756,7 @@ __global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
     // no fence, and the merge reads spread over G blocks
     const unsigned ep = ep0 + 1u;
     const unsigned long long tag = (unsigned long long)ep << 32;
-    unsigned long long* wsk = a.ws + (size_t)kvh * a.max_splits * G * (2 + HD);
+    unsigned long long* wsk = a.ws + ((size_t)z * a.n_kv + kvh) * a.max_splits * G * (2 + HD);
     {
         unsigned long long* wsb = wsk + (size_t)split * G * (2 + HD);
         for (int i = tid; i < G * HD; i += NT) {
@@ -852,7 +861,7 @@ __global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
                 }
             __syncthreads();
         }
-        if (tid < HD) a.out[(size_t)(group_base + g) * HD + tid] = O / L;
+        if (tid < HD) outz[(size_t)(group_base + g) * HD + tid] = O / L;
     }
     if (back == 0 && tid == 0 && !a.epoch) a.counters[kvh] = ep;   // the next launch's epoch base (stream order)
 }
@@ -1658,11 +1667,107 @@ __global__ void __launch_bounds__(256) lowrank_batched_kernel(const uint16_t* X,
     if (threadIdx.x == 0) tmp[(size_t)m * k + j] = p * S[j];
 }
 
-template <int TB, int TG, int RBW>
+// Batched operands from fp32 rows (prefill): one block per token (padded
+// tokens of the last 16-token group: zero fragments).  x' = (x * inv) * w as
+// gsd_lq_cpu_engine.c:66-82, then (u, v) * 2^e as fp16 high and low parts
+// at xa[((g16 * nc + c) * 8 + hl * 4 + h * 2 + t) * 64 + (m & 15) + 16 lg]
+// (pair 64c + 32h + 8lg + 4t + e, component e of the uint4), and the rank-k
+// projections of the tensors that read this input.
+__device__ float block_max(float v, float* lds) {
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+    v = wave_max(v);
+    __syncthreads();
+    if (lane == 0) lds[wid] = v;
+    __syncthreads();
+    float t = 0.f;
+    for (int w = 0; w < nw; w++) t = fmaxf(t, lds[w]);
+    return t;
+}
+
+__global__ void __launch_bounds__(256) batch_prep_kernel(const BatchPrep p) {
+    __shared__ float scratch[16];
+    constexpr float kS32 = 0.866025403784438646763723170752936183f;
+    const int m = blockIdx.x, tid = threadIdx.x;
+    const int nc = (p.cols + 127) >> 7, np = p.cols >> 1;
+    const bool valid = m < p.M;
+    const float* xr = p.X + (size_t)(valid ? m : 0) * p.ldx;
+    float inv = 1.f;
+    if (p.norm_w) {
+        float ss = 0.f;
+        if (valid)
+            for (int c = tid; c < p.cols; c += 256) ss = fmaf(xr[c], xr[c], ss);
+        ss = block_sum(ss, scratch);
+        inv = 1.0f / sqrtf(ss / (float)p.cols + p.eps);
+    }
+    auto xprime = [&](int c) { return p.norm_w ? (xr[c] * inv) * p.norm_w[c] : xr[c]; };
+    float mx = 0.f;
+    if (valid)
+        for (int q = tid; q < np; q += 256) {
+            const float xa = xprime(2 * q), xb = xprime(2 * q + 1);
+            p.xn[(size_t)m * p.cols + 2 * q] = xa;
+            p.xn[(size_t)m * p.cols + 2 * q + 1] = xb;
+            mx = fmaxf(mx, fmaxf(fabsf(xa), fabsf(fmaf(kS32, xb, 0.5f * xa))));
+        }
+    mx = block_max(mx, scratch);
+    // rank-k projections (block-wide sums in a fixed order)
+    for (int g = 0; g < kMaxSeg; g++) {
+        for (int j = 0; j < p.k[g]; j++) {
+            float d = 0.f;
+            if (valid) {
+                const uint16_t* vt = p.Vt[g] + (size_t)j * p.cols;
+                for (int c = tid; c < p.cols; c += 256) d = fmaf(xprime(c), h2f(vt[c]), d);
+            }
+            d = block_sum(d, scratch);
+            if (valid && tid == 0) p.tmp[g][(size_t)m * p.k[g] + j] = d * p.S[g][j];
+        }
+    }
+    int ex = 0;
+    if (mx > 0.f && mx < INFINITY) (void)frexpf(mx, &ex);
+    const float up = ldexpf(1.f, 14 - ex);
+    if (tid == 0) p.xs[m] = valid ? ldexpf(1.f, ex - 14) : 0.f;
+    uint32_t* x32 = reinterpret_cast<uint32_t*>(p.xa);
+    const int g16 = m >> 4, ml = m & 15;
+    for (int q = tid; q < nc * 64; q += 256) {
+        float u = 0.f, v = 0.f;
+        if (valid && q < np) {
+            const float xa = xprime(2 * q), xb = xprime(2 * q + 1);
+            u = xa * up;
+            v = fmaf(kS32, xb, 0.5f * xa) * up;
+        }
+        const _Float16 uh = (_Float16)u, vh = (_Float16)v;
+        const _Float16 ul = (_Float16)(u - (float)uh), vl = (_Float16)(v - (float)vh);
+        const int c = q >> 6, h = (q >> 5) & 1, lg = (q >> 3) & 3, t = (q >> 2) & 1, e = q & 3;
+        const size_t i0 = ((((size_t)g16 * nc + c) * 8 + h * 2 + t) * 64 + ml + 16 * lg) * 4 + e;
+        const size_t i1 = i0 + 4 * 64 * 4;   // the low parts: 4 fragments on
+        x32[i0] = (uint32_t)__builtin_bit_cast(uint16_t, uh) | ((uint32_t)__builtin_bit_cast(uint16_t, vh) << 16);
+        x32[i1] = (uint32_t)__builtin_bit_cast(uint16_t, ul) | ((uint32_t)__builtin_bit_cast(uint16_t, vl) << 16);
+    }
+}
+
+__global__ void __launch_bounds__(256) embed_rows_kernel(const uint16_t* embed, const int* tokens, float* X, int hidden) {
+    const int m = blockIdx.y, i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < hidden) X[(size_t)m * hidden + i] = h2f(embed[(size_t)tokens[m] * hidden + i]);
+}
+
+// y of one (token, row) of a batched projection: descaled sum, kinks, rank-k
+__device__ __forceinline__ float hexmm_finish(const MatmulArgs& a, int m, int row, float s) {
+    float y = s * a.xs[m];
+    if (a.w.row_ptr) {
+        const uint32_t e = a.w.row_ptr[row + 1];
+        for (uint32_t j = a.w.row_ptr[row]; j < e; j++)
+            y += a.w.kdel[j] * (a.Xf ? a.Xf[(size_t)m * a.cols + a.w.kcols[j]] : bf2f(a.X[(size_t)m * a.cols + a.w.kcols[j]]));
+    }
+    if (a.w.k > 0)
+        for (int j = 0; j < a.w.k; j++) y += h2f(a.w.U[(size_t)row * a.w.k + j]) * a.tmp_k[(size_t)m * a.w.k + j];
+    return y;
+}
+
+template <int TB, int TG, int RBW, bool HL>
 __global__ void __launch_bounds__(512) hexmm_kernel(const MatmulArgs a) {
     constexpr int W = 8;
+    constexpr int FPG = HL ? 8 : 4;   // A fragments per token group and chunk
     __shared__ __attribute__((aligned(16))) uint32_t stab[TB > 0 ? TB * 64 : 1];
-    __shared__ uint4 As[TG * 4 * 64];
+    __shared__ uint4 As[TG * FPG * 64];
     extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int nc = (a.cols + 127) >> 7;
@@ -1695,14 +1800,15 @@ __global__ void __launch_bounds__(512) hexmm_kernel(const MatmulArgs a) {
         }
     };
     // this thread's share of the block's A fragments for chunk c
-    constexpr int APT = (TG * 256 + 511) / 512;
+    constexpr int APT = (TG * FPG * 64 + 511) / 512;
     auto aload = [&](int c, uint4 (&av)[APT]) {
         c = min(c, nc - 1);
 #pragma unroll
         for (int i = 0; i < APT; i++) {
             const int j = tid + i * 512;
-            const int tg = j >> 8, g = min(g0 + tg, ng - 1);
-            av[i] = j < TG * 256 ? a.xa[((size_t)g * nc + c) * 256 + (j & 255)] : make_uint4(0u, 0u, 0u, 0u);
+            const int tg = j / (FPG * 64), g = min(g0 + tg, ng - 1);
+            av[i] = j < TG * FPG * 64 ? a.xa[((size_t)g * nc + c) * (FPG * 64) + (j % (FPG * 64))]
+                                      : make_uint4(0u, 0u, 0u, 0u);
         }
     };
     uint4 av[APT];
@@ -1763,13 +1869,17 @@ __global__ void __launch_bounds__(512) hexmm_kernel(const MatmulArgs a) {
                 }
 #pragma unroll
                 for (int g = 0; g < TG; g++) {
-                    const uint4 xv = As[(g * 4 + h * 2 + t) * 64 + lane];
-                    u32x4v aw;
-                    aw[0] = xv.x; aw[1] = xv.y; aw[2] = xv.z; aw[3] = xv.w;
 #pragma unroll
-                    for (int r = 0; r < RBW; r++)
-                        d[r][g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, aw),
-                                                                        __builtin_bit_cast(half8v, bw[r]), d[r][g], 0, 0, 0);
+                    for (int hl = 0; hl < (HL ? 2 : 1); hl++) {   // high part, then low part
+                        const uint4 xv = As[(g * FPG + hl * 4 + h * 2 + t) * 64 + lane];
+                        u32x4v aw;
+                        aw[0] = xv.x; aw[1] = xv.y; aw[2] = xv.z; aw[3] = xv.w;
+#pragma unroll
+                        for (int r = 0; r < RBW; r++)
+                            d[r][g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, aw),
+                                                                            __builtin_bit_cast(half8v, bw[r]), d[r][g], 0,
+                                                                            0, 0);
+                    }
                 }
             }
 #pragma unroll
@@ -1789,7 +1899,7 @@ __global__ void __launch_bounds__(512) hexmm_kernel(const MatmulArgs a) {
         lds_barrier();
 #pragma unroll
         for (int i = 0; i < APT; i++)
-            if (tid + i * 512 < TG * 256) As[tid + i * 512] = av[i];
+            if (tid + i * 512 < TG * FPG * 64) As[tid + i * 512] = av[i];
         aload(c + 1, av);
         lds_barrier();
         compute(cA, sA);
@@ -1798,7 +1908,7 @@ __global__ void __launch_bounds__(512) hexmm_kernel(const MatmulArgs a) {
             lds_barrier();
 #pragma unroll
             for (int i = 0; i < APT; i++)
-                if (tid + i * 512 < TG * 256) As[tid + i * 512] = av[i];
+                if (tid + i * 512 < TG * FPG * 64) As[tid + i * 512] = av[i];
             aload(c + 2, av);
             lds_barrier();
             compute(cB, sB);
@@ -1821,16 +1931,9 @@ __global__ void __launch_bounds__(512) hexmm_kernel(const MatmulArgs a) {
                     a.part[((size_t)ks * ng * 16 + m) * rows + row] = acc[r][g][i];
                     continue;
                 }
-                float y = acc[r][g][i] * a.xs[m];
-                if (a.w.row_ptr) {
-                    const uint32_t e = a.w.row_ptr[row + 1];
-                    for (uint32_t j = a.w.row_ptr[row]; j < e; j++)
-                        y += a.w.kdel[j] * bf2f(a.X[(size_t)m * a.cols + a.w.kcols[j]]);
-                }
-                if (a.w.k > 0)
-                    for (int j = 0; j < a.w.k; j++)
-                        y += h2f(a.w.U[(size_t)row * a.w.k + j]) * a.tmp_k[(size_t)m * a.w.k + j];
-                a.Y[(size_t)m * rows + row] = y;
+                const float y = hexmm_finish(a, m, row, acc[r][g][i]);
+                float* yp = a.Y + (size_t)m * rows + row;
+                *yp = a.accumulate ? *yp + y : y;
             }
         }
     }
@@ -1845,14 +1948,8 @@ __global__ void __launch_bounds__(256) hexmm_reduce_kernel(const MatmulArgs a) {
     const int m = (int)(i / rows), row = (int)(i % rows);
     float s = 0.f;
     for (int k = 0; k < a.nsplit; k++) s += a.part[((size_t)k * ng * 16 + m) * rows + row];
-    float y = s * a.xs[m];
-    if (a.w.row_ptr) {
-        const uint32_t e = a.w.row_ptr[row + 1];
-        for (uint32_t j = a.w.row_ptr[row]; j < e; j++) y += a.w.kdel[j] * bf2f(a.X[(size_t)m * a.cols + a.w.kcols[j]]);
-    }
-    if (a.w.k > 0)
-        for (int j = 0; j < a.w.k; j++) y += h2f(a.w.U[(size_t)row * a.w.k + j]) * a.tmp_k[(size_t)m * a.w.k + j];
-    a.Y[i] = y;
+    const float y = hexmm_finish(a, m, row, s);
+    a.Y[i] = a.accumulate ? a.Y[i] + y : y;
 }
 
 }  // namespace
@@ -2005,12 +2102,12 @@ hipError_t launch_hexmv4(const HexArgs& a, hipStream_t st) {
 #undef GSD_MV4
 }
 
-size_t hexmm_xa_bytes(int M, int cols) {
+size_t hexmm_xa_bytes(int M, int cols, int hl) {
     const size_t ng = ((size_t)M + 15) / 16, nc = ((size_t)cols + 127) / 128;
-    return ng * nc * 4 * 64 * 16;
+    return ng * nc * (hl ? 8 : 4) * 64 * 16;
 }
 
-template <int TB, int TG, int RBW>
+template <int TB, int TG, int RBW, bool HL>
 hipError_t launch_hexmm_t(const MatmulArgs& a, hipStream_t st) {
     const int nrb = (a.w.rows + 15) / 16, ng = (a.M + 15) / 16;
     const int n_rt = (nrb + 8 * RBW - 1) / (8 * RBW), n_tt = (ng + TG - 1) / TG;
@@ -2019,13 +2116,13 @@ hipError_t launch_hexmm_t(const MatmulArgs& a, hipStream_t st) {
     if (lds > 0) {
         static size_t attr = 0;
         if (lds > attr) {
-            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&hexmm_kernel<TB, TG, RBW>),
+            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&hexmm_kernel<TB, TG, RBW, HL>),
                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
             if (e != hipSuccess) return e;
             attr = lds;
         }
     }
-    hipLaunchKernelGGL((hexmm_kernel<TB, TG, RBW>), dim3(grid), dim3(512), lds, st, a);
+    hipLaunchKernelGGL((hexmm_kernel<TB, TG, RBW, HL>), dim3(grid), dim3(512), lds, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.nsplit <= 1) return e;
     const size_t n = (size_t)a.M * a.w.rows;
@@ -2058,14 +2155,48 @@ MatmulPlan hexmm_plan(int M, int rows, int cols) {
 
 template <int TB>
 hipError_t launch_hexmm_tb(const MatmulArgs& a, hipStream_t st) {
-    if (a.tg == 8 && a.rbw == 2) return launch_hexmm_t<TB, 8, 2>(a, st);
-    if (a.tg == 4 && a.rbw == 1) return launch_hexmm_t<TB, 4, 1>(a, st);
-    if (a.tg == 2 && a.rbw == 1) return launch_hexmm_t<TB, 2, 1>(a, st);
-    if (a.tg == 1 && a.rbw == 1) return launch_hexmm_t<TB, 1, 1>(a, st);
+    if (a.hl) {
+        if (a.tg == 8 && a.rbw == 2) return launch_hexmm_t<TB, 8, 2, true>(a, st);
+        if (a.tg == 4 && a.rbw == 1) return launch_hexmm_t<TB, 4, 1, true>(a, st);
+        if (a.tg == 2 && a.rbw == 1) return launch_hexmm_t<TB, 2, 1, true>(a, st);
+        if (a.tg == 1 && a.rbw == 1) return launch_hexmm_t<TB, 1, 1, true>(a, st);
+        return hipErrorInvalidValue;
+    }
+    if (a.tg == 8 && a.rbw == 2) return launch_hexmm_t<TB, 8, 2, false>(a, st);
+    if (a.tg == 4 && a.rbw == 1) return launch_hexmm_t<TB, 4, 1, false>(a, st);
+    if (a.tg == 2 && a.rbw == 1) return launch_hexmm_t<TB, 2, 1, false>(a, st);
+    if (a.tg == 1 && a.rbw == 1) return launch_hexmm_t<TB, 1, 1, false>(a, st);
     return hipErrorInvalidValue;
 }
 
+hipError_t launch_hexmm_prepared(const MatmulArgs& a, hipStream_t st) {
+    if (a.M <= 0 || a.cols <= 0 || a.cols % 64 || !a.w.codes_t || !a.w.scales_t || !a.w.fields) return hipErrorInvalidValue;
+    if (!a.hl || !a.Xf || !a.xa || !a.xs) return hipErrorInvalidValue;
+    if (a.nsplit < 1 || (a.nsplit > 1 && !a.part)) return hipErrorInvalidValue;
+    if (a.w.k > 0 && (!a.tmp_k || !a.w.U)) return hipErrorInvalidValue;
+    if (a.w.n_pts == 217) return launch_hexmm_tb<217>(a, st);
+    if (a.w.n_pts == 127) return launch_hexmm_tb<127>(a, st);
+    return launch_hexmm_tb<0>(a, st);
+}
+
+hipError_t launch_batch_prep(const BatchPrep& p, hipStream_t st) {
+    if (p.M <= 0 || p.cols <= 0 || p.cols % 64 || p.ldx < p.cols || !p.X || !p.xa || !p.xs || !p.xn)
+        return hipErrorInvalidValue;
+    for (int g = 0; g < kMaxSeg; g++)
+        if (p.k[g] < 0 || p.k[g] > kMaxRank || (p.k[g] > 0 && (!p.Vt[g] || !p.S[g] || !p.tmp[g])))
+            return hipErrorInvalidValue;
+    hipLaunchKernelGGL(batch_prep_kernel, dim3(((p.M + 15) / 16) * 16), dim3(256), 0, st, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_rows(const uint16_t* embed, const int* tokens, int M, float* X, int hidden, hipStream_t st) {
+    if (M <= 0) return hipSuccess;
+    hipLaunchKernelGGL(embed_rows_kernel, dim3((hidden + 255) / 256, M), dim3(256), 0, st, embed, tokens, X, hidden);
+    return hipGetLastError();
+}
+
 hipError_t launch_hexmm(const MatmulArgs& a, hipStream_t st) {
+    if (a.hl) return hipErrorInvalidValue;
     if (a.M <= 0 || a.cols <= 0 || a.cols % 64 || !a.w.codes_t || !a.w.scales_t || !a.w.fields) return hipErrorInvalidValue;
     if (a.nsplit < 1 || (a.nsplit > 1 && !a.part)) return hipErrorInvalidValue;
     if (a.w.k > 0 && (!a.tmp_k || !a.w.U)) return hipErrorInvalidValue;
@@ -2109,6 +2240,16 @@ hipError_t launch_swiglu(const float* g, const float* u, float* out, int dim, hi
     return hipGetLastError();
 }
 
+hipError_t launch_rope_kv_rows(float* q, const float* k, const float* v, const RopeKV& r, int M, hipStream_t st) {
+    if (M <= 0 || !r.cs || r.pos_dev || r.pos < 0 || r.pos + M > r.max_seq) return hipErrorInvalidValue;
+    CsInline csi;
+    const int half = r.hd / 2;
+    int n = r.n_heads * half;
+    if (r.n_kv * r.hd > n) n = r.n_kv * r.hd;
+    hipLaunchKernelGGL(rope_kv_kernel, dim3((n + 255) / 256, M), dim3(256), 0, st, q, k, v, r, csi, 0);
+    return hipGetLastError();
+}
+
 hipError_t launch_rope_kv(float* q, const float* k, const float* v, const RopeKV& r, const float2* cs_inline,
                           hipStream_t st) {
     CsInline csi;
@@ -2132,7 +2273,9 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
     // score buffer
     if (a.max_splits < 1 || a.max_splits > 256 || a.chunk > 256 || (!a.counters && !a.epoch) || !a.ws)
         return hipErrorInvalidValue;
-    const dim3 grid(a.n_kv, a.max_splits);
+    const int nt = a.ntok > 1 ? a.ntok : 1;
+    if (nt > 1 && (!a.epoch || a.pos_dev)) return hipErrorInvalidValue;
+    const dim3 grid(a.n_kv, a.max_splits, nt);
     const int G = a.n_heads / a.n_kv;
     // 16 waves for up to 4 query heads per KV head (8 would not fit the
     // registers of 16), else 4

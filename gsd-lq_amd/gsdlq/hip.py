@@ -54,6 +54,8 @@ SIGNATURES = {
     "gsdh_model_vector": [vp, i32, i32, vp, u64],
     "gsdh_model_set_step": [vp, i32, i32],
     "gsdh_model_read_kv": [vp, i32, i32, vp, vp],
+    "gsdh_model_prefill": [vp, vp, i32, i32, i32, vp, ctypes.POINTER(i32)],
+    "gsdh_model_set_prefill": [vp, i32],
 }
 RESTYPES = {"gsdh_model_device_bytes": (u64, [vp]), "gsdh_model_stream": (vp, [vp]),
             "gsdh_model_engine": (i32, [vp]),

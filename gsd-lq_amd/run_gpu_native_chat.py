@@ -322,6 +322,28 @@ class GPUMistralV2Model:
         self.cl.lib.gsdh_forward_token(self._m, int(token_id), int(pos), 0, None, None)
         return None
 
+    def prefill(self, token_ids, start_pos: int = 0, return_logits: bool = True):
+        """The prompt tokens token_ids at positions start_pos.. through every
+        layer at once (batched projections on the matrix cores, causal
+        attention over the cache; positions below start_pos are reused as
+        cached).  Returns the last token's f32 logits (vocab,) when
+        return_logits, else None.  The reference runs forward_token per prompt
+        token (run_gpu_native_chat.py:1128-1130); the results agree with it."""
+        ids = np.ascontiguousarray(np.asarray(token_ids, dtype=np.int32))
+        if ids.size == 0:
+            raise ValueError("prefill: no tokens")
+        am = ctypes.c_int(-1)
+        if return_logits:
+            self.cl.lib.gsdh_model_prefill(self._m, _hip.ptr(ids), int(ids.size), int(start_pos), 1,
+                                           _hip.ptr(self._logits), ctypes.byref(am))
+            return self._logits.copy()
+        self.cl.lib.gsdh_model_prefill(self._m, _hip.ptr(ids), int(ids.size), int(start_pos), 0, None, None)
+        return None
+
+    def set_prefill(self, batched: bool) -> None:
+        """generate_greedy's prompt: batched (default) or one decode step per token."""
+        self.cl.lib.gsdh_model_set_prefill(self._m, 1 if batched else 0)
+
     def generate_greedy(self, prompt_ids, n_new: int, start_pos: int = 0):
         """Prefill prompt_ids at start_pos.. then n_new greedy tokens, all on
         the device (one graph launch per token, no logits round trip).
@@ -409,9 +431,7 @@ def run_smoke_verify(model) -> str:
     """Greedy 8 tokens after "The capital of France is" (run_gpu_native_chat.py:1039-1055)."""
     prompt = "The capital of France is"
     ids = model.tokenizer.encode(prompt, add_bos=True)
-    logits = None
-    for pos, tid in enumerate(ids):
-        logits = model.forward_token(tid, pos, return_logits=(pos == len(ids) - 1))
+    logits = model.prefill(ids, 0)
     out_ids = []
     pos = len(ids)
     for _ in range(8):
@@ -471,9 +491,8 @@ def main(argv=None):
                 prefix = 0
                 ids = model.tokenizer.encode(format_mistral_prompt(history, msg), add_bos=True)
             t0 = time.time()
-            logits = None
-            for pos in range(prefix, len(ids)):
-                logits = model.forward_token(ids[pos], pos, return_logits=(pos == len(ids) - 1))
+            # the new prompt tokens in one batched pass over the reused prefix
+            logits = model.prefill(ids[prefix:], prefix)
             pre_s = time.time() - t0
             print("\nMistral-7B (GPU Native) > ", end="", flush=True)
             t1, gen, prev, pos = time.time(), [], "", len(ids)

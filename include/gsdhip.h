@@ -191,9 +191,30 @@ int gsdh_forward_token(gsdh_model* m, int token_id, int pos, int want_logits,
 
 /* Prefill prompt[0..n_prompt) at positions start_pos.., then n_new greedy
  * steps entirely on the device; writes the generated ids and the top1-top2
- * logit margin of every step. */
+ * logit margin of every step.  The prompt goes through gsdh_model_prefill's
+ * batched forward (gsdh_model_set_prefill(m, 0): token by token through the
+ * decode graph, as the reference does). */
 int gsdh_generate_greedy(gsdh_model* m, const int* prompt, int n_prompt, int start_pos, int n_new,
                          int* tokens_out, float* margins_out);
+
+/* Batched prefill (the reference prefills token by token,
+ * run_gpu_native_chat.py:1128-1130, reusing a cached prefix, :1112-1115):
+ * tokens[0..n) at positions start_pos.. through every layer at once, in
+ * chunks of 128 tokens: per layer the q/k/v, o, gate/up and down projections
+ * of all the chunk's tokens on the matrix cores (activations as fp16 high +
+ * low parts, fp32 accumulation, RMSNorm / rank-k / kink terms as the
+ * reference computes them), RoPE and fp16 K/V append at every position, and
+ * causal attention of each token over the cache positions 0..its own (a
+ * cached prefix below start_pos is reused).  When want_logits, the last
+ * token's logits are copied to logits_host (may be NULL) and its greedy
+ * token to *argmax_out; the step state then holds position start_pos + n
+ * for the next decode step.  Allocates nothing (the workspace is the
+ * model's, sized at finalize).  Synchronous. */
+int gsdh_model_prefill(gsdh_model* m, const int* tokens, int n, int start_pos, int want_logits,
+                       float* logits_host, int* argmax_out);
+/* 1: generate_greedy prefills with gsdh_model_prefill (the default); 0: one
+ * decode-graph launch per prompt token. */
+int gsdh_model_set_prefill(gsdh_model* m, int batched);
 
 /* Batched projection for prefill on the matrix cores: Y[m][r] = (W x_m)[r] for
  * the packed tensor (layer, slot) of the model and M tokens at once, kinks and
@@ -204,8 +225,8 @@ int gsdh_generate_greedy(gsdh_model* m, const int* prompt, int n_prompt, int sta
  * gsd_lq_cpu_engine.c:129-183) per token, with the token's (u, v) pair terms
  * rounded once to fp16 (about 1e-4 relative).  No counterpart in the
  * reference, which prefills token by token (run_gpu_native_chat.py:1128-1130).
- * Grows its staging workspace with hipMalloc when M or cols exceed earlier
- * calls (so a first call of a size is not graph-capturable). */
+ * M <= 512 per call; the staging lives in the model's workspace (sized at
+ * finalize), so the call allocates nothing and can be graph-captured. */
 int gsdh_model_matmul(gsdh_model* m, int layer, int slot, const uint16_t* X, int M, float* Y);
 
 /* The codes of packed tensor (layer, slot) as the device holds them, decoded

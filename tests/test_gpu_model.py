@@ -243,7 +243,8 @@ GREEDY_7B = os.path.join(GOLDEN, "greedy_7b_precision.json")
 @pytest.mark.skipif(not os.path.exists(GREEDY_7B), reason="7B golden sequence not generated")
 def test_greedy_7b_precision_128_steps():
     """Mistral-7B-shaped, 32 layers, Precision (radius 6, rank 2): 64-token
-    seeded prompt then 128 greedy steps must equal the reference engine's."""
+    seeded prompt (batched prefill) then 128 greedy steps must equal the
+    reference engine's."""
     from gsdlq import synth
     import run_gpu_native_chat as chat
     g = json.load(open(GREEDY_7B))
@@ -260,11 +261,12 @@ def test_greedy_7b_precision_128_steps():
         print(f"first mismatch at step {first_diff}: gpu {toks[first_diff]} ref {g['tokens'][first_diff]} "
               f"ref margin {g['margins'][first_diff]:.3e} gpu margin {margins[first_diff]:.3e}", flush=True)
     assert toks == g["tokens"]
-    # top-1 logit of the first step against the reference's value
-    lg = gpu.forward_token(g["prompt"][-1], len(g["prompt"]) - 1)
+    # top-5 logits of the first step against the reference's values: from
+    # the batched prefill of the whole prompt and from one decode step
     top = g["top5"][0]
-    for i, v in top:
-        assert abs(lg[i] - v) <= 1e-3 * max(1.0, abs(v))
+    for lg in (gpu.prefill(g["prompt"], 0), gpu.forward_token(g["prompt"][-1], len(g["prompt"]) - 1)):
+        for i, v in top:
+            assert abs(lg[i] - v) <= 1e-3 * max(1.0, abs(v))
     gpu.close()
 
 
