@@ -134,7 +134,9 @@ class MistralSentencePieceTokenizer:
 
     def encode(self, text: str, add_bos: bool = True):
         ids = [self.bos_id] if add_bos else []
-        parts = re.split("(" + "|".join(re.escape(s) for s in self.specials) + ")", text) if self.specials else [text]
+        # with no special tokens the pattern is "()", which matches the empty
+        # string: every character becomes a part of its own, as in the reference
+        parts = re.split("(" + "|".join(re.escape(s) for s in self.specials) + ")", text)
         first = True
         for part in parts:
             if not part:

@@ -190,3 +190,38 @@ def test_tokenizer_roundtrip_placeholder_vocab():
     ids = t.encode("</s>é")
     assert 2 in ids
     assert t.decode(ids).strip() == "é"
+
+
+def _tok_golden():
+    import json
+    from conftest import GOLDEN
+    with open(os.path.join(GOLDEN, "tokenizer_golden.json"), encoding="utf-8") as f:
+        return json.load(f)
+
+
+@pytest.mark.parametrize("vocab", ["with_specials", "no_specials"])
+def test_tokenizer_matches_reference_vectors(vocab):
+    """encode / decode equal the reference tokenizer's outputs
+    (run_gpu_native_chat.py:660-729, vectors written by
+    tests/golden/make_tokenizer_golden.py), with type-3 special tokens and
+    with none (every character then a part of its own)."""
+    import run_gpu_native_chat as chat
+    v = _tok_golden()["vocabularies"][vocab]
+    tk = chat.MistralSentencePieceTokenizer(v["tokens"], v["scores"], v["token_types"], 1, 2)
+    for c in v["encode"]:
+        assert tk.encode(c["text"], add_bos=c["add_bos"]) == c["ids"], c["text"]
+        assert tk.decode(c["ids"]) == c["decoded"], c["text"]
+    for c in v["decode"]:
+        assert tk.decode(c["ids"]) == c["decoded"]
+
+
+def test_prompt_format_matches_reference_vectors():
+    """format_mistral_prompt equals the reference's (run_gpu_native_chat.py:
+    996-1013) with its system text replaced by this build's (which names the
+    MI355X instead of the reference's GPU)."""
+    import run_gpu_native_chat as chat
+    g = _tok_golden()
+    for c in g["format"]:
+        hist = [tuple(h) for h in c["history"]]
+        want = c["prompt"].replace(g["system_rules"], chat.SYSTEM_RULES)
+        assert chat.format_mistral_prompt(hist, c["msg"], is_cpu=c["is_cpu"]) == want

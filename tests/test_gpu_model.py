@@ -4,6 +4,7 @@ small synthetic models (every step checked) and on the 32-layer
 Mistral-7B-shaped Precision model (128 greedy steps, golden sequence written
 by the reference engine)."""
 import json
+import sys
 import os
 
 import numpy as np
@@ -311,3 +312,44 @@ def test_decode_past_2048_to_4096(engine):
     for pos, want in L["rewrites"].items():
         assert rel_l2(gpu.forward_token(L["toks"][0], pos), want) < 1e-3, pos
     gpu.close()
+
+
+def test_gsd2_file_through_drop_in(tmp_path, monkeypatch, capsys):
+    """The drop-in's file path: a written .gsd2 (Precision, kinks) loaded by
+    GPUMistralV2Model(path) against the oracle reading the same file with its
+    own reader (FileSource), the smoke command main([path, '--smoke']) and two
+    chat turns of main([path]) over stdin (the second reusing the first's KV
+    prefix, run_gpu_native_chat.py:1112-1131)."""
+    import io
+    from gsdlq import synth
+    import run_gpu_native_chat as chat
+    spec = _spec(mode="precision", kinks_per_row=2, n_layers=2)
+    path = str(tmp_path / "tiny.gsd2")
+    synth.write_gsd2(spec, path)
+    banner(f"drop-in from {os.path.basename(path)}")
+    gpu = chat.GPUMistralV2Model(path, rope_interleaved=1, verbose=False)
+    ref = O.OracleModel(O.FileSource(path), kind="port", max_seq_len=gpu.max_seq_len)
+    assert gpu.n_layers == 2 and gpu.vocab_size == spec.vocab
+    toks = np.random.default_rng(12).integers(0, gpu.vocab_size, 12).tolist()
+    for pos, t in enumerate(toks):
+        assert rel_l2(gpu.forward_token(t, pos), ref.forward_token(t, pos)) < 1e-3, pos
+    # the smoke verify's greedy text equals the oracle's greedy continuation
+    ids = gpu.tokenizer.encode("The capital of France is", add_bos=True)
+    want_ids, _ = ref.generate_greedy(ids, 8)
+    eos = gpu.tokenizer.eos_id
+    want_ids = want_ids[:want_ids.index(eos)] if eos in want_ids else want_ids
+    got = chat.run_smoke_verify(gpu)
+    assert got == gpu.tokenizer.decode(want_ids)
+    gpu.close()
+    capsys.readouterr()
+    chat.main([path, "--smoke"])
+    assert "[SMOKE TEST]" in capsys.readouterr().out
+    # two chat turns, then quit; turns are logged
+    log = tmp_path / "chat_log.md"
+    monkeypatch.setattr(chat, "LOG_FILE", str(log))
+    monkeypatch.setattr(sys, "stdin", io.StringIO("Hello there\nAnd again\nquit\n"))
+    chat.main([path])
+    out = capsys.readouterr().out
+    assert out.count("[GPU Stats: Prefill") == 2
+    text = log.read_text(encoding="utf-8")
+    assert "### Turn 1" in text and "### Turn 2" in text

@@ -9,6 +9,7 @@ import numpy as np
 import pytest
 
 import oracle as O
+from gsdlq import synth
 from conftest import rel_l2
 
 P = O.P
@@ -356,3 +357,100 @@ def test_attention_closed_forms():
     lib.gsd_cpu_gqa_attention(P(q), P(kc2.view(np.uint16)), P(vc.view(np.uint16)), P(out), 0, 9, nh, nkv, hd, ms, 0.125)
     for h in range(nh):
         assert rel_l2(out[h * hd:(h + 1) * hd], V[:10, h // 4].mean(0)) < 1e-6
+
+
+# ---------------------------------------------------------------------------
+# The oracle's composition (OracleModel.forward_token) against an independent
+# float64 NumPy forward written from the reference's per-token order
+# (gsd_lq_cpu_runtime.py:302-420) with its own dense dequantisation of every
+# packed tensor (codebook closed form, fp16 block scales, CSR kinks,
+# U diag(S) Vt), so a misreading shared by the oracle's driver and the
+# engine's (a head mapping, a residual, the RoPE pairing) cannot hide.
+# ---------------------------------------------------------------------------
+def _dense_f64(src, name):
+    m = src.tensors[name]
+    R, rows, cols, k = m["radius"], m["rows"], m["cols"], m["k_dim"]
+    s3 = np.sqrt(3.0) / 2.0
+    T = np.array([(a + 0.5 * b, b * s3) for a in range(-R, R + 1) for b in range(-R, R + 1) if abs(a + b) <= R])
+    codes = np.asarray(src.hex_field(name, "codes")).reshape(rows, cols // 2)
+    W = T[codes].reshape(rows, cols)
+    sc = np.asarray(src.hex_field(name, "scales")).view(np.float16).astype(np.float64).reshape(rows, cols // 64)
+    W = W * np.repeat(sc, 64, axis=1)
+    rp = np.asarray(src.hex_field(name, "row_ptr"))
+    kc = np.asarray(src.hex_field(name, "kink_cols"))
+    kd = np.asarray(src.hex_field(name, "kink_deltas")).astype(np.float64)
+    for r in range(rows):
+        for i in range(rp[r], rp[r + 1]):
+            W[r, kc[i]] += kd[i]
+    if k > 0:
+        U = np.asarray(src.hex_field(name, "U")).view(np.float16).astype(np.float64).reshape(rows, k)
+        S = np.asarray(src.hex_field(name, "S")).astype(np.float64)
+        Vt = np.asarray(src.hex_field(name, "Vt")).view(np.float16).astype(np.float64).reshape(k, cols)
+        W = W + U @ (S[:, None] * Vt)
+    return W
+
+
+class _F64Model:
+    def __init__(self, src, interleaved):
+        c = src.config
+        self.L, self.H, self.nh, self.nkv = c["n_layers"], c["hidden_size"], c["n_heads"], c["n_kv_heads"]
+        self.hd, self.eps, self.theta = c["head_dim"], c["rms_eps"], c["rope_theta"]
+        self.il = interleaved
+        self.emb = np.asarray(src.dense("token_embd.weight", np.float16)).astype(np.float64)
+        self.W = {n: _dense_f64(src, n) for n in src.tensors if "k_dim" in src.tensors[n]}
+        self.norm = {n: np.asarray(src.dense(n, np.float32)).astype(np.float64)
+                     for n in src.tensors if n.endswith("norm.weight")}
+        self.kc = {}
+        self.vc = {}
+
+    def rms(self, x, w):
+        return x / np.sqrt(np.mean(x * x) + self.eps) * w
+
+    def rope(self, v, pos):
+        hd, half = self.hd, self.hd // 2
+        ang = pos / self.theta ** (np.arange(half) * 2.0 / hd)
+        c, s = np.cos(ang), np.sin(ang)
+        v = v.reshape(-1, hd).copy()
+        i0 = np.arange(half) * 2 if self.il else np.arange(half)
+        i1 = i0 + 1 if self.il else i0 + half
+        a, b = v[:, i0].copy(), v[:, i1].copy()
+        v[:, i0], v[:, i1] = a * c - b * s, a * s + b * c
+        return v
+
+    def forward(self, tok, pos):
+        x = self.emb[tok].copy()
+        g = self.nh // self.nkv
+        for l in range(self.L):
+            p = f"blk.{l}."
+            xb = self.rms(x, self.norm[p + "attn_norm.weight"])
+            q = self.rope(self.W[p + "attn_q.weight"] @ xb, pos)
+            k = self.rope(self.W[p + "attn_k.weight"] @ xb, pos)
+            v = (self.W[p + "attn_v.weight"] @ xb).reshape(self.nkv, self.hd)
+            f16 = lambda a: a.astype(np.float16).astype(np.float64)
+            self.kc[(l, pos)], self.vc[(l, pos)] = f16(k), f16(v)
+            K = np.stack([self.kc[(l, t)] for t in range(pos + 1)])      # [t, nkv, hd]
+            V = np.stack([self.vc[(l, t)] for t in range(pos + 1)])
+            att = np.empty((self.nh, self.hd))
+            for h in range(self.nh):
+                sc = K[:, h // g] @ q[h] / np.sqrt(self.hd)
+                e = np.exp(sc - sc.max())
+                att[h] = (e / e.sum()) @ V[:, h // g]
+            x = x + self.W[p + "attn_output.weight"] @ att.reshape(-1)
+            xb = self.rms(x, self.norm[p + "ffn_norm.weight"])
+            gt, up = self.W[p + "ffn_gate.weight"] @ xb, self.W[p + "ffn_up.weight"] @ xb
+            x = x + self.W[p + "ffn_down.weight"] @ (gt / (1.0 + np.exp(-gt)) * up)
+        return self.W["output.weight"] @ self.rms(x, self.norm["output_norm.weight"])
+
+
+@pytest.mark.parametrize("mode,il,kpr", [("precision", 1, 2), ("turbo", 0, 1)])
+def test_oracle_forward_vs_float64_numpy(mode, il, kpr):
+    spec = synth.SynthSpec(n_layers=2, hidden=128, ffn=256, n_heads=4, n_kv_heads=2, head_dim=32, vocab=300,
+                           mode=mode, kinks_per_row=kpr)
+    src = synth.SynthSource(spec)
+    ref = O.OracleModel(src, kind="port", max_seq_len=32, rope_interleaved=il)
+    f64 = _F64Model(src, il)
+    toks = np.random.default_rng(5).integers(0, spec.vocab, 9).tolist()
+    for pos, t in enumerate(toks):
+        want = f64.forward(t, pos)
+        got = ref.forward_token(t, pos)
+        assert rel_l2(got, want) < 1e-4, (mode, pos)
