@@ -16,6 +16,14 @@ tensors carry radius, rows, cols, k_dim and the blobs codes (u8, one per
 weight pair), scales (fp16 bits, one per 64 weights), row_ptr (u32, rows+1),
 kink_cols (u16), kink_deltas (f32) and, when k_dim > 0, U (fp16 [rows,k]),
 S (f32 [k]), Vt (fp16 [k,cols]).
+
+Extension (this build's writer only; the reference's loaders read u8 codes):
+a packed tensor whose codebook has at most 128 points (radius <= 6, the
+Precision mode) may carry "code_bits": 7, and then its codes blob holds the
+rows * cols / 2 codes as one little-endian bit stream of 7 bits each (code
+i at bits 7i .. 7i + 6, ceil(7n / 8) bytes): 3.76 instead of 4.26 bits per
+weight on disk for a rank-2 Precision model.  Readers return u8 codes either
+way.
 """
 from __future__ import annotations
 
@@ -41,6 +49,40 @@ FIELD_DTYPES = {
     "Vt": np.uint16,
 }
 LAYER_HEX = ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")
+def pack_codes7(codes: np.ndarray) -> np.ndarray:
+    """u8 codes (each < 128) as a 7-bit little-endian stream: code i at bits
+    7i .. 7i + 6; ceil(7 n / 8) bytes."""
+    c = np.ascontiguousarray(codes, dtype=np.uint8).reshape(-1)
+    n = c.size
+    if n and int(c.max()) >= 128:
+        raise ValueError("7-bit codes: a code is >= 128")
+    g = np.zeros((n + 7) // 8 * 8, dtype=np.uint64)
+    g[:n] = c
+    g = g.reshape(-1, 8)
+    word = np.zeros(g.shape[0], dtype=np.uint64)
+    for j in range(8):               # 8 codes -> one 56-bit group (7 bytes)
+        word |= g[:, j] << np.uint64(7 * j)
+    out = word.view(np.uint8).reshape(-1, 8)[:, :7].reshape(-1)
+    return np.ascontiguousarray(out[:(7 * n + 7) // 8])
+
+
+def unpack_codes7(blob: np.ndarray, n: int) -> np.ndarray:
+    """Inverse of pack_codes7: n u8 codes from the 7-bit stream."""
+    b = np.asarray(blob, dtype=np.uint8).reshape(-1)
+    if b.size != (7 * n + 7) // 8:
+        raise ValueError(f"7-bit codes: {b.size} bytes for {n} codes")
+    ng = (n + 7) // 8
+    g7 = np.zeros(ng * 7, dtype=np.uint8)
+    g7[:b.size] = b
+    pad = np.zeros((ng, 8), dtype=np.uint8)
+    pad[:, :7] = g7.reshape(ng, 7)
+    word = pad.reshape(-1).view(np.uint64)
+    out = np.empty((ng, 8), dtype=np.uint8)
+    for j in range(8):
+        out[:, j] = ((word >> np.uint64(7 * j)) & np.uint64(0x7F)).astype(np.uint8)
+    return out.reshape(-1)[:n]
+
+
 CONFIG_KEYS = ("n_layers", "hidden_size", "n_heads", "n_kv_heads", "head_dim", "ffn_size",
                "rms_eps", "rope_theta", "vocab_size", "tokens", "scores", "token_types",
                "bos_id", "eos_id")
@@ -92,7 +134,13 @@ class Gsd2File:
         return np.frombuffer(self._mm, dtype=dtype, count=n // itemsize, offset=off)
 
     def hex_field(self, name: str, field: str) -> np.ndarray:
-        return self.blob(self.tensors[name][field], FIELD_DTYPES[field])
+        meta = self.tensors[name]
+        bits = int(meta.get("code_bits", 8))
+        if field == "codes" and bits != 8:
+            if bits != 7 or int(meta["radius"]) > 6:
+                raise ValueError(f"{name}: code_bits {bits} with radius {meta['radius']} is not a valid encoding")
+            return unpack_codes7(self.blob(meta["codes"], np.uint8), int(meta["rows"]) * int(meta["cols"]) // 2)
+        return self.blob(meta[field], FIELD_DTYPES[field])
 
     def dense(self, name: str, dtype) -> np.ndarray:
         meta = self.tensors[name]["data"]
@@ -146,14 +194,25 @@ class Gsd2Writer:
 
     def add_hex(self, name: str, radius: int, rows: int, cols: int, k_dim: int,
                 fields: Optional[dict] = None, nbytes: Optional[dict] = None,
-                producer: Optional[Callable[[str], np.ndarray]] = None):
+                producer: Optional[Callable[[str], np.ndarray]] = None, code_bits: int = 8):
         """Register a packed tensor.  Either give the arrays (fields) or their
-        byte sizes (nbytes) plus producer(field) -> array, called at write time."""
+        byte sizes (nbytes) plus producer(field) -> array, called at write time.
+        code_bits = 7 stores the codes as a 7-bit stream (radius <= 6; fields only)."""
         meta = {"radius": int(radius), "rows": int(rows), "cols": int(cols), "k_dim": int(k_dim)}
+        if code_bits not in (7, 8):
+            raise ValueError(f"code_bits {code_bits}: 7 or 8")
+        if code_bits == 7:
+            if radius > 6:
+                raise ValueError(f"{name}: 7-bit codes need a codebook of at most 128 points (radius <= 6)")
+            if fields is None:
+                raise ValueError("7-bit codes are written from arrays")
+            meta["code_bits"] = 7
         names = HEX_FIELDS + (LOWRANK_FIELDS if k_dim > 0 else ())
         for fld in names:
             if fields is not None:
                 arr = np.ascontiguousarray(fields[fld], dtype=FIELD_DTYPES[fld])
+                if fld == "codes" and code_bits == 7:
+                    arr = pack_codes7(arr)
                 meta[fld] = self._add_blob(arr.nbytes, arr)
             else:
                 meta[fld] = self._add_blob(nbytes[fld], (producer, fld))
@@ -182,10 +241,10 @@ class Gsd2Writer:
             f.truncate(max(end, f.tell()))
 
 
-def hex_nbytes(rows: int, cols: int, k_dim: int, nk: int) -> dict:
+def hex_nbytes(rows: int, cols: int, k_dim: int, nk: int, code_bits: int = 8) -> dict:
     """Byte size of every blob of a packed tensor with nk kinks."""
     d = {
-        "codes": rows * cols // 2,
+        "codes": rows * cols // 2 if code_bits == 8 else (7 * (rows * cols // 2) + 7) // 8,
         "scales": rows * cols // 64 * 2,
         "row_ptr": (rows + 1) * 4,
         "kink_cols": nk * 2,

@@ -11,7 +11,9 @@ import ctypes
 import os
 
 _PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.path.join(_PKG_DIR, "libgsdhip.so")
+# GSD_HIP_LIB: another build of the engine library (e.g. to compare two
+# builds on one machine); the in-tree build otherwise
+LIB_PATH = os.environ.get("GSD_HIP_LIB") or os.path.join(_PKG_DIR, "libgsdhip.so")
 
 vp, i32, i64, u64, f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_uint64, ctypes.c_float
 

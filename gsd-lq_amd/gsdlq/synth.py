@@ -159,17 +159,21 @@ class SynthSource:
         self._cache = None
 
 
-def write_gsd2(spec: SynthSpec, path: str) -> dict:
-    """Pack every tensor and write a .gsd2 file; returns {name: nk}."""
+def write_gsd2(spec: SynthSpec, path: str, code_bits: int = 8) -> dict:
+    """Pack every tensor and write a .gsd2 file; returns {name: nk}.
+    code_bits = 7 writes the codes of radius <= 6 tensors as 7-bit streams."""
     shapes = tensor_shapes(spec)
     config = make_config(spec)
     packed = {}
     total_bits = 0
     total_w = 0
+    bits_of = lambda f: code_bits if f["radius"] <= 6 else 8
     for name in shapes:
         f = pack_synth(spec, name)
         packed[name] = f
         total_bits += 8 * pack.packed_nbytes(f)
+        if bits_of(f) == 7:   # the code stream is 7/8 of the u8 codes
+            total_bits -= 8 * (f["codes"].size - (7 * f["codes"].size + 7) // 8)
         total_w += f["rows"] * f["cols"]
     w = gsd2.Gsd2Writer(config, total_bits / total_w)
     emb = pack.synth_f16(spec.seed, 1, spec.vocab * spec.hidden, spec.sigma).view(np.float16)
@@ -181,9 +185,9 @@ def write_gsd2(spec: SynthSpec, path: str) -> dict:
         for t in gsd2.LAYER_HEX:
             name = f"blk.{l}.{t}.weight"
             f = packed[name]
-            w.add_hex(name, f["radius"], f["rows"], f["cols"], f["k_dim"], fields=f)
+            w.add_hex(name, f["radius"], f["rows"], f["cols"], f["k_dim"], fields=f, code_bits=bits_of(f))
     w.add_dense("output_norm.weight", ones)
     f = packed["output.weight"]
-    w.add_hex("output.weight", f["radius"], f["rows"], f["cols"], f["k_dim"], fields=f)
+    w.add_hex("output.weight", f["radius"], f["rows"], f["cols"], f["k_dim"], fields=f, code_bits=bits_of(f))
     w.write(path)
     return {n: f["nk"] for n, f in packed.items()}

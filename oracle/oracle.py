@@ -156,7 +156,14 @@ class FileSource:
     def hex_field(self, name, field):
         dt = {"codes": np.uint8, "scales": np.uint16, "row_ptr": np.uint32, "kink_cols": np.uint16,
               "kink_deltas": np.float32, "U": np.uint16, "S": np.float32, "Vt": np.uint16}[field]
-        return self._blob(self.tensors[name][field], dt)
+        meta = self.tensors[name]
+        if field == "codes" and meta.get("code_bits", 8) == 7:
+            # 7-bit stream (this build's extension of the format): code i at
+            # bits 7i .. 7i+6, little-endian; decoded bit by bit
+            n = meta["rows"] * meta["cols"] // 2
+            bits = np.unpackbits(self._blob(meta["codes"], np.uint8), bitorder="little")[:7 * n]
+            return (bits.reshape(n, 7).astype(np.uint16) << np.arange(7, dtype=np.uint16)).sum(1).astype(np.uint8)
+        return self._blob(meta[field], dt)
 
 
 class OracleModel:

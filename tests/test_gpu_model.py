@@ -353,3 +353,22 @@ def test_gsd2_file_through_drop_in(tmp_path, monkeypatch, capsys):
     assert out.count("[GPU Stats: Prefill") == 2
     text = log.read_text(encoding="utf-8")
     assert "### Turn 1" in text and "### Turn 2" in text
+
+
+def test_gsd2_7bit_file_same_results(tmp_path):
+    """The compact Precision file (7-bit code streams) loads into the same
+    device tiles as the u8 file: identical logits, bit for bit."""
+    from gsdlq import synth
+    import run_gpu_native_chat as chat
+    spec = _spec(mode="precision", kinks_per_row=1, n_layers=2)
+    p8, p7 = str(tmp_path / "m8.gsd2"), str(tmp_path / "m7.gsd2")
+    synth.write_gsd2(spec, p8)
+    synth.write_gsd2(spec, p7, code_bits=7)
+    banner("7-bit .gsd2 vs u8 .gsd2")
+    a = chat.GPUMistralV2Model(p8, verbose=False)
+    b = chat.GPUMistralV2Model(p7, verbose=False)
+    assert b.avg_bpw < a.avg_bpw - 0.4
+    for pos, t in enumerate([1, 50, 7, 299, 3]):
+        assert np.array_equal(a.forward_token(t, pos), b.forward_token(t, pos)), pos
+    a.close()
+    b.close()
