@@ -209,16 +209,14 @@ struct AttnArgs {
     int ntok;
 };
 hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
-// Positions per attention split for a context of n_ctx positions: enough
-// splits to spread long contexts over the chip (n_kv * splits ~ 256 blocks),
-// at least 64 and at most 256 positions each (256 is the kernel's LDS score
-// buffer).
+// Positions per attention split for a context of n_ctx positions: one
+// split up to 256 positions (no hand-over, no merge); beyond, enough splits
+// to spread the context over the chip (n_kv * splits ~ 256 blocks), 64, 128
+// or 256 positions each (256 is the kernels' LDS score buffer).
 inline int attention_chunk(int n_ctx, int n_kv) {
-    int c = (n_ctx * n_kv + 255) / 256;
-    c = (c + 63) / 64 * 64;
-    if (c < 64) c = 64;
-    if (c > 256) c = 256;
-    return c;
+    if (n_ctx <= 256) return 256;
+    const int want = (n_ctx * n_kv + 255) / 256;
+    return want <= 64 ? 64 : (want <= 128 ? 128 : 256);
 }
 // Sets the calling thread's error text (gsdh_last_error) and returns code,
 // or -1 for code 0.

@@ -866,6 +866,324 @@ __global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
     if (back == 0 && tid == 0 && !a.epoch) a.counters[kvh] = ep;   // the next launch's epoch base (stream order)
 }
 
+// ------------------------------------------------------------------------
+// Decode attention for one token, query heads per KV head G <= 4, head dim
+// 64 or 128 (the 7B shape: 32 / 8 heads x 128): the matrix-core kernel.
+// Every dispatch fetches its code cold, so the instructions a block executes
+// once are kept few: the loads are unrolled (one instruction each), the dot
+// products are matrix-core steps, and the per-position weighting of V is a
+// rolled loop over V staged in LDS.
+//
+// grid = (n_kv, max_splits), 8 waves; wave w owns positions
+// t0 + pw w .. t0 + pw w + pw - 1 of the block's chunk (pw = chunk / 8;
+// the chunk a multiple of 64 up to 256).
+// Scores with v_mfma_f32_16x16x32_f16, 16 positions x 32 dims per step:
+//   A[m][k] = query head m's dims, m < G: the fp16 high part of q * 2^e,
+//             a second step the low part (q = hi + lo to 2^-22; e puts the
+//             group's largest |q| near 2^13), rows m >= G zero,
+//   B[k][n] = K[position n][dims] as stored (fp16, exact),
+//   D lane n (n < 16), element m = the score of head m at position n.
+// Softmax in the exp2 domain (scores times log2 e), per wave (max, sum);
+// weights e[p][g] go through the wave's LDS to the lanes that hold V[p]
+// (16 bytes, 8 dims per lane); the waves' (max, sum, o) meet in LDS.
+// With more than one split the blocks hand (max, sum, o) per head over as
+// epoch-tagged words; the block of the last split (the fewest positions)
+// waits for them and merges.  Rows
+// past the context are loaded (clamped to the cache) and masked: their
+// score is -inf and their V rows are skipped.
+// ------------------------------------------------------------------------
+constexpr int kAttnDecSplits = 32;   // splits the matrix-core kernel merges (8192 positions at chunk 256)
+
+template <int HD, int G, int PW>
+__global__ void __launch_bounds__(512) attn_dec_kernel(const AttnArgs a) {
+    constexpr int NW = 8;                 // waves; PW positions each (8, 16 or 32)
+    constexpr int NGRP = (PW + 15) / 16;  // groups of 16 positions (matrix-core steps)
+    constexpr int NJ = HD / 32;           // matrix-core steps per 16 positions
+    constexpr int LPR = HD / 8;           // lanes per V row
+    constexpr int RPI = 64 / LPR;         // V rows per load instruction
+    constexpr int NV = PW / RPI;          // V loads per wave
+    constexpr float kLog2e = 1.44269504088896340736f;
+    static_assert(G == 1 || G == 2 || G == 4, "query heads per KV head");
+    static_assert(HD == 64 || HD == 128, "head dim");
+    static_assert(PW == 8 || PW == 16 || PW == 32, "positions per wave");
+    // V staging of wave w (PW rows x HD fp16), reused for its o partials
+    // (4 lane rows x G heads x HD floats: 2048 G bytes at HD 128, 1024 G at
+    // HD 64 after a row fold, both within 64 HD bytes)
+    __shared__ __attribute__((aligned(16))) uint16_t vs[NW][32 * HD];
+    __shared__ __attribute__((aligned(16))) float es[NW][32][4];   // e[p][g] of the wave's positions
+    __shared__ float wm[NW][4], wl[NW][4];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kvh = blockIdx.x, split = blockIdx.y;
+    const int t0 = split * a.chunk;
+    // the position: from the arguments, or read from device memory; a
+    // single-split launch loads its rows before it knows it (they are
+    // masked after), a split launch first learns whether its split exists
+    const bool spec = a.pos_dev == nullptr || a.max_splits == 1;
+    int pos = a.pos;
+    if (!spec) {
+        pos = *a.pos_dev;
+        if (t0 > pos) return;   // (uniform: the whole block leaves)
+    }
+    const size_t rowstride = (size_t)a.n_kv * HD;
+    const size_t lbase = (size_t)a.layer * a.max_seq * rowstride + (size_t)kvh * HD;
+    const uint16_t* kb = a.k_cache + lbase;
+    const uint16_t* vb = a.v_cache + lbase;
+    const int rmax = a.max_seq - 1;
+    const int pw0 = t0 + wid * PW;   // the wave's first position
+
+    // q (A operand source): lane l, head m = l & 15 (m < G), dims
+    // 32 j + 8 (l >> 4) .. + 7; issued first, the K and V rows behind it
+    const int m = lane & 15, kg = lane >> 4;
+    float4 qa[NJ][2];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        qa[j][0] = qa[j][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (m < G) {
+            const float4* qp = reinterpret_cast<const float4*>(a.q + (size_t)(kvh * G + m) * HD + 32 * j + 8 * kg);
+            qa[j][0] = qp[0];
+            qa[j][1] = qp[1];
+        }
+    }
+    // K (B operand): lane l, position pw0 + 16 grp + (l & 15), same dims
+    uint4 kr[NGRP][NJ];
+#pragma unroll
+    for (int grp = 0; grp < NGRP; grp++) {
+        const int t = min(pw0 + 16 * grp + m, rmax);
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+            kr[grp][j] = *reinterpret_cast<const uint4*>(kb + (size_t)t * rowstride + 32 * j + 8 * kg);
+    }
+    // V: lane l, position pw0 + RPI u + l / LPR, dims 8 (l % LPR) .. + 7
+    const int vrow = lane / LPR, vcol = 8 * (lane % LPR);
+    uint4 vr[NV];
+#pragma unroll
+    for (int u = 0; u < NV; u++) {
+        const int t = min(pw0 + RPI * u + vrow, rmax);
+        vr[u] = *reinterpret_cast<const uint4*>(vb + (size_t)t * rowstride + vcol);
+    }
+    if (spec && a.pos_dev) pos = *a.pos_dev;
+    const int n = pos + 1;
+    const int nsplit = (n + a.chunk - 1) / a.chunk;
+    const int t1 = min(n, t0 + a.chunk);   // the block's positions: t0 .. t1 - 1
+    const int te = min(t1, pw0 + PW);      // the wave's: pw0 .. te - 1
+
+    // power-of-two prescale of the group's q: largest |q| into [2^13, 2^14)
+    float mx = 0.f;
+#pragma unroll
+    for (int j = 0; j < NJ; j++)
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(qa[j][h].x), fabsf(qa[j][h].y)), fmaxf(fabsf(qa[j][h].z), fabsf(qa[j][h].w))));
+    mx = wave_max_valu(mx);
+    int ex = 0;
+    if (mx > 0.f && mx < INFINITY) (void)frexpf(mx, &ex);
+    const float up = ldexpf(1.f, 14 - ex);
+    const float scl = ldexpf(1.f, ex - 14) * a.sm_scale * kLog2e;
+    half8v ahi[NJ], alo[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const float f[8] = {qa[j][0].x, qa[j][0].y, qa[j][0].z, qa[j][0].w,
+                            qa[j][1].x, qa[j][1].y, qa[j][1].z, qa[j][1].w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float s = f[e] * up;
+            const _Float16 h = (_Float16)s;
+            ahi[j][e] = h;
+            alo[j][e] = (_Float16)(s - (float)h);
+        }
+    }
+
+    // scores of the wave's 32 positions: lanes 0-15, element g = head g
+    float sv[2][4];
+#pragma unroll
+    for (int g = 0; g < 4; g++) sv[1][g] = -INFINITY;   // (PW <= 16: one group)
+#pragma unroll
+    for (int grp = 0; grp < NGRP; grp++) {
+        float4v d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const half8v b = __builtin_bit_cast(half8v, kr[grp][j]);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[j], b, d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[j], b, d, 0, 0, 0);
+        }
+        const bool ok = pw0 + 16 * grp + m < te;
+#pragma unroll
+        for (int g = 0; g < 4; g++) sv[grp][g] = ok ? d[g] * scl : -INFINITY;
+    }
+    // the wave's max and exp-sum per head (lanes 0-15 of each DPP row; the
+    // other rows compute on values nobody reads)
+    float mw[4], lw[4];
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        mw[g] = row16_max(fmaxf(sv[0][g], sv[1][g]));
+        const float mu = mw[g] == -INFINITY ? 0.f : mw[g];
+        sv[0][g] = __builtin_amdgcn_exp2f(sv[0][g] - mu);
+        sv[1][g] = __builtin_amdgcn_exp2f(sv[1][g] - mu);
+        lw[g] = row16_sum(sv[0][g] + sv[1][g]);
+    }
+    if (lane < 16) {
+#pragma unroll
+        for (int grp = 0; grp < 2; grp++)
+            *reinterpret_cast<float4*>(&es[wid][16 * grp + lane][0]) = make_float4(sv[grp][0], sv[grp][1], sv[grp][2], sv[grp][3]);
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            wm[wid][g] = mw[g];
+            wl[wid][g] = lw[g];
+        }
+    }
+    // V rows into the wave's LDS (each lane reads back its own words)
+    uint4* vw = reinterpret_cast<uint4*>(&vs[wid][0]);
+#pragma unroll
+    for (int u = 0; u < NV; u++) vw[u * 64 + lane] = vr[u];
+
+    float acc[G][8];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[g][e] = 0.f;
+    const int nv_live = (max(te - pw0, 0) + RPI - 1) / RPI;   // loads holding a valid row
+    for (int u = 0; u < nv_live; u++) {
+        const int p = RPI * u + vrow;
+        if (pw0 + p < te) {
+            float vf[8];
+            unpack8(vw[u * 64 + lane], vf);
+            const float4 w4 = *reinterpret_cast<const float4*>(&es[wid][p][0]);
+            const float wg[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+            for (int g = 0; g < G; g++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) acc[g][e] = fmaf(wg[g], vf[e], acc[g][e]);
+        }
+    }
+    // o partials of the wave's lane rows: HD 128: rows l >> 4 (4 rows);
+    // HD 64: rows l >> 3 folded pairwise (row_ror 8) into 4
+    float* ob = reinterpret_cast<float*>(&vs[wid][0]);
+    if constexpr (HD == 64) {
+#pragma unroll
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                acc[g][e] += __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(acc[g][e]), 0x128, 0xF, 0xF, false));
+    }
+    if (HD == 128 || (lane & 15) < 8) {
+        const int r = lane >> 4, c = HD == 128 ? (lane & 15) : (lane & 7);
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float4* op = reinterpret_cast<float4*>(ob + (r * G + g) * HD + 8 * c);
+            op[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+            op[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
+        }
+    }
+    lds_barrier();
+
+    // the block's (max, sum, o) per head: thread (g, d), waves in order
+    const int g = tid / HD, d = tid % HD;
+    const bool own = tid < G * HD;
+    float M = -INFINITY, L = 0.f, O = 0.f;
+    if (own) {
+        for (int w = 0; w < NW; w++) M = fmaxf(M, wm[w][g]);
+        for (int w = 0; w < NW; w++) {
+            const float f = __builtin_amdgcn_exp2f(wm[w][g] - M);   // (-inf: an empty wave, 0)
+            const float* o = reinterpret_cast<const float*>(&vs[w][0]);
+            const float s = (o[(0 * G + g) * HD + d] + o[(1 * G + g) * HD + d]) + (o[(2 * G + g) * HD + d] + o[(3 * G + g) * HD + d]);
+            L = fmaf(f, wl[w][g], L);
+            O = fmaf(f, s, O);
+        }
+    }
+    float* outp = a.out + (size_t)(kvh * G + g) * HD + d;
+    if (nsplit == 1) {
+        if (own) *outp = O / L;
+        return;
+    }
+
+    // hand-over: words [kvh][split][g][2 + HD]; the block of the last split
+    // merges (blocks start in index order, so every other split's block
+    // has started before it and finishes without it)
+    const unsigned ep = a.epoch ? a.epoch : a.counters[kvh] + 1u;
+    const unsigned long long tag = (unsigned long long)ep << 32;
+    constexpr int WPH = 2 + HD;   // words per head
+    unsigned long long* wsk = a.ws + (size_t)kvh * a.max_splits * G * WPH;
+    if (own) {
+        unsigned long long* wsb = wsk + ((size_t)split * G + g) * WPH;
+        __hip_atomic_store(wsb + 2 + d, tag | __float_as_uint(O), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (d == 0) {
+            __hip_atomic_store(wsb, tag | __float_as_uint(M), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(wsb + 1, tag | __float_as_uint(L), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    if (split != nsplit - 1) return;
+    if (tid == 0 && !a.epoch) a.counters[kvh] = ep;   // the next launch's epoch base (stream order)
+
+    // merge: out = sum_s f_s o_s / sum_s f_s l_s with f_s = 2^(m_s - max m),
+    // splits in order.  Thread tid reads word (max, sum) item tid = s G + gi
+    // (tid < nsplit G) and, as thread (g, d), the o words of every split;
+    // the loads bypass the non-coherent caches (sc1) and go out together,
+    // again until every word has this launch's epoch (bounded).  Offsets
+    // past the words read 0 (buffer bounds).
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(wsk, (short)0, nsplit * G * WPH * 8, 0x00020000);
+    const int c = nsplit * G, gi = tid % G;
+    const int vm = tid < c ? tid * WPH * 8 : 0x7FFFFFF0;     // (max, sum) words of item tid
+    const int vo = own ? (g * WPH + 2 + d) * 8 : 0x7FFFFFF0;  // o word of (0, g, d); the split in soffset
+    unsigned long long wm0 = 0, wl0 = 0, ov[kAttnDecSplits];
+    for (int spins = 0;; spins++) {
+        auto w2 = __builtin_amdgcn_raw_buffer_load_b64(rs, vm, 0, 16 /* sc1 */);
+        wm0 = ((unsigned long long)w2[1] << 32) | w2[0];
+        w2 = __builtin_amdgcn_raw_buffer_load_b64(rs, vm, 8, 16);
+        wl0 = ((unsigned long long)w2[1] << 32) | w2[0];
+#pragma unroll
+        for (int kk = 0; kk < kAttnDecSplits; kk++) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, vo, kk * G * WPH * 8, 16);
+            ov[kk] = ((unsigned long long)v[1] << 32) | v[0];
+        }
+        // words past the splits read 0; all are this launch's when exactly
+        // those differ from the epoch
+        int differ = 0;
+#pragma unroll
+        for (int kk = 0; kk < kAttnDecSplits; kk++) differ += (unsigned)(ov[kk] >> 32) != ep;
+        const bool done = (!own || differ == kAttnDecSplits - nsplit) &&
+                          (tid >= c || ((unsigned)(wm0 >> 32) == ep && (unsigned)(wl0 >> 32) == ep));
+        if (done) break;
+        if (spins == (1 << 16)) {
+            if (a.err) *a.err = 1u;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
+    const float m0 = tid < c ? __uint_as_float((unsigned)wm0) : -INFINITY, l0 = __uint_as_float((unsigned)wl0);
+    // max over the splits of head gi: lanes gi, gi + G, ... of each wave,
+    // then the waves (lanes 0..G-1 publish); weights f_s and f_s l_s by item
+    float mg = m0;
+#pragma unroll
+    for (int x = G; x < 64; x <<= 1) mg = fmaxf(mg, __shfl_xor(mg, x, 64));
+    float* red = reinterpret_cast<float*>(&vs[0][0]);                 // [NW][G] wave maxima
+    float2* fw = reinterpret_cast<float2*>(&vs[0][0] + 2 * NW * 4);   // [s][g] (f_s, f_s l_s)
+    if (lane < G) red[wid * G + lane] = mg;
+    lds_barrier();
+    {
+        float Mi = red[gi];
+#pragma unroll
+        for (int w = 1; w < NW; w++) Mi = fmaxf(Mi, red[w * G + gi]);
+        const float f0 = __builtin_amdgcn_exp2f(m0 - Mi);
+        if (tid < kAttnDecSplits * G) fw[tid] = tid < c ? make_float2(f0, f0 * l0) : make_float2(0.f, 0.f);
+    }
+    lds_barrier();
+    if (!own) return;
+    L = 0.f;
+    O = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < kAttnDecSplits; kk++) {
+        const float2 f = fw[kk * G + g];
+        L += f.y;
+        O = fmaf(f.x, __uint_as_float((unsigned)ov[kk]), O);
+    }
+    *outp = O / L;
+}
+
 __global__ void embed_kernel(const uint16_t* embed, const int* token, float* x, int hidden,
                              unsigned long long* clear, int nclear) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -2275,8 +2593,28 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
         return hipErrorInvalidValue;
     const int nt = a.ntok > 1 ? a.ntok : 1;
     if (nt > 1 && (!a.epoch || a.pos_dev)) return hipErrorInvalidValue;
-    const dim3 grid(a.n_kv, a.max_splits, nt);
     const int G = a.n_heads / a.n_kv;
+    // one token, G <= 4, head dim 64 / 128: the matrix-core kernel
+    if (nt == 1 && (G == 1 || G == 2 || G == 4) && (a.hd == 64 || a.hd == 128) &&
+        (a.chunk == 64 || a.chunk == 128 || a.chunk == 256) && a.max_splits <= kAttnDecSplits) {
+        const dim3 grid(a.n_kv, a.max_splits);
+#define GSD_ATTN_P(HD, GG)                                                                            \
+    switch (a.chunk) {                                                                                \
+        case 64: hipLaunchKernelGGL((attn_dec_kernel<HD, GG, 8>), grid, dim3(512), 0, st, a); break;   \
+        case 128: hipLaunchKernelGGL((attn_dec_kernel<HD, GG, 16>), grid, dim3(512), 0, st, a); break; \
+        default: hipLaunchKernelGGL((attn_dec_kernel<HD, GG, 32>), grid, dim3(512), 0, st, a); break;  \
+    }
+#define GSD_ATTN_D(HD, GG) GSD_ATTN_P(HD, GG)
+        if (a.hd == 64) {
+            if (G == 1) GSD_ATTN_D(64, 1) else if (G == 2) GSD_ATTN_D(64, 2) else GSD_ATTN_D(64, 4)
+        } else {
+            if (G == 1) GSD_ATTN_D(128, 1) else if (G == 2) GSD_ATTN_D(128, 2) else GSD_ATTN_D(128, 4)
+        }
+#undef GSD_ATTN_D
+#undef GSD_ATTN_P
+        return hipGetLastError();
+    }
+    const dim3 grid(a.n_kv, a.max_splits, nt);
     // 16 waves for up to 4 query heads per KV head (8 would not fit the
     // registers of 16), else 4
 #define GSD_ATTN_L(HD, GG) \

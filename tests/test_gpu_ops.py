@@ -185,6 +185,31 @@ def _attention_case(lib, ctx, nh, nkv, hd, seed, ms=None):
     assert rel_l2(got, want) < TOL, (ctx, nh, nkv, hd)
 
 
+@pytest.mark.parametrize("ctx,nkv,hd", [(1, 8, 128), (100, 8, 128), (255, 8, 128), (256, 8, 128), (700, 8, 128),
+                                         (60, 8, 64)])
+def test_attention_ignores_cache_rows_past_context(lib, ctx, nkv, hd):
+    """Rows past the context hold NaN (the cache's unwritten slots may hold
+    anything): the kernel loads whole chunks and masks, so no NaN may reach
+    the output, which must equal the oracle's on the valid rows."""
+    banner(f"attention ctx {ctx} with NaN rows past the context")
+    from gsdlq import pack
+    nh, ms = 4 * nkv, ctx + 300
+    kc = pack.synth_f16(71, ctx, ms * nkv * hd, 1.0).reshape(ms, nkv * hd)
+    vc = pack.synth_f16(72, ctx, ms * nkv * hd, 1.0).reshape(ms, nkv * hd)
+    q = np.random.default_rng(ctx).standard_normal(nh * hd).astype(np.float32)
+    want = np.zeros(nh * hd, np.float32)
+    O.load("port").gsd_cpu_gqa_attention(O.P(q), O.P(kc), O.P(vc), O.P(want), 0, ctx - 1, nh, nkv, hd, ms,
+                                         1.0 / float(np.sqrt(hd)))
+    kc, vc = kc.copy(), vc.copy()
+    kc[ctx:] = 0x7E00   # fp16 NaN
+    vc[ctx:] = 0x7E00
+    out, dk, dv, dq = E(nh * hd * 4), D(kc), D(vc), D(q)
+    lib.gsdh_gqa_attention(None, p(dq), p(dk), p(dv), p(out), 0, ctx - 1, nh, nkv, hd, ms, 1.0 / float(np.sqrt(hd)))
+    got = H(out, np.float32, nh * hd)
+    assert np.isfinite(got).all()
+    assert rel_l2(got, want) < TOL
+
+
 def test_attention_shape_changes_between_calls(lib):
     """One call per shape, in an order whose split-word regions overlap: 8 KV
     heads, then 2 KV heads of 256 dims, then 8 KV heads again (a word left by
