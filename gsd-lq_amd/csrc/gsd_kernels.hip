@@ -1352,20 +1352,26 @@ __device__ __forceinline__ void mv4_publish(const HexArgs& a, int lead, float* s
 // LR: rank-k terms.  0: none (the rank-k machinery is not compiled in: the
 // epilogue code is inlined once per pipeline step of the main loop, and a
 // smaller kernel runs faster); 1: ranks <= 2, projections computed by every
-// block from its own staging of x (kLrSlots); 2: any rank, projections
-// published by leading blocks.  EPI: the epilogue (HexEpilogue), or -1 to
-// read it from the arguments.
+// block from its own staging of x (kLrSlots); 3: as 1 when every segment
+// has rank exactly 2 and no tmp_k (every Precision tensor; fewer
+// instructions per launch); 2: any rank, projections published by leading
+// blocks.  EPI: the epilogue (HexEpilogue), or -1 to read it from the
+// arguments.
 template <int TB, int LR, int EPI>
 __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) hexmv4_kernel(const HexArgs a) {
     __shared__ __attribute__((aligned(16))) uint32_t stab[TB > 0 ? TB * 64 : 1];
     __shared__ float red[2][kMv4MaxWaves][16];
     __shared__ float tkl[kMaxSeg][kMaxRank];
-    // LR == 1: each wave's partial rank-k dot products over its own columns
+    // LR 1 and 3 form the projections in the block; LR 3: every segment has
+    // rank exactly 2 and no tmp_k (each Precision tensor), so the slot masks
+    // and the rank-1 and tmp_k paths are not compiled in
+    constexpr bool kIn = LR == 1 || LR == 3, kR2 = LR == 3;
+    // LR 1 / 3: each wave's partial rank-k dot products over its own columns
     // (times S[j]), slot r = j (paired launch: the wave's group's segment) or
     // 2 g + j, wave index last
-    constexpr int kVS = LR != 1 ? 1 : (EPI == kEpiResidual || EPI == kEpiSwiGLU ? 2 : 2 * kMaxSeg);
-    static_assert(LR != 1 || kVS == 2 || kVS == 2 * kMaxSeg, "rank-k slot counts");
-    __shared__ float vtp[kVS][LR == 1 ? kMv4MaxWaves : 1];
+    constexpr int kVS = !kIn ? 1 : (EPI == kEpiResidual || EPI == kEpiSwiGLU ? 2 : 2 * kMaxSeg);
+    static_assert(!kIn || kVS == 2 || kVS == 2 * kMaxSeg, "rank-k slot counts");
+    __shared__ float vtp[kVS][kIn ? kMv4MaxWaves : 1];
     __shared__ float scratch[32];
     __shared__ float ssq[kMv4MaxWaves];   // sum of x^2 over each wave's columns
     // epilogue inputs of the block's units (written and read by the epilogue
@@ -1373,7 +1379,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     __shared__ float lpre[EPI == kEpiResidual || EPI < 0 ? kMv4PreUnits : 1][16];
     __shared__ float2 lcs[EPI == kEpiRopeKV || EPI < 0 ? kMv4PreUnits : 1][16];
     __shared__ uint32_t lup[LR > 0 ? kMv4PreUnits : 1][2][16];
-    __shared__ float lsk[2 * kMaxSeg];   // LR == 1: S[j] of segment g at 2 g + j
+    __shared__ float lsk[2 * kMaxSeg];   // LR 1 / 3: S[j] of segment g at 2 g + j
     extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
 
     // wid in a scalar register: the segment selections below (seg_of) then
@@ -1503,15 +1509,18 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     const uint4* Xw = reinterpret_cast<const uint4*>(X32);
     // chunks of x per batch of loads (4 when the rank-k rows of three
     // segments come with them: 24 more registers instead of 48)
-    constexpr int kXP = LR == 1 && kVS > 2 ? 4 : 8;
+    constexpr int kXP = kIn && kVS > 2 ? 4 : 8;
     float2 xv[kXP], wv[kXP];
-    // LR == 1: the rank-k rows Vt[j] of the wave's columns come with x (slot
+    // LR 1 / 3: the rank-k rows Vt[j] of the wave's columns come with x (slot
     // r of vmask: segment paired ? grp : r / 2, row paired ? r : r % 2), and
     // dk[r] sums x'[c] * Vt[j][c] over them (x' without the RMSNorm factor)
     auto slot_seg = [&](int r) { return paired ? grp : r >> 1; };
     auto slot_row = [&](int r) { return paired ? r : r & 1; };
     unsigned vmask = 0, emask = 0;   // emask: bit 2 g + j, segment g row j, for the epilogue
-    if constexpr (LR == 1) {
+    if constexpr (kR2) {
+        emask = (1u << (2 * a.nseg)) - 1u;
+        vmask = paired ? 3u : emask & ((1u << kVS) - 1u);
+    } else if constexpr (kIn) {
         // (no short-circuit: seg[0..2] are all in the arguments, and one
         // branch per test would wait for each scalar read in turn)
 #pragma unroll
@@ -1524,9 +1533,12 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     // are unconditional and go out back to back
     const uint16_t* vrow[kVS];
 #pragma unroll
-    for (int r = 0; r < kVS; r++)
-        vrow[r] = ((vmask >> r) & 1u) ? kseg[slot_seg(r)].Vt + (size_t)slot_row(r) * cols0
-                                      : reinterpret_cast<const uint16_t*>(a.x);
+    for (int r = 0; r < kVS; r++) {
+        // (LR 3 with a fixed segment count: every slot is used)
+        constexpr bool kAll = kR2 && EPI >= 0 && EPI != kEpiStore;
+        vrow[r] = kAll || ((vmask >> r) & 1u) ? kseg[slot_seg(r)].Vt + (size_t)slot_row(r) * cols0
+                                              : reinterpret_cast<const uint16_t*>(a.x);
+    }
     uint32_t vt[kVS][kXP];
     float dk[kVS];
 #pragma unroll
@@ -1542,7 +1554,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
             if (p < P && col < a.cols) {
                 xv[i] = *reinterpret_cast<const float2*>(a.x + col);
                 if (a.norm_w) wv[i] = *reinterpret_cast<const float2*>(a.norm_w + col);
-                if constexpr (LR == 1) {
+                if constexpr (kIn) {
 #pragma unroll
                     for (int r = 0; r < kVS; r++) vt[r][i] = *reinterpret_cast<const uint32_t*>(vrow[r] + col);
                 }
@@ -1563,7 +1575,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                 ss = fmaf(xv[i].x, xv[i].x, ss);
                 ss = fmaf(xv[i].y, xv[i].y, ss);
                 const float xa = xv[i].x * wv[i].x, xb = xv[i].y * wv[i].y;
-                if constexpr (LR == 1) {
+                if constexpr (kIn) {
                     // every slot, used or not: a loaded word no path consumes
                     // stays pending, and a later reuse of its register then
                     // waits for every load in flight (in the main loop's
@@ -1608,8 +1620,8 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
         ecs[k] = make_float2(1.f, 0.f);
         eup[k][0] = eup[k][1] = 0u;
     }
-    float esk = 0.f;   // LR == 1: lane 2 g + j of wave 0 holds S[j] of segment g
-    if (LR == 1 && wid == 0 && lane < 2 * kMaxSeg && ((emask >> lane) & 1u)) {
+    float esk = 0.f;   // LR 1 / 3: lane 2 g + j of wave 0 holds S[j] of segment g
+    if (kIn && wid == 0 && lane < 2 * kMaxSeg && ((emask >> lane) & 1u)) {
         const float* sp = lane < 2 ? kseg[0].S : (lane < 4 ? kseg[1].S : kseg[2].S);
         esk = sp[lane & 1];
     }
@@ -1627,7 +1639,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
             for (int gi = 0; gi < 2; gi++) {
                 if (LR == 0 || gi >= G) break;
                 KSeg& sp = kseg[paired ? gi : g];
-                const int kk = sp.k, r = min(prow, sp.rows - 1);
+                const int kk = kR2 ? 2 : sp.k, r = min(prow, sp.rows - 1);
                 const uint32_t* up = kk == 2   ? reinterpret_cast<const uint32_t*>(sp.U) + r
                                      : kk == 1 ? reinterpret_cast<const uint32_t*>(sp.U + (r & ~1))
                                                : reinterpret_cast<const uint32_t*>(a.x);
@@ -1672,7 +1684,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     }
     unsigned have = 0;   // epilogue lanes: rank-k values of segment g fetched
     using KF32 = const __attribute__((address_space(4))) float;
-    for (int g = 0; g < (LR ? a.nseg : 0); g++) {
+    for (int g = 0; g < (LR == 1 || LR == 2 ? a.nseg : 0); g++) {
         if (kseg[g].k > 0 && kseg[g].tmp_k) {
             for (int j = 0; j < kseg[g].k; j++) {   // uniform index: scalar loads
                 const float v = ((KF32*)kseg[g].tmp_k)[j];
@@ -1686,7 +1698,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
 
     xfirst(0);
     if (wid == 0 && lane < 16) {   // x has landed, and with it the epilogue inputs
-        if (LR == 1 && lane < 2 * kMaxSeg) lsk[lane] = esk;
+        if (kIn && lane < 2 * kMaxSeg) lsk[lane] = esk;
 #pragma unroll
         for (int k = 0; k < kMv4PreUnits; k++) {
             if constexpr (kHasPre) lpre[k][lane] = epre[k];
@@ -1706,7 +1718,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     ss = wave_sum_valu(ss);
     mx = wave_max_valu(mx);
     if (lane == 0) ssq[wid] = ss;
-    if constexpr (LR == 1) {
+    if constexpr (kIn) {
         // the slots' partial sums reduced together: the 32-lane swaps pair
         // slots, the 16-lane swaps put one slot in each 16-lane row, and one
         // DPP row sum finishes them (unused slots hold values nobody reads)
@@ -1788,7 +1800,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                 for (int w = 0; w < WR; w++) sx += ssq[w];
                 inv = 1.0f / sqrtf(sx / (float)a.cols + a.eps);
             }
-            if constexpr (LR == 1) {
+            if constexpr (kIn) {
                 // first unit end: rank-k values of the segments without tmp_k,
                 // S[j] * inv * (sum of the partials of the waves covering x)
                 // (gsd_lq_cpu_engine.c:110-127); lane l reads wave l's partial
@@ -1821,7 +1833,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                         const uint32_t e = sg.row_ptr[row + 1];
                         for (uint32_t i = sg.row_ptr[row]; i < e; i++) t += sg.kdel[i] * xnorm(a, sg.kcols[i], inv);
                     }
-                    if (LR > 0 && sg.k > 0) {
+                    if (LR > 0 && (kR2 || sg.k > 0)) {
                         if (LR == 2 && !((have >> sg_i) & 1u)) {
                             // bounded wait for the published rank-k words of
                             // this segment (normally already there)
@@ -1841,14 +1853,14 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                             }
                             have |= 1u << sg_i;
                         }
-                        if (LR == 1 || sg.k <= 2) {   // prefetched factors, same order as below
+                        if (kIn || sg.k <= 2) {   // prefetched factors, same order as below
                             // (the asm keeps the use, and the wait for the
                             // load, inside this branch: hoisted, it would wait
                             // for the code loads in flight in every launch)
                             uint32_t uw = lup[uk][gi][lane];
-                            if (sg.k == 1) uw >>= 16 * (row & 1);   // U[row] of the aligned pair
+                            if (!kR2 && sg.k == 1) uw >>= 16 * (row & 1);   // U[row] of the aligned pair
                             t += h2f((uint16_t)(uw & 0xFFFFu)) * tkl[sg_i][0];
-                            if (sg.k == 2) t += h2f((uint16_t)(uw >> 16)) * tkl[sg_i][1];
+                            if (kR2 || sg.k == 2) t += h2f((uint16_t)(uw >> 16)) * tkl[sg_i][1];
                         } else {
                             const uint16_t* up_ = sg.U + (size_t)row * sg.k;
                             for (int jj = 0; jj < sg.k; jj++) t += h2f(up_[jj]) * tkl[sg_i][jj];
@@ -2352,7 +2364,7 @@ hipError_t launch_hexmv4(const HexArgs& a, hipStream_t st) {
     const bool paired = a.epilogue == kEpiSwiGLU;
     if (paired && (a.nseg != 2 || a.seg[0].rows != a.seg[1].rows)) return hipErrorInvalidValue;
     if (a.epilogue == kEpiRopeKV && a.nseg != 3) return hipErrorInvalidValue;
-    bool shared = true, lr = false, inblock = a.epilogue != kEpiResidual || a.nseg == 1;
+    bool shared = true, lr = false, inblock = a.epilogue != kEpiResidual || a.nseg == 1, all2 = true;
     int nlead = 0, nunits = 0, tab_bytes = 0;
     for (int g = 0; g < a.nseg; g++) {
         const HexSeg& s = a.seg[g];
@@ -2360,6 +2372,7 @@ hipError_t launch_hexmv4(const HexArgs& a, hipStream_t st) {
         shared = shared && s.fields == a.seg[0].fields && s.n_pts == a.seg[0].n_pts;
         if (s.k > 0 && (!s.U || (!s.tmp_k && (!s.Vt || !s.S)))) return hipErrorInvalidValue;
         lr = lr || s.k > 0;
+        all2 = all2 && s.k == 2 && !s.tmp_k;
         if (!s.tmp_k && s.k > 0) {
             nlead += s.k;
             inblock = inblock && s.k <= 2;
@@ -2405,6 +2418,7 @@ hipError_t launch_hexmv4(const HexArgs& a, hipStream_t st) {
     {                                                                                           \
         const size_t lds = xbytes + (T == 0 ? (size_t)tab_bytes : 0);                           \
         if (!lr) return launch_hexmv4_t<T, 0, E>(ap, st, nw, lds, nunits, 0);                   \
+        if (inblock && all2) return launch_hexmv4_t<T, 3, E>(ap, st, nw, lds, nunits, 0);       \
         if (inblock) return launch_hexmv4_t<T, 1, E>(ap, st, nw, lds, nunits, 0);               \
         return launch_hexmv4_t<T, 2, -1>(ap, st, nw, lds, nunits, nlead);                       \
     }
