@@ -444,10 +444,11 @@ def probe(kind: str, n: int, ctx: int = 8192, m: int = 128):
 
 def bench_attention(ctxs=(512, 2048, 8192), reps=20):
     """Decode attention with K/V append (32 query heads, 8 KV heads, head dim
-    128, RoPE theta 1e6) at contexts 512 / 2048 / 8192: per layer one RoPE +
-    fp16 K/V append at pos = ctx - 1 (gsdh_rope_and_store_kv) and one split
-    attention over the fp16 cache filled to ctx - 1 (gsdh_gqa_attention),
-    the engine's own kernels (gsd_lq_cpu_engine.c:185-330 computes the same).
+    128, RoPE theta 1e6) at contexts 512 / 2048 / 8192: per layer one launch
+    (gsdh_rope_store_gqa_attention) that rotates q and the new K row, appends
+    fp16 K/V at pos = ctx - 1 and attends over the cache filled to ctx - 1,
+    the two reference calls in one (gsd_lq_cpu_engine.c:185-330 computes the
+    same).
     Enough layers are rotated that the caches exceed 512 MB (beyond the
     Infinity Cache); the launches of all layers are captured in one graph on
     the stream of a small model context and timed with HIP events there.
@@ -489,12 +490,10 @@ def bench_attention(ctxs=(512, 2048, 8192), reps=20):
 
         def run():
             for l in range(L):
-                lib.gsdh_rope_and_store_kv(sp, at("q", l, n_heads * hd), at("k", l, n_kv * hd), at("v", l, n_kv * hd),
-                                           bufs["kc"], bufs["vc"], l, pos, n_heads, n_kv, hd, ctx,
-                                           ctypes.c_float(theta), 1)
-                lib.gsdh_gqa_attention(sp, at("q", l, n_heads * hd), bufs["kc"], bufs["vc"],
-                                       at("out", l, n_heads * hd), l, pos, n_heads, n_kv, hd, ctx,
-                                       ctypes.c_float(sm_scale))
+                lib.gsdh_rope_store_gqa_attention(sp, at("q", l, n_heads * hd), at("k", l, n_kv * hd),
+                                                  at("v", l, n_kv * hd), bufs["kc"], bufs["vc"],
+                                                  at("out", l, n_heads * hd), l, pos, n_heads, n_kv, hd, ctx,
+                                                  ctypes.c_float(theta), 1, ctypes.c_float(sm_scale))
 
         run()                                    # sizes the attention workspace outside the capture
         lib.gsdh_stream_sync(sp)
@@ -510,7 +509,8 @@ def bench_attention(ctxs=(512, 2048, 8192), reps=20):
                             "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "layers_rotated": L}
     model.close()
     res["workload"] = ("32 q heads / 8 KV heads x 128, fp16 KV cache ~N(0,1) filled to ctx-1, RoPE + append at "
-                       "ctx-1, split attention; graph of all layers, HIP events")
+                       "ctx-1 and attention in one launch per layer (gsdh_rope_store_gqa_attention); graph of all "
+                       "layers, HIP events")
     return res
 
 

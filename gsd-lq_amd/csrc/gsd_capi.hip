@@ -208,22 +208,24 @@ int gsdh_rope_and_store_kv(void* stream, float* q, const float* k, const float* 
     return 0;
 }
 
-int gsdh_gqa_attention(void* stream, const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
-                       float* attn_out, int layer_idx, int pos, int n_heads, int n_kv_heads, int head_dim,
-                       int max_seq_len, float sm_scale) {
+namespace {
+// Checks a one-token attention call and fills a (positions, chunking, the
+// stream's workspace and the next epoch on it); g_attn_mu held.
+int attention_setup(void* stream, AttnArgs& a, const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                    float* attn_out, int layer_idx, int pos, int n_heads, int n_kv_heads, int head_dim,
+                    int max_seq_len, float sm_scale) {
     if (head_dim != 64 && head_dim != 128 && head_dim != 256) return fail(-1, "attention: head_dim %d not in {64,128,256}", head_dim);
     if (n_kv_heads <= 0 || n_heads % n_kv_heads || (8 % (n_heads / n_kv_heads)) != 0)
         return fail(-1, "attention: n_heads %d / n_kv_heads %d is not a group size in {1,2,4,8}", n_heads, n_kv_heads);
     if (pos < 0 || pos >= max_seq_len) return fail(-1, "attention: pos %d outside 0..%d", pos, max_seq_len - 1);
     const int n = pos + 1, G = n_heads / n_kv_heads;
-    AttnArgs a{};
+    a = AttnArgs{};
     a.q = q; a.k_cache = k_cache; a.v_cache = v_cache; a.out = attn_out; a.pos_dev = nullptr; a.pos = pos;
     a.layer = layer_idx; a.n_heads = n_heads; a.n_kv = n_kv_heads; a.hd = head_dim; a.max_seq = max_seq_len;
     a.sm_scale = sm_scale;
     a.chunk = attention_chunk(n, n_kv_heads);
     a.max_splits = (n + a.chunk - 1) / a.chunk;
     const size_t need = attention_ws_bytes(n_kv_heads, a.max_splits, G, head_dim);
-    std::lock_guard<std::mutex> lk(g_attn_mu);
     AttnWs& w = g_attn_ws[S(stream)];
     if (need > w.bytes || w.epoch >= 0xFFFFFFF0u) {
         // a larger workspace (the stream's earlier launches finish first),
@@ -242,6 +244,44 @@ int gsdh_gqa_attention(void* stream, const float* q, const uint16_t* k_cache, co
     a.ws = w.ws;
     a.counters = nullptr;
     a.epoch = ++w.epoch;
+    return 0;
+}
+}  // namespace
+
+int gsdh_gqa_attention(void* stream, const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                       float* attn_out, int layer_idx, int pos, int n_heads, int n_kv_heads, int head_dim,
+                       int max_seq_len, float sm_scale) {
+    std::lock_guard<std::mutex> lk(g_attn_mu);
+    AttnArgs a;
+    const int rc = attention_setup(stream, a, q, k_cache, v_cache, attn_out, layer_idx, pos, n_heads, n_kv_heads,
+                                   head_dim, max_seq_len, sm_scale);
+    if (rc) return rc;
+    HIPCHK(launch_attention(a, S(stream)));
+    return 0;
+}
+
+int gsdh_rope_store_gqa_attention(void* stream, float* q, const float* k, const float* v, uint16_t* k_cache,
+                                  uint16_t* v_cache, float* attn_out, int layer_idx, int pos, int n_heads,
+                                  int n_kv_heads, int head_dim, int max_seq_len, float rope_theta, int interleaved,
+                                  float sm_scale) {
+    if (head_dim <= 0 || head_dim % 2 || head_dim > 256) return fail(-1, "rope: head_dim %d", head_dim);
+    std::lock_guard<std::mutex> lk(g_attn_mu);
+    AttnArgs a;
+    const int rc = attention_setup(stream, a, q, k_cache, v_cache, attn_out, layer_idx, pos, n_heads, n_kv_heads,
+                                   head_dim, max_seq_len, sm_scale);
+    if (rc) return rc;
+    std::vector<float> cs(head_dim);
+    rope_cs(rope_theta, head_dim, pos, cs.data());
+    const float2* cs2 = reinterpret_cast<const float2*>(cs.data());
+    const hipError_t e = launch_rope_attention(a, k, v, interleaved, cs2, S(stream));
+    if (e == hipSuccess) return 0;
+    if (e != hipErrorNotSupported) return fail((int)e, "rope + attention: %s", hipGetErrorString(e));
+    // shapes outside the fused kernel: the two launches
+    RopeKV r{};
+    r.cs = nullptr; r.pos_dev = nullptr; r.pos = pos; r.k_cache = k_cache; r.v_cache = v_cache;
+    r.layer = layer_idx; r.n_heads = n_heads; r.n_kv = n_kv_heads; r.hd = head_dim; r.max_seq = max_seq_len;
+    r.interleaved = interleaved;
+    HIPCHK(launch_rope_kv(q, k, v, r, cs2, S(stream)));
     HIPCHK(launch_attention(a, S(stream)));
     return 0;
 }

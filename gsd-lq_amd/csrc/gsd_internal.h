@@ -209,6 +209,13 @@ struct AttnArgs {
     int ntok;
 };
 hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
+// RoPE + K/V append at a.pos fused into the one-token attention launch
+// (host position; k, v: the new rows before RoPE; cs: (cos, sin) of pos,
+// hd / 2 pairs): q is rotated in place, the cache rows written, out as
+// launch_attention.  hipErrorNotSupported for shapes the fused kernel does
+// not cover (then run launch_rope_kv and launch_attention).
+hipError_t launch_rope_attention(const AttnArgs& a, const float* k, const float* v, int interleaved,
+                                 const float2* cs, hipStream_t stream);
 // Positions per attention split for a context of n_ctx positions: one
 // split up to 256 positions (no hand-over, no merge); beyond, enough splits
 // to spread the context over the chip (n_kv * splits ~ 256 blocks), 64, 128

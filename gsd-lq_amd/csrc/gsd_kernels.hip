@@ -894,8 +894,17 @@ __global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
 // ------------------------------------------------------------------------
 constexpr int kAttnDecSplits = 32;   // splits the matrix-core kernel merges (8192 positions at chunk 256)
 
-template <int HD, int G, int PW>
-__global__ void __launch_bounds__(512) attn_dec_kernel(const AttnArgs a) {
+// RoPE + append fused in front (one token, host position): the new K and V
+// rows (fp32, before RoPE), the pairing and the position's (cos, sin)
+struct AttnRope {
+    const float* k;
+    const float* v;
+    int interleaved;
+    float2 cs[64];   // head dim <= 128
+};
+
+template <int HD, int G, int PW, bool ROPE>
+__device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope* rp) {
     constexpr int NW = 8;                 // waves; PW positions each (8, 16 or 32)
     constexpr int NGRP = (PW + 15) / 16;  // groups of 16 positions (matrix-core steps)
     constexpr int NJ = HD / 32;           // matrix-core steps per 16 positions
@@ -912,6 +921,9 @@ __global__ void __launch_bounds__(512) attn_dec_kernel(const AttnArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t vs[NW][32 * HD];
     __shared__ __attribute__((aligned(16))) float es[NW][32][4];   // e[p][g] of the wave's positions
     __shared__ float wm[NW][4], wl[NW][4];
+    // ROPE: each wave's copy of (cos, sin) of pos and of the new K and V rows
+    __shared__ __attribute__((aligned(16))) float2 rcs[ROPE ? NW : 1][ROPE ? HD / 2 : 1];
+    __shared__ __attribute__((aligned(16))) float rkv[ROPE ? NW : 1][ROPE ? 2 * HD : 1];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -936,6 +948,17 @@ __global__ void __launch_bounds__(512) attn_dec_kernel(const AttnArgs a) {
     // q (A operand source): lane l, head m = l & 15 (m < G), dims
     // 32 j + 8 (l >> 4) .. + 7; issued first, the K and V rows behind it
     const int m = lane & 15, kg = lane >> 4;
+    // ROPE: (cos, sin) pairs and the new rows, one 8-byte load per lane and
+    // table, first of all (into this wave's LDS once they land)
+    float2 rin[3];
+    if constexpr (ROPE) {
+#pragma unroll
+        for (int t = 0; t < 3; t++) {
+            const int i = lane < HD / 2 ? lane : 0;
+            rin[t] = t == 0 ? rp->cs[i]
+                            : reinterpret_cast<const float2*>((t == 1 ? rp->k : rp->v) + (size_t)kvh * HD)[i];
+        }
+    }
     float4 qa[NJ][2];
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
@@ -968,6 +991,109 @@ __global__ void __launch_bounds__(512) attn_dec_kernel(const AttnArgs a) {
     const int nsplit = (n + a.chunk - 1) / a.chunk;
     const int t1 = min(n, t0 + a.chunk);   // the block's positions: t0 .. t1 - 1
     const int te = min(t1, pw0 + PW);      // the wave's: pw0 .. te - 1
+
+    // ROPE: the rotated q rows of the group, written back in place (wave 0)
+    // once every block of the KV head has read q: by the only block, or by
+    // the merging block after every split's words have arrived
+    float4 qkeep[ROPE ? NJ : 1][2];
+    auto write_q = [&]() {
+        if (ROPE && wid == 0 && m < G) {
+#pragma unroll
+            for (int j = 0; j < (ROPE ? NJ : 1); j++) {
+                float4* qp = reinterpret_cast<float4*>(const_cast<float*>(a.q) + (size_t)(kvh * G + m) * HD + 32 * j + 8 * kg);
+                qp[0] = qkeep[j][0];
+                qp[1] = qkeep[j][1];
+            }
+        }
+    };
+    if constexpr (ROPE) {
+        // RoPE (gsd_lq_cpu_engine.c:213-256) in registers, evaluated without
+        // contraction like the reference: q's rows of the group (every block
+        // of the KV head rotates its own copy),
+        // and the new K row, which the lanes holding position pos put in
+        // place of the row they loaded and store to the cache with V's row.
+        // A lane's dims pair with dims in its own registers: interleaved,
+        // elements 2i and 2i + 1 of a step; rotate-half, element e of steps
+        // j and j + NJ / 2.
+#pragma clang fp contract(off)
+        // every element from the original values, the pairing by selects
+        // (no array indexed at run time): interleaved, partner e ^ 1 of
+        // step j, first of the pair when e is even; rotate-half, element e
+        // of step j ^ NJ / 2, first when j < NJ / 2
+        const bool il = rp->interleaved != 0;
+        if (lane < HD / 2) {
+            rcs[wid][lane] = rin[0];
+            reinterpret_cast<float2*>(&rkv[wid][0])[lane] = rin[1];
+            reinterpret_cast<float2*>(&rkv[wid][HD])[lane] = rin[2];
+        }
+        auto rope8 = [&](float (&f)[NJ][8]) {
+            float o[NJ][8];
+#pragma unroll
+            for (int j = 0; j < NJ; j++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float x = f[j][e];
+                    const float pr = il ? f[j][e ^ 1] : f[j ^ (NJ / 2)][e];
+                    const bool first = il ? (e & 1) == 0 : j < NJ / 2;
+                    const int ci = il ? (32 * j + 8 * kg + e) >> 1 : 32 * (j % (NJ / 2)) + 8 * kg + e;
+                    const float2 cs = rcs[wid][ci];
+                    o[j][e] = first ? x * cs.x - pr * cs.y : pr * cs.y + x * cs.x;
+                }
+#pragma unroll
+            for (int j = 0; j < NJ; j++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) f[j][e] = o[j][e];
+        };
+        {
+            float f[NJ][8];
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                f[j][0] = qa[j][0].x; f[j][1] = qa[j][0].y; f[j][2] = qa[j][0].z; f[j][3] = qa[j][0].w;
+                f[j][4] = qa[j][1].x; f[j][5] = qa[j][1].y; f[j][6] = qa[j][1].z; f[j][7] = qa[j][1].w;
+            }
+            rope8(f);
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                qa[j][0] = qkeep[j][0] = make_float4(f[j][0], f[j][1], f[j][2], f[j][3]);
+                qa[j][1] = qkeep[j][1] = make_float4(f[j][4], f[j][5], f[j][6], f[j][7]);
+            }
+        }
+        uint16_t* kc = const_cast<uint16_t*>(a.k_cache) + lbase + (size_t)pos * rowstride;
+        uint16_t* vc = const_cast<uint16_t*>(a.v_cache) + lbase + (size_t)pos * rowstride;
+        auto pack8 = [](const float (&f)[8]) {
+            return make_uint4((uint32_t)f2h(f[0]) | ((uint32_t)f2h(f[1]) << 16), (uint32_t)f2h(f[2]) | ((uint32_t)f2h(f[3]) << 16),
+                              (uint32_t)f2h(f[4]) | ((uint32_t)f2h(f[5]) << 16), (uint32_t)f2h(f[6]) | ((uint32_t)f2h(f[7]) << 16));
+        };
+#pragma unroll
+        for (int grp = 0; grp < NGRP; grp++) {
+            if (pw0 + 16 * grp + m == pos) {
+                float f[NJ][8];
+#pragma unroll
+                for (int j = 0; j < NJ; j++) {
+                    const float4* kp = reinterpret_cast<const float4*>(&rkv[wid][32 * j + 8 * kg]);
+                    const float4 k0 = kp[0], k1 = kp[1];
+                    f[j][0] = k0.x; f[j][1] = k0.y; f[j][2] = k0.z; f[j][3] = k0.w;
+                    f[j][4] = k1.x; f[j][5] = k1.y; f[j][6] = k1.z; f[j][7] = k1.w;
+                }
+                rope8(f);
+#pragma unroll
+                for (int j = 0; j < NJ; j++) {
+                    kr[grp][j] = pack8(f[j]);
+                    *reinterpret_cast<uint4*>(kc + 32 * j + 8 * kg) = kr[grp][j];
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < NV; u++) {
+            if (pw0 + RPI * u + vrow == pos) {
+                const float4* vp = reinterpret_cast<const float4*>(&rkv[wid][HD + vcol]);
+                const float4 v0 = vp[0], v1 = vp[1];
+                const float f[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+                vr[u] = pack8(f);
+                *reinterpret_cast<uint4*>(vc + vcol) = vr[u];
+            }
+        }
+    }
 
     // power-of-two prescale of the group's q: largest |q| into [2^13, 2^14)
     float mx = 0.f;
@@ -1097,6 +1223,7 @@ __global__ void __launch_bounds__(512) attn_dec_kernel(const AttnArgs a) {
     float* outp = a.out + (size_t)(kvh * G + g) * HD + d;
     if (nsplit == 1) {
         if (own) *outp = O / L;
+        write_q();
         return;
     }
 
@@ -1182,6 +1309,16 @@ __global__ void __launch_bounds__(512) attn_dec_kernel(const AttnArgs a) {
         O = fmaf(f.x, __uint_as_float((unsigned)ov[kk]), O);
     }
     *outp = O / L;
+    write_q();
+}
+
+template <int HD, int G, int PW>
+__global__ void __launch_bounds__(512) attn_dec_kernel(const AttnArgs a) {
+    attn_dec_body<HD, G, PW, false>(a, nullptr);
+}
+template <int HD, int G, int PW>
+__global__ void __launch_bounds__(512) attn_rope_kernel(const AttnArgs a, const AttnRope r) {
+    attn_dec_body<HD, G, PW, true>(a, &r);
 }
 
 __global__ void embed_kernel(const uint16_t* embed, const int* token, float* x, int hidden,
@@ -2596,6 +2733,33 @@ hipError_t launch_rope_kv(float* q, const float* k, const float* v, const RopeKV
     int n = r.n_heads * half;
     if (r.n_kv * r.hd > n) n = r.n_kv * r.hd;
     hipLaunchKernelGGL(rope_kv_kernel, dim3((n + 255) / 256), dim3(256), 0, st, q, k, v, r, csi, cs_inline ? 1 : 0);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_attention(const AttnArgs& a, const float* k, const float* v, int interleaved,
+                                 const float2* cs, hipStream_t st) {
+    const int G = a.n_kv > 0 ? a.n_heads / a.n_kv : 0;
+    if (a.pos_dev || a.ntok > 1 || !a.ws || !a.epoch || !(G == 1 || G == 2 || G == 4) || !(a.hd == 64 || a.hd == 128) ||
+        !(a.chunk == 64 || a.chunk == 128 || a.chunk == 256) || a.max_splits > kAttnDecSplits)
+        return hipErrorNotSupported;
+    AttnRope r{};
+    r.k = k;
+    r.v = v;
+    r.interleaved = interleaved;
+    for (int i = 0; i < a.hd / 2; i++) r.cs[i] = cs[i];
+    const dim3 grid(a.n_kv, a.max_splits);
+#define GSD_ATTN_R(HD, GG)                                                                                  \
+    switch (a.chunk) {                                                                                      \
+        case 64: hipLaunchKernelGGL((attn_rope_kernel<HD, GG, 8>), grid, dim3(512), 0, st, a, r); break;   \
+        case 128: hipLaunchKernelGGL((attn_rope_kernel<HD, GG, 16>), grid, dim3(512), 0, st, a, r); break; \
+        default: hipLaunchKernelGGL((attn_rope_kernel<HD, GG, 32>), grid, dim3(512), 0, st, a, r); break;  \
+    }
+    if (a.hd == 64) {
+        if (G == 1) GSD_ATTN_R(64, 1) else if (G == 2) GSD_ATTN_R(64, 2) else GSD_ATTN_R(64, 4)
+    } else {
+        if (G == 1) GSD_ATTN_R(128, 1) else if (G == 2) GSD_ATTN_R(128, 2) else GSD_ATTN_R(128, 4)
+    }
+#undef GSD_ATTN_R
     return hipGetLastError();
 }
 

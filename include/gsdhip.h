@@ -94,6 +94,20 @@ int gsdh_gqa_attention(void* stream, const float* q, const uint16_t* k_cache,
                        const uint16_t* v_cache, float* attn_out, int layer_idx, int pos,
                        int n_heads, int n_kv_heads, int head_dim, int max_seq_len, float sm_scale);
 
+/* gsd_cpu_rope_and_store_kv followed by gsd_cpu_gqa_attention
+ * (gsd_lq_cpu_engine.c:185-330), the two calls of one decode step's
+ * attention (gsd_lq_cpu_runtime.py:335-350), in one launch: q is rotated in
+ * place, fp16(k') and fp16(v) are stored at position pos, and attn_out is the
+ * attention over positions 0..pos.  Same results, bit for bit, as
+ * gsdh_rope_and_store_kv then gsdh_gqa_attention on the same stream (the
+ * rotation uses the same host cos/sin and no contraction).  One launch for
+ * head_dim 64 or 128, 1, 2 or 4 query heads per KV head and up to 8192
+ * positions; other shapes run the two launches. */
+int gsdh_rope_store_gqa_attention(void* stream, float* q, const float* k, const float* v,
+                                  uint16_t* k_cache, uint16_t* v_cache, float* attn_out,
+                                  int layer_idx, int pos, int n_heads, int n_kv_heads, int head_dim,
+                                  int max_seq_len, float rope_theta, int interleaved, float sm_scale);
+
 /* gsd_cpu_gqa_attention for callers that cannot allocate device memory (code
  * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
  * No counterpart in the reference.  Same arguments and results as
@@ -101,8 +115,9 @@ int gsdh_gqa_attention(void* stream, const float* q, const uint16_t* k_cache,
  * array of the library (one per GPU, kept until the process ends), so the
  * call allocates nothing.  Limit: n_kv_heads * splits * (n_heads/n_kv_heads)
  * * (head_dim + 2) * 8 bytes <= 8 MiB, splits = ceil((pos+1) / chunk) with
- * chunk = clamp(round_up((pos+1) * n_kv_heads / 256, 64), 64, 256); e.g. 8 KV
- * heads x 4 x 128 dims up to 32 splits (context 8192) use 1.1 MB.  Larger
+ * chunk = 256 up to 256 positions, else the smallest of 64, 128, 256 that is
+ * >= (pos+1) * n_kv_heads / 256 (256 at most); e.g. 8 KV heads x 4 x 128
+ * dims up to 32 splits (context 8192) use 1.1 MB.  Larger
  * calls fail with an error.  All calls on one GPU share the array: calls
  * that overlap on one GPU (different streams, or threads) race. */
 int gsdh_gqa_attention_noalloc(void* stream, const float* q, const uint16_t* k_cache,

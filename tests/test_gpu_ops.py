@@ -210,6 +210,43 @@ def test_attention_ignores_cache_rows_past_context(lib, ctx, nkv, hd):
     assert rel_l2(got, want) < TOL
 
 
+@pytest.mark.parametrize("ctx,nh,nkv,hd,il", [(1, 32, 8, 128, 1), (100, 32, 8, 128, 0), (256, 32, 8, 128, 1),
+                                               (700, 32, 8, 128, 1), (5000, 32, 8, 128, 0), (300, 8, 8, 64, 1),
+                                               (90, 8, 4, 64, 0), (777, 16, 2, 256, 1)])
+def test_rope_store_attention_equals_two_calls(lib, ctx, nh, nkv, hd, il):
+    """gsdh_rope_store_gqa_attention (one launch where the shape allows)
+    against gsdh_rope_and_store_kv + gsdh_gqa_attention on copies of the same
+    inputs: rotated q, the cache rows at pos and the output, bit for bit
+    (head dim 256 runs the two launches)."""
+    banner(f"rope + attention fused: ctx {ctx} heads {nh}/{nkv} hd {hd} interleaved {il}")
+    from gsdlq import pack
+    ms, pos = ctx + 4, ctx - 1
+    kc = pack.synth_f16(81, ctx, ms * nkv * hd, 1.0)
+    vc = pack.synth_f16(82, ctx, ms * nkv * hd, 1.0)
+    rng = np.random.default_rng(ctx + il)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k = rng.standard_normal(nkv * hd).astype(np.float32)
+    v = rng.standard_normal(nkv * hd).astype(np.float32)
+    sc = 1.0 / float(np.sqrt(hd))
+    outs = []
+    for fused in (False, True):
+        dq, dk, dv, dkc, dvc, out = D(q), D(k), D(v), D(kc), D(vc), E(nh * hd * 4)
+        if fused:
+            assert lib.gsdh_rope_store_gqa_attention(None, p(dq), p(dk), p(dv), p(dkc), p(dvc), p(out), 0, pos, nh,
+                                                     nkv, hd, ms, 1e6, il, sc) == 0
+        else:
+            assert lib.gsdh_rope_and_store_kv(None, p(dq), p(dk), p(dv), p(dkc), p(dvc), 0, pos, nh, nkv, hd, ms,
+                                              1e6, il) == 0
+            assert lib.gsdh_gqa_attention(None, p(dq), p(dkc), p(dvc), p(out), 0, pos, nh, nkv, hd, ms, sc) == 0
+        outs.append((H(dq, np.uint32, nh * hd), H(dkc, np.uint16, ms * nkv * hd), H(dvc, np.uint16, ms * nkv * hd),
+                     H(out, np.float32, nh * hd)))
+    (q0, k0, v0, o0), (q1, k1, v1, o1) = outs
+    assert np.array_equal(q0, q1), "rotated q"
+    assert np.array_equal(k0, k1) and np.array_equal(v0, v1), "cache"
+    assert np.isfinite(o1).all()
+    assert np.array_equal(o0.view(np.uint32), o1.view(np.uint32)), rel_l2(o1, o0)
+
+
 def test_attention_shape_changes_between_calls(lib):
     """One call per shape, in an order whose split-word regions overlap: 8 KV
     heads, then 2 KV heads of 256 dims, then 8 KV heads again (a word left by
