@@ -408,7 +408,8 @@ def probe(kind: str, n: int, ctx: int = 8192, m: int = 128):
     'gateup' = the fused gate/up matvec over 8 rotated Turbo layers,
     'copy' = a 256 MiB device copy (the calibration of FETCH/WRITE_SIZE),
     'attn' = RoPE + K/V append and decode attention at context `ctx`,
-    'prefill' = the batched projection of 8 Turbo layer sets for `m` tokens."""
+    'prefill' = the batched projection of 8 Turbo layer sets for `m` tokens,
+    'decode' = `n` greedy tokens of the 32-layer 7B Precision model."""
     from gsdlq import hip
     lib = hip.lib()
     if kind == "attn":
@@ -418,6 +419,16 @@ def probe(kind: str, n: int, ctx: int = 8192, m: int = 128):
     if kind == "prefill":
         r = bench_prefill(LayerBank("turbo", 8), ms=(m,), reps=n)
         print(f"[probe] prefill M {m}: {r}", flush=True)
+        return
+    if kind == "decode":
+        bank = LayerBank("precision", 3)
+        model = build_model(bank, 32, max_seq=n + 16)
+        model.generate_greedy([1], 4)   # warm (graphs captured)
+        t0 = time.time()
+        model.generate_greedy([1], n)
+        dt = time.time() - t0
+        model.close()
+        print(f"[probe] decode {n} tokens of the 32-layer 7B Precision model: {n / dt:.1f} tok/s", flush=True)
         return
     if kind == "copy":
         nbytes = 256 << 20
@@ -547,7 +558,7 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-attention", action="store_true")
     ap.add_argument("--no-c1", action="store_true")
-    ap.add_argument("--probe", choices=["gateup", "copy", "attn", "prefill"],
+    ap.add_argument("--probe", choices=["gateup", "copy", "attn", "prefill", "decode"],
                     help="run one kernel for rocprofv3 counters")
     ap.add_argument("--ctx", type=int, default=8192, help="--probe attn: context length")
     ap.add_argument("--m", type=int, default=128, help="--probe prefill: tokens")

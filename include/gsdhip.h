@@ -96,7 +96,7 @@ int gsdh_gqa_attention(void* stream, const float* q, const uint16_t* k_cache,
 
 /* gsd_cpu_rope_and_store_kv followed by gsd_cpu_gqa_attention
  * (gsd_lq_cpu_engine.c:185-330), the two calls of one decode step's
- * attention (gsd_lq_cpu_runtime.py:335-350), in one launch: q is rotated in
+ * attention (gsd_lq_cpu_runtime.py:325-361), in one launch: q is rotated in
  * place, fp16(k') and fp16(v) are stored at position pos, and attn_out is the
  * attention over positions 0..pos.  Same results, bit for bit, as
  * gsdh_rope_and_store_kv then gsdh_gqa_attention on the same stream (the
