@@ -367,9 +367,11 @@ struct gsdh_model {
     int* gen_tok = nullptr;
     float* gen_margin = nullptr;
     // per-token graphs: with and without the lm_head / argmax, for any
-    // position (split attention + merge) and for positions < kShortCtx (one
-    // attention block per KV head, no merge launch)
-    hipGraphExec_t g_full = nullptr, g_prefill = nullptr, g_full_s = nullptr, g_prefill_s = nullptr;
+    // position (split attention + merge) and, for positions below 64, 128
+    // and 256, one attention block per KV head whose chunk is that size (it
+    // loads the chunk's rows before it reads the position)
+    hipGraphExec_t g_full = nullptr, g_prefill = nullptr;
+    hipGraphExec_t g_full_s[kShortTiers] = {}, g_prefill_s[kShortTiers] = {};
     hipGraph_t capture_graph = nullptr;
     // persistent token kernel (one launch per token): device layer table,
     // hand-off words, per-block top-2 words and launch counters, and the
@@ -494,7 +496,9 @@ int issue_head(gsdh_model* m, bool greedy) {
 }
 
 // The per-token launch sequence (run_gpu_native_chat.py:892-969, fused).
-int issue_token(gsdh_model* m, bool with_head, bool short_ctx) {
+// short_chunk: 0 for the graph of any position, else the single attention
+// chunk (64, 128 or 256) of the graph for positions below it
+int issue_token(gsdh_model* m, bool with_head, int short_chunk) {
     const auto& c = m->c;
     m->pub_next = 0;
     HIPCHK(launch_embed(m->embed, &m->st->token, m->x, c.hidden, m->pub, m->pub_words, m->stream));
@@ -514,8 +518,8 @@ int issue_token(gsdh_model* m, bool with_head, bool short_ctx) {
         a.sm_scale = 1.0f / (float)std::sqrt((double)c.head_dim);
         a.chunk = m->chunk; a.max_splits = m->max_splits; a.ws = m->ws; a.counters = m->counters;
         a.err = &m->st->err;
-        if (short_ctx) {   // positions < kShortCtx: one block per KV head
-            a.chunk = kShortCtx;
+        if (short_chunk) {   // positions < short_chunk: one block per KV head
+            a.chunk = short_chunk;
             a.max_splits = 1;
         }
         HIPCHK(launch_attention(a, m->stream));
@@ -528,7 +532,8 @@ int issue_token(gsdh_model* m, bool with_head, bool short_ctx) {
 
 hipGraphExec_t token_graph(const gsdh_model* m, bool with_head, int pos) {
     if (m->engine == GSDH_ENGINE_PERSISTENT) return with_head ? m->gt_full : m->gt_prefill;
-    if (pos < kShortCtx) return with_head ? m->g_full_s : m->g_prefill_s;
+    for (int t = 0; t < kShortTiers; t++)
+        if (pos < kShortChunk[t]) return with_head ? m->g_full_s[t] : m->g_prefill_s[t];
     return with_head ? m->g_full : m->g_prefill;
 }
 
@@ -782,10 +787,10 @@ int run_prefill(gsdh_model* m, const int* prompt, int n, int start, bool head, i
     return 0;
 }
 
-int capture(gsdh_model* m, bool with_head, bool short_ctx, hipGraphExec_t* out) {
+int capture(gsdh_model* m, bool with_head, int short_chunk, hipGraphExec_t* out) {
     hipGraph_t g = nullptr;
     HIPCHK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
-    int rc = issue_token(m, with_head, short_ctx);
+    int rc = issue_token(m, with_head, short_chunk);
     hipError_t e = hipStreamEndCapture(m->stream, &g);
     if (rc) {
         if (g) (void)hipGraphDestroy(g);
@@ -894,8 +899,11 @@ int gsdh_model_create(const gsdh_model_config* cfg, gsdh_model** out) {
 int gsdh_model_destroy(gsdh_model* m) {
     if (!m) return 0;
     if (m->stream) (void)hipStreamSynchronize(m->stream);
-    for (hipGraphExec_t g : {m->g_full, m->g_prefill, m->g_full_s, m->g_prefill_s, m->gt_full, m->gt_prefill})
+    for (hipGraphExec_t g : {m->g_full, m->g_prefill, m->gt_full, m->gt_prefill})
         if (g) (void)hipGraphExecDestroy(g);
+    for (int t = 0; t < kShortTiers; t++)
+        for (hipGraphExec_t g : {m->g_full_s[t], m->g_prefill_s[t]})
+            if (g) (void)hipGraphExecDestroy(g);
     for (auto& t : m->hex)
         if (t.block) (void)hipFree(t.block);
     for (void* p : m->allocs) (void)hipFree(p);
@@ -1033,10 +1041,12 @@ int gsdh_model_finalize(gsdh_model* m) {
         for (int s = 0; s < 7; s++)
             if (!m->slot(l, s).set) return fail(-1, "finalize: layer %d slot %d not set", l, s);
     if (!m->slot(0, GSDH_LM_HEAD).set) return fail(-1, "finalize: lm_head not set");
-    int rc = capture(m, true, false, &m->g_full);
-    if (!rc) rc = capture(m, false, false, &m->g_prefill);
-    if (!rc) rc = capture(m, true, true, &m->g_full_s);
-    if (!rc) rc = capture(m, false, true, &m->g_prefill_s);
+    int rc = capture(m, true, 0, &m->g_full);
+    if (!rc) rc = capture(m, false, 0, &m->g_prefill);
+    for (int t = 0; t < kShortTiers && !rc; t++) {
+        rc = capture(m, true, kShortChunk[t], &m->g_full_s[t]);
+        if (!rc) rc = capture(m, false, kShortChunk[t], &m->g_prefill_s[t]);
+    }
     if (!rc) rc = setup_token_kernel(m);
     if (!rc) rc = setup_batched(m);
     if (rc) return rc;

@@ -178,6 +178,10 @@ hipError_t launch_rope_kv_rows(float* q, const float* k, const float* v, const R
 // Contexts up to this length run attention as one block per KV head (the
 // score buffer of attn_kernel holds 256 positions).
 constexpr int kShortCtx = 256;
+// the decode graphs of short contexts: one attention chunk per KV head, sized
+// to the position (a chunk's rows are loaded whatever the position)
+constexpr int kShortTiers = 3;
+constexpr int kShortChunk[kShortTiers] = {64, 128, kShortCtx};
 
 struct AttnArgs {
     const float* q;
