@@ -66,6 +66,20 @@ __device__ __forceinline__ float wave_sum_valu(float v) {
     v = swap_add16(v, v);
     return swap_add32(v, v, false);
 }
+// Whole-wave max of values >= 0 (no NaN) in every lane: unsigned compares of
+// the bit patterns order such floats, and need none of the canonicalising
+// moves that float max inserts after each DPP or swap.
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+    unsigned u = __float_as_uint(v);
+    u = max(u, (unsigned)__builtin_amdgcn_update_dpp(0, (int)u, 0xB1, 0xF, 0xF, false));
+    u = max(u, (unsigned)__builtin_amdgcn_update_dpp(0, (int)u, 0x4E, 0xF, 0xF, false));
+    u = max(u, (unsigned)__builtin_amdgcn_update_dpp(0, (int)u, 0x141, 0xF, 0xF, false));
+    u = max(u, (unsigned)__builtin_amdgcn_update_dpp(0, (int)u, 0x140, 0xF, 0xF, false));
+    auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    u = max(r[0], r[1]);
+    r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __uint_as_float(max(r[0], r[1]));
+}
 __device__ __forceinline__ float wave_max_valu(float v) {
     v = row16_max(v);
     auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);

@@ -1496,13 +1496,19 @@ __device__ __forceinline__ void mv4_publish(const HexArgs& a, int lead, float* s
 // arguments.
 template <int TB, int LR, int EPI>
 __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) hexmv4_kernel(const HexArgs a) {
-    __shared__ __attribute__((aligned(16))) uint32_t stab[TB > 0 ? TB * 64 : 1];
+    // (whole 16-entry slices: every filling wave writes 16 entries, the
+    // padding ones from the zero padding of the field table)
+    __shared__ __attribute__((aligned(16))) uint32_t stab[TB > 0 ? ((TB + 15) & ~15) * 64 : 1];
     __shared__ float red[2][kMv4MaxWaves][16];
     __shared__ float tkl[kMaxSeg][kMaxRank];
     // LR 1 and 3 form the projections in the block; LR 3: every segment has
     // rank exactly 2 and no tmp_k (each Precision tensor), so the slot masks
     // and the rank-1 and tmp_k paths are not compiled in
     constexpr bool kIn = LR == 1 || LR == 3, kR2 = LR == 3;
+    // RMSNorm of x: always in the fused q/k/v (RoPE) and gate/up (SwiGLU)
+    // launches, never in the residual ones (the launcher sends any other
+    // combination to the generic kernel), read from the arguments otherwise
+    constexpr int kNorm = EPI == kEpiResidual ? 0 : (EPI == kEpiSwiGLU || EPI == kEpiRopeKV ? 1 : -1);
     // LR 1 / 3: each wave's partial rank-k dot products over its own columns
     // (times S[j]), slot r = j (paired launch: the wave's group's segment) or
     // 2 g + j, wave index last
@@ -1680,7 +1686,27 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     float dk[kVS];
 #pragma unroll
     for (int r = 0; r < kVS; r++) dk[r] = 0.f;
+    // whole chunks (cols a multiple of 128, every 7B shape) and a norm known
+    // here: the loads need no per-lane column test and no fill, and address as
+    // a uniform chunk base plus the lane's offset
+    const bool whole = kNorm >= 0 && (cols0 & 127) == 0;
     auto xload = [&](int p0) {
+        if (whole) {
+#pragma unroll
+            for (int i = 0; i < kXP; i++) {
+                const int p = p0 + i;
+                if (p < P) {
+                    const int c0 = (wr + p * WR) * 128;
+                    xv[i] = *reinterpret_cast<const float2*>(a.x + c0 + 2 * lane);
+                    if constexpr (kNorm == 1) wv[i] = *reinterpret_cast<const float2*>(a.norm_w + c0 + 2 * lane);
+                    if constexpr (kIn) {
+#pragma unroll
+                        for (int r = 0; r < kVS; r++) vt[r][i] = *reinterpret_cast<const uint32_t*>(vrow[r] + c0 + 2 * lane);
+                    }
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < kXP; i++) {
             const int p = p0 + i, col = (wr + p * WR) * 128 + 2 * lane;
@@ -1690,7 +1716,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
             for (int r = 0; r < kVS; r++) vt[r][i] = 0u;
             if (p < P && col < a.cols) {
                 xv[i] = *reinterpret_cast<const float2*>(a.x + col);
-                if (a.norm_w) wv[i] = *reinterpret_cast<const float2*>(a.norm_w + col);
+                if (kNorm != 0 && a.norm_w) wv[i] = *reinterpret_cast<const float2*>(a.norm_w + col);
                 if constexpr (kIn) {
 #pragma unroll
                     for (int r = 0; r < kVS; r++) vt[r][i] = *reinterpret_cast<const uint32_t*>(vrow[r] + col);
@@ -1711,7 +1737,8 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
             if (p < P) {
                 ss = fmaf(xv[i].x, xv[i].x, ss);
                 ss = fmaf(xv[i].y, xv[i].y, ss);
-                const float xa = xv[i].x * wv[i].x, xb = xv[i].y * wv[i].y;
+                const float xa = kNorm == 0 ? xv[i].x : xv[i].x * wv[i].x;
+                const float xb = kNorm == 0 ? xv[i].y : xv[i].y * wv[i].y;
                 if constexpr (kIn) {
                     // every slot, used or not: a loaded word no path consumes
                     // stays pending, and a later reuse of its register then
@@ -1758,9 +1785,23 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
         eup[k][0] = eup[k][1] = 0u;
     }
     float esk = 0.f;   // LR 1 / 3: lane 2 g + j of wave 0 holds S[j] of segment g
-    if (kIn && wid == 0 && lane < 2 * kMaxSeg && ((emask >> lane) & 1u)) {
-        const float* sp = lane < 2 ? kseg[0].S : (lane < 4 ? kseg[1].S : kseg[2].S);
-        esk = sp[lane & 1];
+    if constexpr (kIn) {
+        // the three pointers as scalar reads, selected per lane (a per-lane
+        // index into the arguments becomes a vector load of the pointer, and
+        // the wait for it drains every load in flight); every lane of every
+        // wave loads (unused lanes: the start of x), so that no branch merges
+        // load sequences of different lengths, after which the compiler
+        // drains all loads before the first use of x
+        // (global pointers: through a generic one the load would be a flat
+        // load, and a flat load in flight makes every later wait a full drain)
+        using GF = const __attribute__((address_space(1))) float;
+        GF* s0 = (GF*)kseg[0].S;
+        GF* s1 = (GF*)kseg[1].S;
+        GF* s2 = (GF*)kseg[2].S;
+        __asm__ volatile("" : "+s"(s0), "+s"(s1), "+s"(s2));
+        const bool use = lane < 2 * kMaxSeg && ((emask >> lane) & 1u);
+        GF* sp = !use ? (GF*)a.x : (lane < 2 ? s0 : (lane < 4 ? s1 : s2));
+        esk = sp[use ? (lane & 1) : 0];
     }
     if (wid == 0 && lane < 16) {
 #pragma unroll
@@ -1806,8 +1847,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     if (TB > 0) {
         if (wid * 16 < TB) {
 #pragma unroll
-            for (int j = 0; j < 16; j++)
-                if (wid * 16 + j < TB) stab[(wid * 16 + j) * 64 + lane] = fv[j];
+            for (int j = 0; j < 16; j++) stab[(wid * 16 + j) * 64 + lane] = fv[j];
         }
         // fewer than TB / 16 waves: the remaining slices, one entry at a time
         KU32* f = (KU32*)a.seg[0].fields;
@@ -1853,7 +1893,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     // wave reductions in VALU (DPP and lane swaps): the LDS permutes of
     // shuffles cost 16 waves x 6 steps per value
     ss = wave_sum_valu(ss);
-    mx = wave_max_valu(mx);
+    mx = wave_max_nonneg(mx);   // (fmaxf above keeps NaN out of mx)
     if (lane == 0) ssq[wid] = ss;
     if constexpr (kIn) {
         // the slots' partial sums reduced together: the 32-lane swaps pair
@@ -2567,8 +2607,13 @@ hipError_t launch_hexmv4(const HexArgs& a, hipStream_t st) {
         case kEpiRopeKV: GSD_MV4(T, kEpiRopeKV)              \
         default: return hipErrorInvalidValue;                \
     }
-    if (shared && a.seg[0].n_pts == 217) GSD_MV4E(217)
-    if (shared && a.seg[0].n_pts == 127) GSD_MV4E(127)
+    // the epilogue-specialised kernels fix the RMSNorm by the epilogue (with
+    // it: RoPE + K/V append and SwiGLU; without it: residual)
+    const bool norm_fixed = a.epilogue == kEpiResidual ? a.norm_w == nullptr
+                            : (a.epilogue == kEpiSwiGLU || a.epilogue == kEpiRopeKV) ? a.norm_w != nullptr
+                                                                                      : true;
+    if (shared && norm_fixed && a.seg[0].n_pts == 217) GSD_MV4E(217)
+    if (shared && norm_fixed && a.seg[0].n_pts == 127) GSD_MV4E(127)
     GSD_MV4(0, -1)
 #undef GSD_MV4E
 #undef GSD_MV4
