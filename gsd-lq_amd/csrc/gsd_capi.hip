@@ -5,6 +5,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -361,6 +362,11 @@ struct gsdh_model {
     } pf;
     unsigned long long* pub = nullptr;   // rank-k publication words, one range per matvec launch
     int pub_words = 0, pub_next = 0;
+    // decode attention inside the q/k/v launch (short-context graphs): the
+    // q/k/v hand-off words [qd + kvd] and the token counter that tags them
+    unsigned long long* fa_words = nullptr;
+    unsigned* fa_epoch = nullptr;
+    bool fa_on = true;                   // GSD_FUSED_ATTN=0 turns it off (A/B)
     int chunk = 64, max_splits = 1;
     StepState* st = nullptr;        // device
     StepState* st_host = nullptr;   // pinned
@@ -427,27 +433,59 @@ int prep_lowrank(gsdh_model* m, HexArgs& a) {
     return 0;
 }
 
-int issue_linear(gsdh_model* m, int l, int mask) {
+// q, k, v of layer l: fused attention RMSNorm; interleaved RoPE + KV append in the epilogue
+HexArgs qkv_args(gsdh_model* m, int l) {
     const auto& c = m->c;
+    HexArgs a{};
+    a.nseg = 3;
+    fill_seg(a.seg[0], m->slot(l, GSDH_Q), m, m->q);
+    fill_seg(a.seg[1], m->slot(l, GSDH_K), m, m->k);
+    fill_seg(a.seg[2], m->slot(l, GSDH_V), m, m->v);
+    a.x = m->x; a.norm_w = m->norm(l, 0); a.eps = c.rms_eps; a.cols = c.hidden; a.epilogue = kEpiStore;
+    a.scale_t = 1;
+    if (c.rope_interleaved) {
+        a.epilogue = kEpiRopeKV;
+        RopeKV& r = a.rope;
+        r.cs = m->cs; r.pos_dev = &m->st->pos; r.k_cache = m->kc; r.v_cache = m->vc; r.layer = l;
+        r.n_heads = c.n_heads; r.n_kv = c.n_kv_heads; r.hd = c.head_dim; r.max_seq = c.max_seq_len;
+        r.interleaved = 1;
+    }
+    return a;
+}
+
+// q, k, v of layer l and the decode attention of positions < 256 in one
+// launch (sets *fused); *fused = false, with nothing launched, where the
+// fused kernel does not cover the model (the caller then issues the two).
+int issue_qkv_attention(gsdh_model* m, int l, bool* fused) {
+    const auto& c = m->c;
+    *fused = false;
+    if (!m->fa_on || !m->fa_words || !c.rope_interleaved) return 0;
+    HexArgs a = qkv_args(m, l);
+    const int pub0 = m->pub_next;
+    int rc = prep_lowrank(m, a);
+    if (rc) return rc;
+    a.fa.words = m->fa_words; a.fa.out = m->attn; a.fa.epoch_dev = m->fa_epoch;
+    a.fa.sm_scale = 1.0f / (float)std::sqrt((double)c.head_dim);
+    a.fa.nkv = c.n_kv_heads;
+    a.err = &m->st->err;
+    const hipError_t e = launch_hexmv4(a, m->stream);
+    if (e == hipErrorNotSupported) {
+        m->pub_next = pub0;   // (nothing launched: the two-launch path takes these words)
+        return 0;
+    }
+    HIPCHK(e);
+    *fused = true;
+    return 0;
+}
+
+int issue_linear(gsdh_model* m, int l, int mask) {
     int rc = 0;
-    if (mask & 1) {   // q, k, v: fused attention RMSNorm; interleaved RoPE + KV append in the epilogue
-        HexArgs a{};
-        a.nseg = 3;
-        fill_seg(a.seg[0], m->slot(l, GSDH_Q), m, m->q);
-        fill_seg(a.seg[1], m->slot(l, GSDH_K), m, m->k);
-        fill_seg(a.seg[2], m->slot(l, GSDH_V), m, m->v);
-        a.x = m->x; a.norm_w = m->norm(l, 0); a.eps = c.rms_eps; a.cols = c.hidden; a.epilogue = kEpiStore;
-        a.scale_t = 1;
-        if (c.rope_interleaved) {
-            a.epilogue = kEpiRopeKV;
-            RopeKV& r = a.rope;
-            r.cs = m->cs; r.pos_dev = &m->st->pos; r.k_cache = m->kc; r.v_cache = m->vc; r.layer = l;
-            r.n_heads = c.n_heads; r.n_kv = c.n_kv_heads; r.hd = c.head_dim; r.max_seq = c.max_seq_len;
-            r.interleaved = 1;
-        }
+    if (mask & 1) {
+        HexArgs a = qkv_args(m, l);
         if ((rc = prep_lowrank(m, a))) return rc;
         HIPCHK(launch_hexmv4(a, m->stream));
     }
+    const auto& c = m->c;
     if (mask & 2) {   // o projection + residual
         HexArgs a{};
         a.nseg = 1;
@@ -501,9 +539,18 @@ int issue_head(gsdh_model* m, bool greedy) {
 int issue_token(gsdh_model* m, bool with_head, int short_chunk) {
     const auto& c = m->c;
     m->pub_next = 0;
-    HIPCHK(launch_embed(m->embed, &m->st->token, m->x, c.hidden, m->pub, m->pub_words, m->stream));
+    HIPCHK(launch_embed(m->embed, &m->st->token, m->x, c.hidden, m->pub, m->pub_words, m->fa_epoch, m->stream));
     for (int l = 0; l < c.n_layers; l++) {
-        int rc = issue_linear(m, l, 1);
+        // positions < 256: the attention in the q/k/v launch where it covers the model
+        bool fused = false;
+        int rc = short_chunk ? issue_qkv_attention(m, l, &fused) : 0;
+        if (rc) return rc;
+        if (fused) {
+            rc = issue_linear(m, l, 2 | 4 | 8);
+            if (rc) return rc;
+            continue;
+        }
+        rc = issue_linear(m, l, 1);
         if (rc) return rc;
         if (!c.rope_interleaved) {   // (i, i+hd/2) pairs are not adjacent rows: separate kernel
             RopeKV r{};
@@ -846,6 +893,12 @@ int gsdh_model_create(const gsdh_model_config* cfg, gsdh_model** out) {
     A((void**)&m->counters, (size_t)c.n_kv_heads * 4);
     m->pub_words = (4 * c.n_layers + 1) * kLeadMax;
     A((void**)&m->pub, (size_t)m->pub_words * 8);
+    A((void**)&m->fa_words, (qd + kvd) * 8);
+    A((void**)&m->fa_epoch, 4);
+    {
+        const char* fe = std::getenv("GSD_FUSED_ATTN");
+        m->fa_on = !(fe && fe[0] == '0');
+    }
     A((void**)&m->st, sizeof(StepState));
     A((void**)&m->gen_tok, (size_t)c.max_seq_len * 4);
     A((void**)&m->gen_margin, (size_t)c.max_seq_len * 4);
@@ -876,6 +929,8 @@ int gsdh_model_create(const gsdh_model_config* cfg, gsdh_model** out) {
                                 attention_ws_bytes(c.n_kv_heads, m->max_splits, c.n_heads / c.n_kv_heads, c.head_dim) / 4,
                                 m->stream);
         if (e == hipSuccess) e = launch_fill_u32((unsigned*)m->pub, 0u, 2 * (size_t)m->pub_words, m->stream);
+        if (e == hipSuccess) e = launch_fill_u32((unsigned*)m->fa_words, 0u, 2 * (qd + kvd), m->stream);
+        if (e == hipSuccess) e = launch_fill_u32(m->fa_epoch, 0u, 1, m->stream);
         if (e == hipSuccess) e = launch_fill_u32((unsigned*)m->kc, 0u, kvn / 2, m->stream);
         if (e == hipSuccess) e = launch_fill_u32((unsigned*)m->vc, 0u, kvn / 2, m->stream);
         if (e == hipSuccess) e = hipStreamSynchronize(m->stream);

@@ -79,6 +79,21 @@ struct HexArgs {
     // be zero when the launch starts (each launch of a sequence has its own).
     unsigned long long* pub;
     unsigned* err;             // set to 1 when the wait exceeds its bound
+    // Decode attention in the q/k/v launch (kEpiRopeKV, positions < 256):
+    // the last nkv blocks of the grid are attention blocks, one per KV head.
+    // The q/k/v epilogue publishes its outputs as 64-bit words, tag << 32 |
+    // bits (q rows as fp32; the new K and V rows, as written to the cache, as
+    // fp16 pairs), one relaxed device-scope store each; the attention block
+    // of a KV head waits for the words of its rows to carry the launch's tag
+    // = *epoch_dev * 64 + layer + 1 (epoch_dev: the token counter the
+    // embedding launch advances; layers < 64), so nothing is ever cleared.
+    struct FusedAttn {
+        unsigned long long* words;   // [n_heads * hd + n_kv * hd]: q rows, K pairs, V pairs
+        float* out;                  // attention output [n_heads * hd]
+        const unsigned* epoch_dev;
+        float sm_scale;
+        int nkv;                     // 0: no attention blocks
+    } fa;
     // hexmv4 launch plan, filled in by launch_hexmv4 (callers leave it zero):
     // per-launch constants the kernel would otherwise derive with integer
     // divisions ahead of its first loads
@@ -88,6 +103,7 @@ struct HexArgs {
         int nunits;            // row-block units of the launch
         int ub1, ub2;          // first units of segments 1 and 2
         int units_q, units_r;  // units of matvec block b: units_q + (b < units_r)
+        int nw;                // matvec waves per block (blocks may be larger: fa)
     } mv;
 };
 
@@ -235,9 +251,10 @@ int fail(int code, const char* fmt, ...);
 size_t attention_ws_bytes(int n_kv, int max_splits, int group, int hd);
 
 // embedding row of *token_dev to fp32 x; also zeroes clear[0..nclear) (the
-// rank-k publication words of the token's matvec launches)
+// rank-k publication words of the token's matvec launches) and, when epoch
+// is non-null, advances the token counter *epoch by one
 hipError_t launch_embed(const uint16_t* embed, const int* token_dev, float* x, int hidden,
-                        unsigned long long* clear, int nclear, hipStream_t stream);
+                        unsigned long long* clear, int nclear, unsigned* epoch, hipStream_t stream);
 
 // Greedy argmax with the reference's nan_to_num (gsd_lq_cpu_runtime.py:423);
 // with a step state st it writes the token and the margin top1-top2 there

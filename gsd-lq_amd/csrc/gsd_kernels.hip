@@ -944,6 +944,11 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
     const uint16_t* vb = a.v_cache + lbase;
     const int rmax = a.max_seq - 1;
     const int pw0 = t0 + wid * PW;   // the wave's first position
+    // this launch's epoch, read before any work: the merging block advances
+    // the head's counter once it has every split's words, so each block
+    // must have read it by then (a block that read it late, after a fast
+    // merger's update, would tag its words with the next launch's epoch)
+    const unsigned ep = a.epoch ? a.epoch : (a.max_splits > 1 ? a.counters[kvh] + 1u : 0u);
 
     // q (A operand source): lane l, head m = l & 15 (m < G), dims
     // 32 j + 8 (l >> 4) .. + 7; issued first, the K and V rows behind it
@@ -1230,7 +1235,6 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
     // hand-over: words [kvh][split][g][2 + HD]; the block of the last split
     // merges (blocks start in index order, so every other split's block
     // has started before it and finishes without it)
-    const unsigned ep = a.epoch ? a.epoch : a.counters[kvh] + 1u;
     const unsigned long long tag = (unsigned long long)ep << 32;
     constexpr int WPH = 2 + HD;   // words per head
     unsigned long long* wsk = a.ws + (size_t)kvh * a.max_splits * G * WPH;
@@ -1243,7 +1247,6 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
         }
     }
     if (split != nsplit - 1) return;
-    if (tid == 0 && !a.epoch) a.counters[kvh] = ep;   // the next launch's epoch base (stream order)
 
     // merge: out = sum_s f_s o_s / sum_s f_s l_s with f_s = 2^(m_s - max m),
     // splits in order.  Thread tid reads word (max, sum) item tid = s G + gi
@@ -1281,6 +1284,8 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
         }
         __builtin_amdgcn_s_sleep(2);
     }
+    // every split's block has read the counter: the next launch's epoch base (stream order)
+    if (tid == 0 && !a.epoch) a.counters[kvh] = ep;
     const float m0 = tid < c ? __uint_as_float((unsigned)wm0) : -INFINITY, l0 = __uint_as_float((unsigned)wl0);
     // max over the splits of head gi: lanes gi, gi + G, ... of each wave,
     // then the waves (lanes 0..G-1 publish); weights f_s and f_s l_s by item
@@ -1322,10 +1327,11 @@ __global__ void __launch_bounds__(512) attn_rope_kernel(const AttnArgs a, const 
 }
 
 __global__ void embed_kernel(const uint16_t* embed, const int* token, float* x, int hidden,
-                             unsigned long long* clear, int nclear) {
+                             unsigned long long* clear, int nclear, unsigned* epoch) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < hidden) x[i] = h2f(embed[(size_t)(*token) * hidden + i]);
     if (i < nclear) clear[i] = 0ull;
+    if (i == 0 && epoch) *epoch += 1u;   // the token counter of the fused attention tags
 }
 
 
@@ -1494,8 +1500,283 @@ __device__ __forceinline__ void mv4_publish(const HexArgs& a, int lead, float* s
 // instructions per launch); 2: any rank, projections published by leading
 // blocks.  EPI: the epilogue (HexEpilogue), or -1 to read it from the
 // arguments.
-template <int TB, int LR, int EPI>
+// ------------------------------------------------------------------------
+// Decode attention of one KV head inside the q/k/v launch, positions
+// 0 .. pos with pos < 256 (gsd_lq_cpu_engine.c:264-330): the arithmetic of
+// attn_dec_body for one split of 8 waves x 32 positions, with q and the new
+// K / V rows taken from the words the q/k/v epilogue publishes (that launch
+// is still writing them), and the cache rows of the earlier positions
+// loaded at the start, while the matvec blocks run.  The part after the wait
+// runs twice: first on a zero q with no output, while the words are still
+// outstanding, which brings its code into the instruction cache (every
+// launch starts with a cold one, and the fetch of straight-line code is what
+// the short tail after the wait would otherwise spend), then on the words.
+// ------------------------------------------------------------------------
+// Inputs of the attention blocks, by value (the kernel's argument block is
+// read through scalar loads in the matvec path)
+struct FaIn {
+    const uint16_t* k_cache;
+    const uint16_t* v_cache;
+    const int* pos_dev;
+    const unsigned long long* words;
+    float* out;
+    unsigned* err;
+    int layer, max_seq, n_kv, n_heads;
+    float sm_scale;
+};
+
+// 16-byte load through a global pointer
+__device__ __forceinline__ uint4 gload4(const __attribute__((address_space(1))) uint16_t* p) {
+    const u32x4v v = *reinterpret_cast<const __attribute__((address_space(1))) u32x4v*>(p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+template <int HD, int G>
+__device__ __forceinline__ void attn_fa_block(const FaIn a, int kvh, unsigned tag) {
+    constexpr int NW = 8, PW = 32, NGRP = 2, NJ = HD / 32, LPR = HD / 8, RPI = 64 / LPR, NV = PW / RPI;
+    constexpr int NQ = G * HD, NT = NQ + HD;   // words taken: q rows, then K and V pairs
+    constexpr float kLog2e = 1.44269504088896340736f;
+    static_assert(G == 1 || G == 2 || G == 4, "query heads per KV head");
+    static_assert(HD == 64 || HD == 128, "head dim");
+    __shared__ __attribute__((aligned(16))) uint16_t vs[NW][32 * HD];   // V staging, then o partials
+    __shared__ __attribute__((aligned(16))) float es[NW][32][4];        // e[p][g] of the wave's positions
+    __shared__ float wm[NW][4], wl[NW][4];
+    __shared__ __attribute__((aligned(16))) float qs[NQ];               // q rows of the group
+    __shared__ __attribute__((aligned(16))) uint32_t kvn[HD];           // new K row, then V row (fp16 pairs)
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    if (wid >= NW) return;
+    using KI32 = const __attribute__((address_space(4))) int;
+    const int pos = *(KI32*)a.pos_dev;
+    const size_t rowstride = (size_t)a.n_kv * HD;
+    const size_t lbase = (size_t)a.layer * a.max_seq * rowstride + (size_t)kvh * HD;
+    const uint16_t* kb = a.k_cache + lbase;
+    const uint16_t* vb = a.v_cache + lbase;
+    const int rmax = a.max_seq - 1;
+    const int pw0 = wid * PW;   // the wave's first position
+    const int m = lane & 15, kg = lane >> 4;
+    const int vrow = lane / LPR, vcol = 8 * (lane % LPR);
+    for (int i = tid; i < NQ; i += NW * 64) qs[i] = 0.f;
+    const int n = pos + 1;
+    const int te = min(n, pw0 + PW);   // the wave's positions: pw0 .. te - 1
+    const int g = tid / HD, d = tid % HD;
+    const bool own = tid < G * HD;
+    const int qd = a.n_heads * HD, kvd = a.n_kv * HD;
+    const unsigned long long* wq = a.words + (size_t)kvh * NQ;
+    const unsigned long long* wk = a.words + qd + (size_t)kvh * (HD / 2);
+    const unsigned long long* wv = wk + kvd / 2;
+    int nit = 2;
+    __asm__ volatile("" : "+s"(nit));   // a loop, not two copies of its body
+#pragma clang loop unroll(disable)
+    for (int it = 0; it < nit; it++) {
+        lds_barrier();   // q zeroed (first pass) / the previous pass's LDS reads done
+        // K (B operand): lane l, position pw0 + 16 grp + (l & 15), dims
+        // 32 j + 8 (l >> 4) .. + 7; V: lane l, position pw0 + RPI u + l / LPR,
+        // dims 8 (l % LPR) .. + 7 (the second pass finds them in L2, and
+        // loads them ahead of its wait)
+        // (the bases pass through an asm at each pass: hoisted out of the
+        // loop, the 16 row addresses would stay live, and spill, across it)
+        using GU16 = const __attribute__((address_space(1))) uint16_t;
+        GU16* kbi = (GU16*)kb;
+        GU16* vbi = (GU16*)vb;
+        int rm = rmax;
+        __asm__ volatile("" : "+s"(kbi), "+s"(vbi), "+s"(rm));
+        uint4 kr[NGRP][NJ];
+#pragma unroll
+        for (int grp = 0; grp < NGRP; grp++) {
+            const int t = min(pw0 + 16 * grp + m, rm);
+#pragma unroll
+            for (int j = 0; j < NJ; j++)
+                kr[grp][j] = gload4(kbi + (size_t)t * rowstride + 32 * j + 8 * kg);
+        }
+        uint4 vr[NV];
+#pragma unroll
+        for (int u = 0; u < NV; u++) {
+            const int t = min(pw0 + RPI * u + vrow, rm);
+            vr[u] = gload4(vbi + (size_t)t * rowstride + vcol);
+        }
+        // V rows into the wave's LDS (each lane reads back its own words)
+        uint4* vw = reinterpret_cast<uint4*>(&vs[wid][0]);
+#pragma unroll
+        for (int u = 0; u < NV; u++) vw[u * 64 + lane] = vr[u];
+        if (it == 1) {
+            // the words of this KV head, all with this launch's tag: each
+            // wave waits for its own share (no block barrier per round), then
+            // the block meets once (bounded)
+            for (int spins = 0;; spins++) {
+                unsigned stale = 0u;
+                for (int i = tid; i < NT; i += NW * 64) {
+                    const unsigned long long* p = i < NQ ? wq + i : (i < NQ + HD / 2 ? wk + (i - NQ) : wv + (i - NQ - HD / 2));
+                    const unsigned long long w = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if ((unsigned)(w >> 32) != tag) stale = 1u;
+                    else if (i < NQ) qs[i] = __uint_as_float((unsigned)w);
+                    else kvn[i - NQ] = (unsigned)w;
+                }
+                if (__ballot(stale != 0u) == 0ull) break;
+                if (spins == (1 << 18)) {
+                    if (a.err) *a.err = 1u;
+                    break;
+                }
+            }
+            lds_barrier();
+        }
+        // position pos takes the new K and V rows (the words; in the first
+        // pass whatever the LDS holds), selected where the rows are used
+        uint4 knew[NJ];
+#pragma unroll
+        for (int j = 0; j < NJ; j++) knew[j] = *reinterpret_cast<const uint4*>(&kvn[16 * j + 4 * kg]);
+        const uint4 vnew = *reinterpret_cast<const uint4*>(&kvn[HD / 2 + vcol / 2]);
+
+        // q of the group's heads (A operand: lane l, head m = l & 15 < G)
+        float4 qa[NJ][2];
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            qa[j][0] = qa[j][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (m < G) {
+                const float4* qp = reinterpret_cast<const float4*>(&qs[m * HD + 32 * j + 8 * kg]);
+                qa[j][0] = qp[0];
+                qa[j][1] = qp[1];
+            }
+        }
+        // power-of-two prescale of q: largest |q| into [2^13, 2^14); fp16 high + low parts
+        float mx = 0.f;
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(qa[j][h].x), fabsf(qa[j][h].y)), fmaxf(fabsf(qa[j][h].z), fabsf(qa[j][h].w))));
+        mx = wave_max_valu(mx);
+        int ex = 0;
+        if (mx > 0.f && mx < INFINITY) (void)frexpf(mx, &ex);
+        const float up = ldexpf(1.f, 14 - ex);
+        const float scl = ldexpf(1.f, ex - 14) * a.sm_scale * kLog2e;
+        half8v ahi[NJ], alo[NJ];
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const float f[8] = {qa[j][0].x, qa[j][0].y, qa[j][0].z, qa[j][0].w,
+                                qa[j][1].x, qa[j][1].y, qa[j][1].z, qa[j][1].w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float s = f[e] * up;
+                const _Float16 h = (_Float16)s;
+                ahi[j][e] = h;
+                alo[j][e] = (_Float16)(s - (float)h);
+            }
+        }
+        // scores of the wave's 32 positions: lanes 0-15, element g = head g
+        float sv[NGRP][4];
+#pragma unroll
+        for (int grp = 0; grp < NGRP; grp++) {
+            float4v dd = {0.f, 0.f, 0.f, 0.f};
+            const bool at = pw0 + 16 * grp + m == pos;
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                const half8v b = __builtin_bit_cast(half8v, at ? knew[j] : kr[grp][j]);
+                dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[j], b, dd, 0, 0, 0);
+                dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[j], b, dd, 0, 0, 0);
+            }
+            const bool ok = pw0 + 16 * grp + m < te;
+#pragma unroll
+            for (int gg = 0; gg < 4; gg++) sv[grp][gg] = ok ? dd[gg] * scl : -INFINITY;
+        }
+        // the wave's max and exp2-sum per head
+        float mw[4], lw[4];
+#pragma unroll
+        for (int gg = 0; gg < 4; gg++) {
+            mw[gg] = row16_max(fmaxf(sv[0][gg], sv[1][gg]));
+            const float mu = mw[gg] == -INFINITY ? 0.f : mw[gg];
+            sv[0][gg] = __builtin_amdgcn_exp2f(sv[0][gg] - mu);
+            sv[1][gg] = __builtin_amdgcn_exp2f(sv[1][gg] - mu);
+            lw[gg] = row16_sum(sv[0][gg] + sv[1][gg]);
+        }
+        if (lane < 16) {
+#pragma unroll
+            for (int grp = 0; grp < NGRP; grp++)
+                *reinterpret_cast<float4*>(&es[wid][16 * grp + lane][0]) = make_float4(sv[grp][0], sv[grp][1], sv[grp][2], sv[grp][3]);
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int gg = 0; gg < 4; gg++) {
+                wm[wid][gg] = mw[gg];
+                wl[wid][gg] = lw[gg];
+            }
+        }
+        if (pos >= pw0 && pos < pw0 + PW && vrow == (pos - pw0) % RPI)   // the lanes that staged row pos
+            vw[((pos - pw0) / RPI) * 64 + lane] = vnew;
+        float acc[G][8];
+#pragma unroll
+        for (int gg = 0; gg < G; gg++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc[gg][e] = 0.f;
+        const int nv_live = (max(te - pw0, 0) + RPI - 1) / RPI;   // loads holding a valid row
+        for (int u = 0; u < nv_live; u++) {
+            const int p = RPI * u + vrow;
+            if (pw0 + p < te) {
+                float vf[8];
+                unpack8(vw[u * 64 + lane], vf);
+                const float4 w4 = *reinterpret_cast<const float4*>(&es[wid][p][0]);
+                const float wg[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+                for (int gg = 0; gg < G; gg++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) acc[gg][e] = fmaf(wg[gg], vf[e], acc[gg][e]);
+            }
+        }
+        // o partials of the wave's lane rows (HD 64: rows folded pairwise)
+        float* ob = reinterpret_cast<float*>(&vs[wid][0]);
+        if constexpr (HD == 64) {
+#pragma unroll
+            for (int gg = 0; gg < G; gg++)
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    acc[gg][e] += __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(acc[gg][e]), 0x128, 0xF, 0xF, false));
+        }
+        if (HD == 128 || (lane & 15) < 8) {
+            const int rr = lane >> 4, c = HD == 128 ? (lane & 15) : (lane & 7);
+#pragma unroll
+            for (int gg = 0; gg < G; gg++) {
+                float4* op = reinterpret_cast<float4*>(ob + (rr * G + gg) * HD + 8 * c);
+                op[0] = make_float4(acc[gg][0], acc[gg][1], acc[gg][2], acc[gg][3]);
+                op[1] = make_float4(acc[gg][4], acc[gg][5], acc[gg][6], acc[gg][7]);
+            }
+        }
+        lds_barrier();
+        // the block's (max, sum, o) per head: thread (g, d), waves in order
+        if (own) {
+            float M = -INFINITY, L = 0.f, O = 0.f;
+            for (int w = 0; w < NW; w++) M = fmaxf(M, wm[w][g]);
+            for (int w = 0; w < NW; w++) {
+                const float f = __builtin_amdgcn_exp2f(wm[w][g] - M);   // (-inf: an empty wave, 0)
+                const float* o = reinterpret_cast<const float*>(&vs[w][0]);
+                const float s = (o[(0 * G + g) * HD + d] + o[(1 * G + g) * HD + d]) + (o[(2 * G + g) * HD + d] + o[(3 * G + g) * HD + d]);
+                L = fmaf(f, wl[w][g], L);
+                O = fmaf(f, s, O);
+            }
+            if (it == 1) a.out[(size_t)(kvh * G + g) * HD + d] = O / L;
+        }
+    }
+}
+
+// FAHD > 0: the q/k/v launch with the decode attention of positions < 256 in
+// its last a.fa.nkv blocks (one per KV head, head dim FAHD, FAG query heads
+// per KV head); the matvec blocks are the others and run a.mv.nw waves each
+// (the attention runs 8), and the RoPE + K/V epilogue also publishes q and
+// the new K/V rows as tagged words (HexArgs::FusedAttn).
+template <int TB, int LR, int EPI, int FAHD = 0, int FAG = 0>
 __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) hexmv4_kernel(const HexArgs a) {
+    constexpr bool FA = FAHD > 0;
+    if constexpr (FA) {
+        const int nmv = (int)gridDim.x - a.fa.nkv;
+        if ((int)blockIdx.x >= nmv) {
+            using KU32c = const __attribute__((address_space(4))) uint32_t;
+            const unsigned tag = *(KU32c*)a.fa.epoch_dev * 64u + (unsigned)a.rope.layer + 1u;
+            const FaIn fi{a.rope.k_cache, a.rope.v_cache, a.rope.pos_dev, a.fa.words, a.fa.out, a.err,
+                          a.rope.layer, a.rope.max_seq, a.rope.n_kv, a.rope.n_heads, a.fa.sm_scale};
+            attn_fa_block<FAHD, FAG>(fi, (int)blockIdx.x - nmv, tag);
+            return;
+        }
+        if ((int)(threadIdx.x >> 6) >= a.mv.nw) return;
+    }
     // (whole 16-entry slices: every filling wave writes 16 entries, the
     // padding ones from the zero padding of the field table)
     __shared__ __attribute__((aligned(16))) uint32_t stab[TB > 0 ? ((TB + 15) & ~15) * 64 : 1];
@@ -1555,6 +1836,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     // (argument values used right away pass through an asm placed after the
     // batch, so nothing waits for them before the batch is out)
     unsigned bdim = blockDim.x;
+    if constexpr (FA) bdim = (unsigned)a.mv.nw * 64u;
     int cols0 = a.cols, epi0 = a.epilogue;
     int P = a.mv.P, wrl = a.mv.wr_log2, nunits = a.mv.nunits, ub1 = a.mv.ub1, ub2 = a.mv.ub2;
     int units_q = a.mv.units_q, units_r = a.mv.units_r;
@@ -1577,7 +1859,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
         mv4_publish(a, (int)blockIdx.x, scratch);
         return;
     }
-    const int nblk = (int)gridDim.x - nlead;
+    const int nblk = (int)gridDim.x - nlead - (FA ? a.fa.nkv : 0);
 
     // units: paired -> row-block rb of gate and up; else the row-blocks of
     // the segments in order (first units ub1, ub2 of segments 1, 2)
@@ -1648,6 +1930,8 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     // loads, which never wait behind the vector loads of the codes
     using KI32 = const __attribute__((address_space(4))) int;
     const int rpos = epi == kEpiRopeKV ? (a.rope.pos_dev ? *(KI32*)a.rope.pos_dev : a.rope.pos) : 0;
+    // FA: the tag of this launch's words (token counter * 64 + layer + 1)
+    const unsigned fa_tag = FA ? *(KU32*)a.fa.epoch_dev * 64u + (unsigned)a.rope.layer + 1u : 0u;
     uint32_t* X32 = reinterpret_cast<uint32_t*>(dyn + tab_bytes) + (size_t)wid * P * 128;
     const uint4* Xw = reinterpret_cast<const uint4*>(X32);
     // chunks of x per batch of loads (4 when the rank-k rows of three
@@ -2063,16 +2347,29 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                 const RopeKV& r = a.rope;
                 const float partner = __shfl_xor(fin0, 1, 64);
                 const size_t base = ((size_t)r.layer * r.max_seq + (size_t)rpos) * (size_t)r.n_kv * r.hd;
+                const bool odd = (lane & 1) != 0;
+                const float x0 = odd ? partner : fin0, x1 = odd ? fin0 : partner;
+                const float2 cs = lcs[kHasCs ? uk : 0][lane];
+                const float y = g == 2 ? fin0 : (odd ? (x0 * cs.y + x1 * cs.x) : (x0 * cs.x - x1 * cs.y));
                 if (row < s0.rows) {
-                    if (g == 2) {
-                        r.v_cache[base + row] = f2h(fin0);
-                    } else {
-                        const bool odd = (lane & 1) != 0;
-                        const float x0 = odd ? partner : fin0, x1 = odd ? fin0 : partner;
-                        const float2 cs = lcs[kHasCs ? uk : 0][lane];
-                        const float y = odd ? (x0 * cs.y + x1 * cs.x) : (x0 * cs.x - x1 * cs.y);
-                        if (g == 0) s0.out[row] = y;
-                        else r.k_cache[base + row] = f2h(y);
+                    if (g == 2) r.v_cache[base + row] = f2h(y);
+                    else if (g == 0) s0.out[row] = y;
+                    else r.k_cache[base + row] = f2h(y);
+                }
+                if constexpr (FA) {
+                    // the same values for the attention blocks: q rows as
+                    // fp32, K / V rows as the cache's fp16 pairs (rows 2i,
+                    // 2i + 1 in the even lane's word)
+                    const uint32_t hp = (uint32_t)f2h(y) | ((uint32_t)f2h(__shfl_xor(y, 1, 64)) << 16);
+                    const unsigned long long tag = (unsigned long long)fa_tag << 32;
+                    const int qd = r.n_heads * r.hd, kvd = r.n_kv * r.hd;
+                    if (row < s0.rows) {
+                        if (g == 0)
+                            __hip_atomic_store(a.fa.words + row, tag | __float_as_uint(y), __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+                        else if (!odd)
+                            __hip_atomic_store(a.fa.words + qd + (g == 2 ? kvd / 2 : 0) + (row >> 1), tag | hp,
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     }
                 }
             }
@@ -2535,6 +2832,36 @@ hipError_t launch_hexmv4_t(const HexArgs& a0, hipStream_t st, int nw, size_t lds
     return hipGetLastError();
 }
 
+// q/k/v + decode attention (hexmv4_kernel with FAHD > 0): matvec blocks first, then one
+// attention block per KV head, all resident at once (the attention blocks
+// wait for words of matvec blocks); blocks of max(nw, 8) waves (the
+// attention runs 8).  hipErrorNotSupported before any launch when that does
+// not fit.
+template <int TB, int LR, int HD, int G>
+hipError_t launch_qkva_t(const HexArgs& a0, hipStream_t st, int nw, size_t lds, int nunits) {
+    const int nt = (nw > 8 ? nw : 8) * 64;
+    static size_t attr_lds = 0;
+    if (lds > attr_lds) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&hexmv4_kernel<TB, LR, kEpiRopeKV, HD, G>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        attr_lds = lds;
+    }
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, hexmv4_kernel<TB, LR, kEpiRopeKV, HD, G>, nt, lds) != hipSuccess || per_cu < 1)
+        return hipErrorNotSupported;
+    const int ncu = device_cu_count() > 0 ? device_cu_count() : 256;
+    int grid = ncu * per_cu - a0.fa.nkv;   // matvec blocks
+    if (grid > nunits) grid = nunits;
+    if (grid < 1 || grid < (nunits + kMv4PreUnits - 1) / kMv4PreUnits) return hipErrorNotSupported;
+    HexArgs a = a0;
+    a.mv.units_q = nunits / grid;
+    a.mv.units_r = nunits % grid;
+    a.mv.nw = nw;
+    hipLaunchKernelGGL((hexmv4_kernel<TB, LR, kEpiRopeKV, HD, G>), dim3(grid + a.fa.nkv), dim3(nt), lds, st, a);
+    return hipGetLastError();
+}
+
 hipError_t launch_hexmv4(const HexArgs& a, hipStream_t st) {
     if (a.nseg < 1 || a.nseg > kMaxSeg || a.cols <= 0 || a.cols % 64) return hipErrorInvalidValue;
     const int nc = (a.cols + 127) / 128;
@@ -2590,6 +2917,28 @@ hipError_t launch_hexmv4(const HexArgs& a, hipStream_t st) {
     ap.mv.ub1 = (a.seg[0].rows + 15) / 16;
     ap.mv.ub2 = ap.mv.ub1 + (a.nseg > 1 ? (a.seg[1].rows + 15) / 16 : 0);
     const size_t xbytes = (size_t)G * nc * 512;   // every wave's own chunks of x
+    ap.mv.nw = nw;
+    if (a.fa.nkv > 0) {
+        // the q/k/v launch with the decode attention in its last blocks
+        const int gq = a.rope.n_kv > 0 ? a.rope.n_heads / a.rope.n_kv : 0;
+        const int lrm = !lr ? 0 : (inblock && all2 ? 3 : -1);
+        if (a.epilogue != kEpiRopeKV || !shared || !a.norm_w || !a.fa.words || !a.fa.out || !a.fa.epoch_dev ||
+            !a.rope.pos_dev || a.fa.nkv != a.rope.n_kv || gq * a.rope.n_kv != a.rope.n_heads || a.rope.layer < 0 ||
+            a.rope.layer >= 64)
+            return hipErrorNotSupported;
+#define GSD_QA(T, L)                                                                                            \
+    {                                                                                                           \
+        if (a.rope.hd == 128 && gq == 4) return launch_qkva_t<T, L, 128, 4>(ap, st, nw, xbytes, nunits);        \
+        if (a.rope.hd == 64 && gq == 2) return launch_qkva_t<T, L, 64, 2>(ap, st, nw, xbytes, nunits);          \
+        return hipErrorNotSupported;                                                                            \
+    }
+        if (a.seg[0].n_pts == 217 && lrm == 0) GSD_QA(217, 0)
+        if (a.seg[0].n_pts == 217 && lrm == 3) GSD_QA(217, 3)
+        if (a.seg[0].n_pts == 127 && lrm == 0) GSD_QA(127, 0)
+        if (a.seg[0].n_pts == 127 && lrm == 3) GSD_QA(127, 3)
+#undef GSD_QA
+        return hipErrorNotSupported;
+    }
     // the shared-codebook kernels are specialised on the epilogue as well
 #define GSD_MV4(T, E)                                                                           \
     {                                                                                           \
@@ -2865,10 +3214,10 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
 }
 
 hipError_t launch_embed(const uint16_t* embed, const int* token_dev, float* x, int hidden,
-                        unsigned long long* clear, int nclear, hipStream_t st) {
+                        unsigned long long* clear, int nclear, unsigned* epoch, hipStream_t st) {
     const int n = hidden > nclear ? hidden : nclear;
     hipLaunchKernelGGL(embed_kernel, dim3((n + 255) / 256), dim3(256), 0, st, embed, token_dev, x, hidden, clear,
-                       nclear);
+                       nclear, epoch);
     return hipGetLastError();
 }
 

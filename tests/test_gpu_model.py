@@ -211,6 +211,40 @@ def test_decode_across_short_context_switch(engine):
     gpu.close()
 
 
+@pytest.mark.parametrize("mode,shape", [
+    ("precision", dict(kinks_per_row=2)),                                            # head dim 64, 2 heads per KV head
+    ("turbo", dict(n_layers=1, hidden=1024, ffn=1024, n_heads=8, n_kv_heads=2, head_dim=128)),   # 128, 4
+])
+def test_fused_attention_matches_two_launches(mode, shape, monkeypatch):
+    """Positions below 256 run the attention inside the q/k/v launch (its
+    last blocks wait for the q/k/v words of the same launch); with
+    GSD_FUSED_ATTN=0 the model issues the q/k/v launch and the attention
+    launch instead.  Both match the oracle at every position up to 300 (the
+    fused path through 255, the split path after), and each other closely."""
+    banner(f"fused q/k/v + attention vs two launches {mode} {shape}")
+    from gsdlq import synth
+    import run_gpu_native_chat as chat
+    src = synth.SynthSource(_spec(mode=mode, **shape))
+    models = []
+    for fa in ("1", "0"):
+        monkeypatch.setenv("GSD_FUSED_ATTN", fa)
+        models.append(chat.GPUMistralV2Model(src, max_seq_len=512, verbose=False))
+    fused, plain = models
+    ref = O.OracleModel(src, kind="port", max_seq_len=512)
+    toks = np.random.default_rng(7).integers(0, fused.vocab_size, 300).tolist()
+    for pos, t in enumerate(toks):
+        want = pos % 7 == 0 or pos in (63, 64, 127, 128, 255, 256, 299)
+        a = fused.forward_token(t, pos, return_logits=want)
+        b = plain.forward_token(t, pos, return_logits=want)
+        r = ref.forward_token(t, pos, return_logits=want)
+        if want:
+            assert rel_l2(a, r) < 1e-3, pos
+            assert rel_l2(b, r) < 1e-3, pos
+            assert rel_l2(a, b) < 1e-4, pos
+    for m in models:
+        m.close()
+
+
 def test_model_rejects_invalid_codes():
     from gsdlq import synth
     import run_gpu_native_chat as chat
