@@ -2551,6 +2551,154 @@ __global__ void __launch_bounds__(256) batch_prep_kernel(const BatchPrep p) {
     }
 }
 
+// The same preparation for inputs of up to kPrep2MaxCols columns and ranks of
+// at most 2 per segment, in four passes over the token's row instead of one
+// per quantity: the row is read from memory once into LDS (loads in flight
+// together), then normed in place, then all rank-k dot products of the
+// launch are formed in one pass with one block reduction, then the fp16
+// operands are written.  One block of 512 threads per token.
+constexpr int kPrep2MaxCols = 32768;
+__global__ void __launch_bounds__(512) batch_prep2_kernel(const BatchPrep p) {
+    extern __shared__ __attribute__((aligned(16))) float xl[];   // x' of the token [cols]
+    __shared__ float red[8][2 * kMaxSeg + 2];
+    constexpr float kS32 = 0.866025403784438646763723170752936183f;
+    constexpr int NT = 512, NS = 2 * kMaxSeg;
+    const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int nc = (p.cols + 127) >> 7, np = p.cols >> 1, nv4 = p.cols >> 2;
+    const bool valid = m < p.M;
+    const float4* xr4 = reinterpret_cast<const float4*>(p.X + (size_t)(valid ? m : 0) * p.ldx);
+    float4* xl4 = reinterpret_cast<float4*>(xl);
+    auto block_sums = [&](float (&v)[NS + 2], int n) {   // sums over the block of v[0..n)
+        for (int s = 0; s < n; s++) {
+            const float w = wave_sum_valu(v[s]);
+            if (lane == 0) red[wid][s] = w;
+        }
+        __syncthreads();
+        for (int s = 0; s < n; s++) {
+            float t = 0.f;
+            for (int w = 0; w < NT / 64; w++) t += red[w][s];
+            v[s] = t;
+        }
+        __syncthreads();
+    };
+    // 1. the row into LDS, and its sum of squares
+    float ss = 0.f;
+    for (int b = tid; b < nv4; b += 4 * NT) {
+        float4 v[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            v[k] = valid && b + k * NT < nv4 ? xr4[b + k * NT] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            if (b + k * NT < nv4) {
+                xl4[b + k * NT] = v[k];
+                ss = fmaf(v[k].x, v[k].x, ss);
+                ss = fmaf(v[k].y, v[k].y, ss);
+                ss = fmaf(v[k].z, v[k].z, ss);
+                ss = fmaf(v[k].w, v[k].w, ss);
+            }
+        }
+    }
+    float sv[NS + 2];
+    sv[0] = ss;
+    block_sums(sv, 1);
+    const float inv = p.norm_w ? 1.0f / sqrtf(sv[0] / (float)p.cols + p.eps) : 1.f;
+    // 2. x' = (x * inv) * w as the reference forms it, in place; xn; the
+    //    largest |u|, |v| (each thread rewrites only its own float4s)
+    const float4* w4 = reinterpret_cast<const float4*>(p.norm_w);
+    float4* xn4 = reinterpret_cast<float4*>(p.xn + (size_t)m * p.cols);
+    float mx = 0.f;
+    for (int b = tid; b < nv4; b += 4 * NT) {
+        float4 w[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            w[k] = p.norm_w && b + k * NT < nv4 ? w4[b + k * NT] : make_float4(1.f, 1.f, 1.f, 1.f);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            if (b + k * NT < nv4) {
+                float4 x = xl4[b + k * NT];
+                if (p.norm_w) {
+                    x.x = (x.x * inv) * w[k].x;
+                    x.y = (x.y * inv) * w[k].y;
+                    x.z = (x.z * inv) * w[k].z;
+                    x.w = (x.w * inv) * w[k].w;
+                    xl4[b + k * NT] = x;
+                }
+                if (valid) xn4[b + k * NT] = x;
+                mx = fmaxf(mx, fmaxf(fabsf(x.x), fabsf(fmaf(kS32, x.y, 0.5f * x.x))));
+                mx = fmaxf(mx, fmaxf(fabsf(x.z), fabsf(fmaf(kS32, x.w, 0.5f * x.z))));
+            }
+        }
+    }
+    // 3. rank-k terms: slot s = 2 g + j (j < k[g] <= 2), x' . Vt[g][j] over
+    //    the row, Vt read 4 halves per x' float4
+    const uint2* vt[NS];
+    bool act[NS];
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+        act[s] = (s & 1) < p.k[s >> 1];
+        vt[s] = act[s] ? reinterpret_cast<const uint2*>(p.Vt[s >> 1] + (size_t)(s & 1) * p.cols) : nullptr;
+    }
+#pragma unroll
+    for (int s = 0; s < NS; s++) sv[s] = 0.f;
+    sv[NS] = mx;
+    const bool any = act[0] || act[2] || act[4];
+    if (valid && any) {
+        for (int b = tid; b < nv4; b += 2 * NT) {
+            uint2 h[NS][2];
+#pragma unroll
+            for (int s = 0; s < NS; s++)
+#pragma unroll
+                for (int k = 0; k < 2; k++) h[s][k] = act[s] && b + k * NT < nv4 ? vt[s][b + k * NT] : make_uint2(0u, 0u);
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                if (b + k * NT < nv4) {
+                    const float4 x = xl4[b + k * NT];
+#pragma unroll
+                    for (int s = 0; s < NS; s++) {
+                        sv[s] = fmaf(x.x, h2f((uint16_t)(h[s][k].x & 0xFFFFu)), sv[s]);
+                        sv[s] = fmaf(x.y, h2f((uint16_t)(h[s][k].x >> 16)), sv[s]);
+                        sv[s] = fmaf(x.z, h2f((uint16_t)(h[s][k].y & 0xFFFFu)), sv[s]);
+                        sv[s] = fmaf(x.w, h2f((uint16_t)(h[s][k].y >> 16)), sv[s]);
+                    }
+                }
+            }
+        }
+    }
+    // one reduction for the terms (and the max, as a max)
+    {
+        const float w = wave_max_valu(sv[NS]);
+        if (lane == 0) red[wid][NS] = w;
+        block_sums(sv, NS);
+        float t = 0.f;
+        for (int w2 = 0; w2 < NT / 64; w2++) t = fmaxf(t, red[w2][NS]);
+        mx = t;
+    }
+    if (valid && tid < NS && act[tid]) p.tmp[tid >> 1][(size_t)m * p.k[tid >> 1] + (tid & 1)] = sv[tid] * p.S[tid >> 1][tid & 1];
+    // 4. (u, v) of x' as fp16 high and low parts after a power-of-two prescale
+    int ex = 0;
+    if (mx > 0.f && mx < INFINITY) (void)frexpf(mx, &ex);
+    const float up = ldexpf(1.f, 14 - ex);
+    if (tid == 0) p.xs[m] = valid ? ldexpf(1.f, ex - 14) : 0.f;
+    uint32_t* x32 = reinterpret_cast<uint32_t*>(p.xa);
+    const int g16 = m >> 4, ml = m & 15;
+    for (int q = tid; q < nc * 64; q += NT) {
+        float u = 0.f, v = 0.f;
+        if (valid && q < np) {
+            const float2 x2 = reinterpret_cast<const float2*>(xl)[q];
+            u = x2.x * up;
+            v = fmaf(kS32, x2.y, 0.5f * x2.x) * up;
+        }
+        const _Float16 uh = (_Float16)u, vh = (_Float16)v;
+        const _Float16 ul = (_Float16)(u - (float)uh), vl = (_Float16)(v - (float)vh);
+        const int c = q >> 6, h = (q >> 5) & 1, lg = (q >> 3) & 3, t2 = (q >> 2) & 1, e = q & 3;
+        const size_t i0 = ((((size_t)g16 * nc + c) * 8 + h * 2 + t2) * 64 + ml + 16 * lg) * 4 + e;
+        const size_t i1 = i0 + 4 * 64 * 4;   // the low parts: 4 fragments on
+        x32[i0] = (uint32_t)__builtin_bit_cast(uint16_t, uh) | ((uint32_t)__builtin_bit_cast(uint16_t, vh) << 16);
+        x32[i1] = (uint32_t)__builtin_bit_cast(uint16_t, ul) | ((uint32_t)__builtin_bit_cast(uint16_t, vl) << 16);
+    }
+}
+
 __global__ void __launch_bounds__(256) embed_rows_kernel(const uint16_t* embed, const int* tokens, float* X, int hidden) {
     const int m = blockIdx.y, i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < hidden) X[(size_t)m * hidden + i] = h2f(embed[(size_t)tokens[m] * hidden + i]);
@@ -3051,6 +3199,23 @@ hipError_t launch_batch_prep(const BatchPrep& p, hipStream_t st) {
     for (int g = 0; g < kMaxSeg; g++)
         if (p.k[g] < 0 || p.k[g] > kMaxRank || (p.k[g] > 0 && (!p.Vt[g] || !p.S[g] || !p.tmp[g])))
             return hipErrorInvalidValue;
+    // inputs of at most kPrep2MaxCols columns, ranks <= 2, rows 16-byte
+    // aligned: the four-pass kernel (row in LDS)
+    bool fast = p.cols <= kPrep2MaxCols && p.ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(p.X) & 15) == 0 &&
+                (reinterpret_cast<uintptr_t>(p.xn) & 15) == 0 && (!p.norm_w || (reinterpret_cast<uintptr_t>(p.norm_w) & 15) == 0);
+    for (int g = 0; g < kMaxSeg; g++) fast = fast && p.k[g] <= 2 && (p.k[g] == 0 || (reinterpret_cast<uintptr_t>(p.Vt[g]) & 7) == 0);
+    if (fast) {
+        const size_t lds = (size_t)p.cols * 4;
+        static size_t attr = 0;
+        if (lds > attr) {
+            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&batch_prep2_kernel),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return e;
+            attr = lds;
+        }
+        hipLaunchKernelGGL(batch_prep2_kernel, dim3(((p.M + 15) / 16) * 16), dim3(512), lds, st, p);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(batch_prep_kernel, dim3(((p.M + 15) / 16) * 16), dim3(256), 0, st, p);
     return hipGetLastError();
 }
