@@ -2463,6 +2463,67 @@ __global__ void __launch_bounds__(256) hexmm_xprep_kernel(const uint16_t* X, int
     }
 }
 
+// The same operands for rows of at most 16384 columns from one pass: each
+// thread loads its 8-column groups of the row (one 16-byte load each, all in
+// flight together), the block finds the largest |u|, |v|, and each group's
+// four pairs go out as one 16-byte store.
+__global__ void __launch_bounds__(512) hexmm_xprep2_kernel(const uint16_t* X, int M, int cols, uint4* xa, float* xs) {
+    __shared__ float red[8];
+    constexpr float kS32 = 0.866025403784438646763723170752936183f;
+    const int m = blockIdx.x, tid = threadIdx.x, wid = tid >> 6;
+    const int nc = (cols + 127) >> 7, ng8 = cols >> 3;   // 8-column groups (4 pairs)
+    const bool valid = m < M;
+    const uint4* xr = reinterpret_cast<const uint4*>(X + (size_t)(valid ? m : 0) * cols);
+    uint4 v[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int i = tid + 512 * k;
+        v[k] = valid && i < ng8 ? xr[i] : make_uint4(0u, 0u, 0u, 0u);
+    }
+    auto pair = [](uint32_t w, float& xa_, float& xb_) {
+        xa_ = bf2f((uint16_t)(w & 0xFFFFu));
+        xb_ = bf2f((uint16_t)(w >> 16));
+    };
+    float mx = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint32_t w4[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float xa_, xb_;
+            pair(w4[e], xa_, xb_);
+            mx = fmaxf(mx, fmaxf(fabsf(xa_), fabsf(fmaf(kS32, xb_, 0.5f * xa_))));
+        }
+    }
+    mx = wave_max(mx);
+    if ((tid & 63) == 0) red[wid] = mx;
+    __syncthreads();
+    mx = red[0];
+#pragma unroll
+    for (int w = 1; w < 8; w++) mx = fmaxf(mx, red[w]);
+    int ex = 0;
+    if (mx > 0.f && mx < INFINITY) (void)frexpf(mx, &ex);
+    const float up = ldexpf(1.f, 14 - ex);
+    if (tid == 0) xs[m] = valid ? ldexpf(1.f, ex - 14) : 0.f;
+    const int g16 = m >> 4, ml = m & 15;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int i = tid + 512 * k;   // pairs 4 i .. 4 i + 3 (zeros past the row: chunk padding)
+        if (i >= nc * 16) continue;
+        const int q0 = 4 * i, c = q0 >> 6, h = (q0 >> 5) & 1, lg = (q0 >> 3) & 3, t2 = (q0 >> 2) & 1;
+        const uint32_t w4[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float xa_, xb_;
+            pair(w4[e], xa_, xb_);
+            const float u = xa_ * up, vv = fmaf(kS32, xb_, 0.5f * xa_) * up;
+            o[e] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)u) | ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)vv) << 16);
+        }
+        xa[(((size_t)g16 * nc + c) * 4 + h * 2 + t2) * 64 + ml + 16 * lg] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+}
+
 __global__ void __launch_bounds__(256) lowrank_batched_kernel(const uint16_t* X, const uint16_t* Vt, const float* S,
                                                              float* tmp, int k, int cols) {
     __shared__ float scratch[16];
@@ -3231,8 +3292,12 @@ hipError_t launch_hexmm(const MatmulArgs& a, hipStream_t st) {
     if (a.M <= 0 || a.cols <= 0 || a.cols % 64 || !a.w.codes_t || !a.w.scales_t || !a.w.fields) return hipErrorInvalidValue;
     if (a.nsplit < 1 || (a.nsplit > 1 && !a.part)) return hipErrorInvalidValue;
     if (a.w.k > 0 && (!a.tmp_k || !a.w.U)) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(hexmm_xprep_kernel, dim3(((a.M + 15) / 16) * 16), dim3(256), 0, st, a.X, a.M, a.cols, a.xa,
-                       a.xs);
+    if (a.cols <= 16384 && (reinterpret_cast<uintptr_t>(a.X) & 15) == 0)
+        hipLaunchKernelGGL(hexmm_xprep2_kernel, dim3(((a.M + 15) / 16) * 16), dim3(512), 0, st, a.X, a.M, a.cols, a.xa,
+                           a.xs);
+    else
+        hipLaunchKernelGGL(hexmm_xprep_kernel, dim3(((a.M + 15) / 16) * 16), dim3(256), 0, st, a.X, a.M, a.cols, a.xa,
+                           a.xs);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (a.w.n_pts == 217) return launch_hexmm_tb<217>(a, st);
