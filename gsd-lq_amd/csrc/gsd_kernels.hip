@@ -2962,8 +2962,18 @@ __global__ void __launch_bounds__(256) hexmm_reduce_kernel(const MatmulArgs a) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= (size_t)a.M * rows) return;
     const int m = (int)(i / rows), row = (int)(i % rows);
+    // the partials of 8 splits at a time in flight, summed in split order
+    const size_t stride = (size_t)ng * 16 * rows;
+    const float* pp = a.part + (size_t)m * rows + row;
     float s = 0.f;
-    for (int k = 0; k < a.nsplit; k++) s += a.part[((size_t)k * ng * 16 + m) * rows + row];
+    for (int k0 = 0; k0 < a.nsplit; k0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = k0 + k < a.nsplit ? pp[(size_t)(k0 + k) * stride] : 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            if (k0 + k < a.nsplit) s += v[k];
+    }
     const float y = hexmm_finish(a, m, row, s);
     a.Y[i] = a.accumulate ? a.Y[i] + y : y;
 }
