@@ -227,6 +227,10 @@ struct AttnArgs {
     // z = grid.z index at position pos + z, q / out rows z * n_heads * hd, its
     // words at ws + z * n_kv * max_splits * group * (2 + hd); needs epoch.
     int ntok;
+    // one-token matrix-core kernel: blocks that merge a KV head's splits
+    // (0 or 1: the last split's; up to 8 when every block of the grid is
+    // resident at once; set by the launcher)
+    int mergers;
 };
 hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
 // RoPE + K/V append at a.pos fused into the one-token attention launch

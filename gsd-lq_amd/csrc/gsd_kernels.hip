@@ -1246,75 +1246,100 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
             __hip_atomic_store(wsb + 1, tag | __float_as_uint(L), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
-    if (split != nsplit - 1) return;
-
-    // merge: out = sum_s f_s o_s / sum_s f_s l_s with f_s = 2^(m_s - max m),
-    // splits in order.  Thread tid reads word (max, sum) item tid = s G + gi
-    // (tid < nsplit G) and, as thread (g, d), the o words of every split;
-    // the loads bypass the non-coherent caches (sc1) and go out together,
-    // again until every word has this launch's epoch (bounded).  Offsets
-    // past the words read 0 (buffer bounds).
+    // merge: out = sum_s f_s o_s / sum_s f_s l_s with f_s = 2^(m_s - max m).
+    // The G HD outputs of the KV head come in slices of 64 (query head
+    // o / HD, dim o % HD); the blocks of the last nm splits merge, block
+    // split nsplit - 1 - r taking slices r, r + nm, ...  With one merger
+    // (a grid that may not be resident at once) it is the last split's
+    // block: blocks start in index order, so every other split's block has
+    // started before it and finishes without it; several mergers wait on
+    // blocks after their own, so the host allows them only when every block
+    // of the grid fits on the device at once.
+    constexpr int NSL = G * HD / 64;
+    const int nm = min(nsplit, min(max(a.mergers, 1), NSL));
+    const int r = nsplit - 1 - split;
+    if (r >= nm) return;
+    // Thread (wave w, lane l): output l of the slice over splits w, w + 8,
+    // w + 16, w + 24; its o, max and sum words (the latter two
+    // the same address across the wave) loaded together, bypassing the
+    // non-coherent caches (sc1), again until every word of a split below
+    // nsplit has this launch's epoch (bounded).  Offsets past the words
+    // read 0 (buffer bounds).  Then (max, sum, o) of the wave's splits,
+    // and the 8 waves' combined by wave 0 through LDS, in a fixed order.
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc(wsk, (short)0, nsplit * G * WPH * 8, 0x00020000);
-    const int c = nsplit * G, gi = tid % G;
-    const int vm = tid < c ? tid * WPH * 8 : 0x7FFFFFF0;     // (max, sum) words of item tid
-    const int vo = own ? (g * WPH + 2 + d) * 8 : 0x7FFFFFF0;  // o word of (0, g, d); the split in soffset
-    unsigned long long wm0 = 0, wl0 = 0, ov[kAttnDecSplits];
-    for (int spins = 0;; spins++) {
-        auto w2 = __builtin_amdgcn_raw_buffer_load_b64(rs, vm, 0, 16 /* sc1 */);
-        wm0 = ((unsigned long long)w2[1] << 32) | w2[0];
-        w2 = __builtin_amdgcn_raw_buffer_load_b64(rs, vm, 8, 16);
-        wl0 = ((unsigned long long)w2[1] << 32) | w2[0];
+    constexpr int KS = kAttnDecSplits / NW;   // splits per wave
+    float* mlo = reinterpret_cast<float*>(&vs[0][0]);   // [3][NW][64]
+    lds_barrier();   // (every wave is past its reads of vs above)
+    for (int sl = r; sl < NSL; sl += nm) {
+        const int o = sl * 64 + lane, g2 = o / HD, d2 = o % HD;
+        int vo[KS], vml[KS];
 #pragma unroll
-        for (int kk = 0; kk < kAttnDecSplits; kk++) {
-            const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, vo, kk * G * WPH * 8, 16);
-            ov[kk] = ((unsigned long long)v[1] << 32) | v[0];
+        for (int k = 0; k < KS; k++) {
+            const int s = wid + NW * k;
+            vml[k] = s < nsplit ? (s * G + g2) * WPH * 8 : 0x7FFFFFF0;
+            vo[k] = s < nsplit ? vml[k] + (2 + d2) * 8 : 0x7FFFFFF0;
         }
-        // words past the splits read 0; all are this launch's when exactly
-        // those differ from the epoch
-        int differ = 0;
+        unsigned long long wo[KS], wmx[KS], wsm[KS];
+        for (int spins = 0;; spins++) {
 #pragma unroll
-        for (int kk = 0; kk < kAttnDecSplits; kk++) differ += (unsigned)(ov[kk] >> 32) != ep;
-        const bool done = (!own || differ == kAttnDecSplits - nsplit) &&
-                          (tid >= c || ((unsigned)(wm0 >> 32) == ep && (unsigned)(wl0 >> 32) == ep));
-        if (done) break;
-        if (spins == (1 << 16)) {
-            if (a.err) *a.err = 1u;
-            break;
+            for (int k = 0; k < KS; k++) {
+                auto w2 = __builtin_amdgcn_raw_buffer_load_b64(rs, vo[k], 0, 16 /* sc1 */);
+                wo[k] = ((unsigned long long)w2[1] << 32) | w2[0];
+                w2 = __builtin_amdgcn_raw_buffer_load_b64(rs, vml[k], 0, 16);
+                wmx[k] = ((unsigned long long)w2[1] << 32) | w2[0];
+                w2 = __builtin_amdgcn_raw_buffer_load_b64(rs, vml[k], 8, 16);
+                wsm[k] = ((unsigned long long)w2[1] << 32) | w2[0];
+            }
+            bool done = true;
+#pragma unroll
+            for (int k = 0; k < KS; k++)
+                done = done && (wid + NW * k >= nsplit ||
+                                ((unsigned)(wo[k] >> 32) == ep && (unsigned)(wmx[k] >> 32) == ep &&
+                                 (unsigned)(wsm[k] >> 32) == ep));
+            if (done) break;
+            if (spins == (1 << 16)) {
+                if (a.err) *a.err = 1u;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
         }
-        __builtin_amdgcn_s_sleep(2);
-    }
-    // every split's block has read the counter: the next launch's epoch base (stream order)
-    if (tid == 0 && !a.epoch) a.counters[kvh] = ep;
-    const float m0 = tid < c ? __uint_as_float((unsigned)wm0) : -INFINITY, l0 = __uint_as_float((unsigned)wl0);
-    // max over the splits of head gi: lanes gi, gi + G, ... of each wave,
-    // then the waves (lanes 0..G-1 publish); weights f_s and f_s l_s by item
-    float mg = m0;
+        float mp = -INFINITY, lp = 0.f, op = 0.f;
 #pragma unroll
-    for (int x = G; x < 64; x <<= 1) mg = fmaxf(mg, __shfl_xor(mg, x, 64));
-    float* red = reinterpret_cast<float*>(&vs[0][0]);                 // [NW][G] wave maxima
-    float2* fw = reinterpret_cast<float2*>(&vs[0][0] + 2 * NW * 4);   // [s][g] (f_s, f_s l_s)
-    if (lane < G) red[wid * G + lane] = mg;
-    lds_barrier();
-    {
-        float Mi = red[gi];
+        for (int k = 0; k < KS; k++)
+            if (wid + NW * k < nsplit) mp = fmaxf(mp, __uint_as_float((unsigned)wmx[k]));
 #pragma unroll
-        for (int w = 1; w < NW; w++) Mi = fmaxf(Mi, red[w * G + gi]);
-        const float f0 = __builtin_amdgcn_exp2f(m0 - Mi);
-        if (tid < kAttnDecSplits * G) fw[tid] = tid < c ? make_float2(f0, f0 * l0) : make_float2(0.f, 0.f);
-    }
-    lds_barrier();
-    if (!own) return;
-    L = 0.f;
-    O = 0.f;
+        for (int k = 0; k < KS; k++)
+            if (wid + NW * k < nsplit) {
+                const float f = __builtin_amdgcn_exp2f(__uint_as_float((unsigned)wmx[k]) - mp);
+                lp = fmaf(f, __uint_as_float((unsigned)wsm[k]), lp);
+                op = fmaf(f, __uint_as_float((unsigned)wo[k]), op);
+            }
+        mlo[(0 * NW + wid) * 64 + lane] = mp;
+        mlo[(1 * NW + wid) * 64 + lane] = lp;
+        mlo[(2 * NW + wid) * 64 + lane] = op;
+        lds_barrier();
+        if (wid == 0) {
+            float M2 = mlo[lane];
 #pragma unroll
-    for (int kk = 0; kk < kAttnDecSplits; kk++) {
-        const float2 f = fw[kk * G + g];
-        L += f.y;
-        O = fmaf(f.x, __uint_as_float((unsigned)ov[kk]), O);
+            for (int w = 1; w < NW; w++) M2 = fmaxf(M2, mlo[w * 64 + lane]);
+            float L2 = 0.f, O2 = 0.f;
+#pragma unroll
+            for (int w = 0; w < NW; w++) {
+                const float f = __builtin_amdgcn_exp2f(mlo[w * 64 + lane] - M2);   // (-inf: no split, 0)
+                L2 = fmaf(f, mlo[(NW + w) * 64 + lane], L2);
+                O2 = fmaf(f, mlo[(2 * NW + w) * 64 + lane], O2);
+            }
+            a.out[(size_t)(kvh * G + g2) * HD + d2] = O2 / L2;
+        }
+        lds_barrier();
     }
-    *outp = O / L;
-    write_q();
+    // (the last split's block) every split's block has read the counter
+    // and q: the next launch's epoch base (stream order), q written back
+    if (r == 0) {
+        if (tid == 0 && !a.epoch) a.counters[kvh] = ep;
+        write_q();
+    }
 }
 
 template <int HD, int G, int PW>
@@ -3370,6 +3395,14 @@ hipError_t launch_rope_kv(float* q, const float* k, const float* v, const RopeKV
     return hipGetLastError();
 }
 
+// Mergers of the one-token matrix-core attention: 8 when all `blocks`
+// blocks (one 512-thread block fits on a CU with room to spare) are
+// resident at once on this device, else 1 (the last split's block)
+static int attn_mergers(int blocks) {
+    const int ncu = device_cu_count();
+    return ncu > 0 && blocks <= ncu ? 8 : 1;
+}
+
 hipError_t launch_rope_attention(const AttnArgs& a, const float* k, const float* v, int interleaved,
                                  const float2* cs, hipStream_t st) {
     const int G = a.n_kv > 0 ? a.n_heads / a.n_kv : 0;
@@ -3382,11 +3415,13 @@ hipError_t launch_rope_attention(const AttnArgs& a, const float* k, const float*
     r.interleaved = interleaved;
     for (int i = 0; i < a.hd / 2; i++) r.cs[i] = cs[i];
     const dim3 grid(a.n_kv, a.max_splits);
+    AttnArgs b = a;
+    b.mergers = attn_mergers(a.n_kv * a.max_splits);
 #define GSD_ATTN_R(HD, GG)                                                                                  \
     switch (a.chunk) {                                                                                      \
-        case 64: hipLaunchKernelGGL((attn_rope_kernel<HD, GG, 8>), grid, dim3(512), 0, st, a, r); break;   \
-        case 128: hipLaunchKernelGGL((attn_rope_kernel<HD, GG, 16>), grid, dim3(512), 0, st, a, r); break; \
-        default: hipLaunchKernelGGL((attn_rope_kernel<HD, GG, 32>), grid, dim3(512), 0, st, a, r); break;  \
+        case 64: hipLaunchKernelGGL((attn_rope_kernel<HD, GG, 8>), grid, dim3(512), 0, st, b, r); break;   \
+        case 128: hipLaunchKernelGGL((attn_rope_kernel<HD, GG, 16>), grid, dim3(512), 0, st, b, r); break; \
+        default: hipLaunchKernelGGL((attn_rope_kernel<HD, GG, 32>), grid, dim3(512), 0, st, b, r); break;  \
     }
     if (a.hd == 64) {
         if (G == 1) GSD_ATTN_R(64, 1) else if (G == 2) GSD_ATTN_R(64, 2) else GSD_ATTN_R(64, 4)
@@ -3413,11 +3448,13 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
     if (nt == 1 && (G == 1 || G == 2 || G == 4) && (a.hd == 64 || a.hd == 128) &&
         (a.chunk == 64 || a.chunk == 128 || a.chunk == 256) && a.max_splits <= kAttnDecSplits) {
         const dim3 grid(a.n_kv, a.max_splits);
+        AttnArgs b = a;
+        b.mergers = attn_mergers(a.n_kv * a.max_splits);
 #define GSD_ATTN_P(HD, GG)                                                                            \
     switch (a.chunk) {                                                                                \
-        case 64: hipLaunchKernelGGL((attn_dec_kernel<HD, GG, 8>), grid, dim3(512), 0, st, a); break;   \
-        case 128: hipLaunchKernelGGL((attn_dec_kernel<HD, GG, 16>), grid, dim3(512), 0, st, a); break; \
-        default: hipLaunchKernelGGL((attn_dec_kernel<HD, GG, 32>), grid, dim3(512), 0, st, a); break;  \
+        case 64: hipLaunchKernelGGL((attn_dec_kernel<HD, GG, 8>), grid, dim3(512), 0, st, b); break;   \
+        case 128: hipLaunchKernelGGL((attn_dec_kernel<HD, GG, 16>), grid, dim3(512), 0, st, b); break; \
+        default: hipLaunchKernelGGL((attn_dec_kernel<HD, GG, 32>), grid, dim3(512), 0, st, b); break;  \
     }
 #define GSD_ATTN_D(HD, GG) GSD_ATTN_P(HD, GG)
         if (a.hd == 64) {
