@@ -2807,8 +2807,14 @@ template <int TB, int TG, int RBW, bool HL>
 __global__ void __launch_bounds__(512) hexmm_kernel(const MatmulArgs a) {
     constexpr int W = 8;
     constexpr int FPG = HL ? 8 : 4;   // A fragments per token group and chunk
+    constexpr int AF = TG * FPG * 64;   // the block's A fragments of one chunk (uint4)
+    // two A buffers (one barrier per chunk) for the smaller token tiles (a
+    // thread's share of A at most 2 fragments), when they fit beside the
+    // codebook; the 8-group tiles measured faster with one buffer and the
+    // A fragments one chunk ahead
+    constexpr int NAB = (AF + 511) / 512 <= 2 && 2 * AF * 16 + (TB > 0 ? TB * 256 : 0) <= 160 * 1024 ? 2 : 1;
     __shared__ __attribute__((aligned(16))) uint32_t stab[TB > 0 ? TB * 64 : 1];
-    __shared__ uint4 As[TG * FPG * 64];
+    __shared__ uint4 As[NAB][AF];
     extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int nc = (a.cols + 127) >> 7;
@@ -2841,23 +2847,30 @@ __global__ void __launch_bounds__(512) hexmm_kernel(const MatmulArgs a) {
         }
     };
     // this thread's share of the block's A fragments for chunk c
-    constexpr int APT = (TG * FPG * 64 + 511) / 512;
+    constexpr int APT = (AF + 511) / 512;
     auto aload = [&](int c, uint4 (&av)[APT]) {
         c = min(c, nc - 1);
 #pragma unroll
         for (int i = 0; i < APT; i++) {
             const int j = tid + i * 512;
             const int tg = j / (FPG * 64), g = min(g0 + tg, ng - 1);
-            av[i] = j < TG * FPG * 64 ? a.xa[((size_t)g * nc + c) * (FPG * 64) + (j % (FPG * 64))]
-                                      : make_uint4(0u, 0u, 0u, 0u);
+            av[i] = j < AF ? a.xa[((size_t)g * nc + c) * (FPG * 64) + (j % (FPG * 64))] : make_uint4(0u, 0u, 0u, 0u);
         }
     };
-    uint4 av[APT];
-    aload(c0, av);
-    uint4 cA[RBW], cB[RBW];
-    uint32_t sA[RBW], sB[RBW];
-    load(c0, cA, sA);
-    load(c0 + 1, cB, sB);
+    // D chunks in flight (A fragments and codes, a ring indexed by the
+    // unrolled position): with few MFMAs per chunk a load issued one chunk
+    // ahead would leave its whole latency exposed at every chunk
+    // (the A fragments one chunk ahead when a thread holds 4 or more)
+    constexpr int D = APT <= 1 && RBW <= 1 ? 4 : (APT <= 2 ? 3 : 2);
+    constexpr int DA = APT >= 4 ? 1 : D;
+    uint4 av[DA][APT];
+    uint4 cw[D][RBW];
+    uint32_t sw[D][RBW];
+#pragma unroll
+    for (int i = 0; i < D; i++) {
+        if (i < DA) aload(c0 + i, av[i < DA ? i : 0]);
+        load(c0 + i, cw[i], sw[i]);
+    }
 
     // codebook: entry e of lane l at byte e * 256 + l * 4
     const int n_pts = a.w.n_pts;
@@ -2875,7 +2888,7 @@ __global__ void __launch_bounds__(512) hexmm_kernel(const MatmulArgs a) {
     // the shared-codebook kernels decode their one tile format directly; the
     // generic one turns 7-bit words into u8 words first (one decode path)
     constexpr bool B7 = TB > 0 && TB <= 128;
-    auto compute = [&](const uint4 (&cw)[RBW], const uint32_t (&sw)[RBW]) {
+    auto compute = [&](const uint4 (&cw)[RBW], const uint32_t (&sw)[RBW], const uint4* Ab) {
         uint32_t w4[RBW][4];
 #pragma unroll
         for (int r = 0; r < RBW; r++) {
@@ -2912,7 +2925,7 @@ __global__ void __launch_bounds__(512) hexmm_kernel(const MatmulArgs a) {
                 for (int g = 0; g < TG; g++) {
 #pragma unroll
                     for (int hl = 0; hl < (HL ? 2 : 1); hl++) {   // high part, then low part
-                        const uint4 xv = As[(g * FPG + hl * 4 + h * 2 + t) * 64 + lane];
+                        const uint4 xv = Ab[(g * FPG + hl * 4 + h * 2 + t) * 64 + lane];
                         u32x4v aw;
                         aw[0] = xv.x; aw[1] = xv.y; aw[2] = xv.z; aw[3] = xv.w;
 #pragma unroll
@@ -2934,26 +2947,28 @@ __global__ void __launch_bounds__(512) hexmm_kernel(const MatmulArgs a) {
         }
     };
 
-    // chunks in pairs (codes A / B alternate); the A fragments of chunk c go
-    // to LDS between two barriers, those of c + 1 are already in flight
-    for (int c = c0; c < c1; c += 2) {
-        lds_barrier();
+    // chunk c: its A fragments go from registers to LDS buffer c % NAB (and
+    // the registers reload chunk c + DA), a barrier, the MFMAs; then its
+    // code slot reloads chunk c + D (clamped past the end: in bounds,
+    // unused).  With two buffers one barrier per
+    // chunk suffices: a wave stores buffer b for chunk c + 2 only after the
+    // barrier of chunk c + 1, which every wave reaches after its reads of b
+    // for chunk c.
+    for (int c = c0; c < c1; c += D) {
 #pragma unroll
-        for (int i = 0; i < APT; i++)
-            if (tid + i * 512 < TG * FPG * 64) As[tid + i * 512] = av[i];
-        aload(c + 1, av);
-        lds_barrier();
-        compute(cA, sA);
-        load(c + 2, cA, sA);
-        if (c + 1 < c1) {
-            lds_barrier();
+        for (int i = 0; i < D; i++) {
+            if (c + i < c1) {
+                uint4* Ab = As[NAB == 2 ? (c - c0 + i) & 1 : 0];   // (by chunk parity: D may be odd)
+                if (NAB == 1) lds_barrier();
+                const int ia = DA == 1 ? 0 : i;
 #pragma unroll
-            for (int i = 0; i < APT; i++)
-                if (tid + i * 512 < TG * FPG * 64) As[tid + i * 512] = av[i];
-            aload(c + 2, av);
-            lds_barrier();
-            compute(cB, sB);
-            load(c + 3, cB, sB);
+                for (int k = 0; k < APT; k++)
+                    if (tid + k * 512 < AF) Ab[tid + k * 512] = av[ia][k];
+                aload(c + i + DA, av[ia]);
+                lds_barrier();
+                compute(cw[i], sw[i], Ab);
+                load(c + i + D, cw[i], sw[i]);
+            }
         }
     }
 
