@@ -903,8 +903,12 @@ struct AttnRope {
     float2 cs[64];   // head dim <= 128
 };
 
-template <int HD, int G, int PW, bool ROPE>
+// RP: 0 no RoPE; 1 / 2 RoPE + append in front with the interleaved /
+// rotate-half pairing (a template parameter: the pairing then costs no
+// selects in the rotation code, which every block runs once)
+template <int HD, int G, int PW, int RP>
 __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope* rp) {
+    constexpr bool ROPE = RP > 0, IL = RP == 1;
     constexpr int NW = 8;                 // waves; PW positions each (8, 16 or 32)
     constexpr int NGRP = (PW + 15) / 16;  // groups of 16 positions (matrix-core steps)
     constexpr int NJ = HD / 32;           // matrix-core steps per 16 positions
@@ -1021,11 +1025,10 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
         // elements 2i and 2i + 1 of a step; rotate-half, element e of steps
         // j and j + NJ / 2.
 #pragma clang fp contract(off)
-        // every element from the original values, the pairing by selects
-        // (no array indexed at run time): interleaved, partner e ^ 1 of
-        // step j, first of the pair when e is even; rotate-half, element e
-        // of step j ^ NJ / 2, first when j < NJ / 2
-        const bool il = rp->interleaved != 0;
+        // every element from the original values (no array indexed at run
+        // time): interleaved, partner e ^ 1 of step j, first of the pair
+        // when e is even; rotate-half, element e of step j ^ NJ / 2, first
+        // when j < NJ / 2
         if (lane < HD / 2) {
             rcs[wid][lane] = rin[0];
             reinterpret_cast<float2*>(&rkv[wid][0])[lane] = rin[1];
@@ -1038,9 +1041,9 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
                     const float x = f[j][e];
-                    const float pr = il ? f[j][e ^ 1] : f[j ^ (NJ / 2)][e];
-                    const bool first = il ? (e & 1) == 0 : j < NJ / 2;
-                    const int ci = il ? (32 * j + 8 * kg + e) >> 1 : 32 * (j % (NJ / 2)) + 8 * kg + e;
+                    const float pr = IL ? f[j][e ^ 1] : f[j ^ (NJ / 2)][e];
+                    const bool first = IL ? (e & 1) == 0 : j < NJ / 2;
+                    const int ci = IL ? (32 * j + 8 * kg + e) >> 1 : 32 * (j % (NJ / 2)) + 8 * kg + e;
                     const float2 cs = rcs[wid][ci];
                     o[j][e] = first ? x * cs.x - pr * cs.y : pr * cs.y + x * cs.x;
                 }
@@ -1344,11 +1347,11 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
 
 template <int HD, int G, int PW>
 __global__ void __launch_bounds__(512) attn_dec_kernel(const AttnArgs a) {
-    attn_dec_body<HD, G, PW, false>(a, nullptr);
+    attn_dec_body<HD, G, PW, 0>(a, nullptr);
 }
-template <int HD, int G, int PW>
+template <int HD, int G, int PW, bool IL>
 __global__ void __launch_bounds__(512) attn_rope_kernel(const AttnArgs a, const AttnRope r) {
-    attn_dec_body<HD, G, PW, true>(a, &r);
+    attn_dec_body<HD, G, PW, IL ? 1 : 2>(a, &r);
 }
 
 __global__ void embed_kernel(const uint16_t* embed, const int* token, float* x, int hidden,
@@ -3432,18 +3435,21 @@ hipError_t launch_rope_attention(const AttnArgs& a, const float* k, const float*
     const dim3 grid(a.n_kv, a.max_splits);
     AttnArgs b = a;
     b.mergers = attn_mergers(a.n_kv * a.max_splits);
-#define GSD_ATTN_R(HD, GG)                                                                                  \
-    switch (a.chunk) {                                                                                      \
-        case 64: hipLaunchKernelGGL((attn_rope_kernel<HD, GG, 8>), grid, dim3(512), 0, st, b, r); break;   \
-        case 128: hipLaunchKernelGGL((attn_rope_kernel<HD, GG, 16>), grid, dim3(512), 0, st, b, r); break; \
-        default: hipLaunchKernelGGL((attn_rope_kernel<HD, GG, 32>), grid, dim3(512), 0, st, b, r); break;  \
+#define GSD_ATTN_RI(HD, GG, IL)                                                                                 \
+    switch (a.chunk) {                                                                                          \
+        case 64: hipLaunchKernelGGL((attn_rope_kernel<HD, GG, 8, IL>), grid, dim3(512), 0, st, b, r); break;   \
+        case 128: hipLaunchKernelGGL((attn_rope_kernel<HD, GG, 16, IL>), grid, dim3(512), 0, st, b, r); break; \
+        default: hipLaunchKernelGGL((attn_rope_kernel<HD, GG, 32, IL>), grid, dim3(512), 0, st, b, r); break;  \
     }
+#define GSD_ATTN_R(HD, GG) \
+    if (interleaved) { GSD_ATTN_RI(HD, GG, true) } else { GSD_ATTN_RI(HD, GG, false) }
     if (a.hd == 64) {
         if (G == 1) GSD_ATTN_R(64, 1) else if (G == 2) GSD_ATTN_R(64, 2) else GSD_ATTN_R(64, 4)
     } else {
         if (G == 1) GSD_ATTN_R(128, 1) else if (G == 2) GSD_ATTN_R(128, 2) else GSD_ATTN_R(128, 4)
     }
 #undef GSD_ATTN_R
+#undef GSD_ATTN_RI
     return hipGetLastError();
 }
 
