@@ -925,9 +925,11 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
     __shared__ __attribute__((aligned(16))) uint16_t vs[NW][32 * HD];
     __shared__ __attribute__((aligned(16))) float es[NW][32][4];   // e[p][g] of the wave's positions
     __shared__ float wm[NW][4], wl[NW][4];
-    // ROPE: each wave's copy of (cos, sin) of pos and of the new K and V rows
-    __shared__ __attribute__((aligned(16))) float2 rcs[ROPE ? NW : 1][ROPE ? HD / 2 : 1];
-    __shared__ __attribute__((aligned(16))) float rkv[ROPE ? NW : 1][ROPE ? 2 * HD : 1];
+    // ROPE: each wave's copy of the group's rotated q rows and of the new K
+    // (rotated) and V rows as the cache's fp16
+    __shared__ __attribute__((aligned(16))) float rq[ROPE ? NW : 1][ROPE ? G * HD : 1];
+    __shared__ __attribute__((aligned(16))) uint16_t rkh[ROPE ? NW : 1][ROPE ? HD : 1];
+    __shared__ __attribute__((aligned(16))) uint16_t rvh[ROPE ? NW : 1][ROPE ? HD : 1];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -957,22 +959,32 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
     // q (A operand source): lane l, head m = l & 15 (m < G), dims
     // 32 j + 8 (l >> 4) .. + 7; issued first, the K and V rows behind it
     const int m = lane & 15, kg = lane >> 4;
-    // ROPE: (cos, sin) pairs and the new rows, one 8-byte load per lane and
-    // table, first of all (into this wave's LDS once they land)
-    float2 rin[3];
+    // ROPE: rotation pairs one per lane and step, first of all: lane l takes
+    // pair i = l % (HD / 2) (dims 2i, 2i + 1 interleaved, i and i + HD / 2
+    // rotate-half) of the new K row, its V dims 2i, 2i + 1 (lanes < HD / 2),
+    // the cos / sin of pair i, and pairs l + 64 k of the group's q rows
+    // (query head P / (HD / 2) for pair index P)
+    constexpr int NPQ = G * HD / 2, KQ = (NPQ + 63) / 64;
+    const int ri = lane % (HD / 2), d0 = IL ? 2 * ri : ri, d1 = IL ? 2 * ri + 1 : ri + HD / 2;
+    float2 rcs_ = make_float2(1.f, 0.f), rk = make_float2(0.f, 0.f), rv = make_float2(0.f, 0.f);
+    float2 rqv[ROPE ? KQ : 1];
     if constexpr (ROPE) {
+        rcs_ = rp->cs[ri];
+        const float* kn = rp->k + (size_t)kvh * HD;
+        rk = make_float2(kn[d0], kn[d1]);
+        rv = reinterpret_cast<const float2*>(rp->v + (size_t)kvh * HD)[ri];
 #pragma unroll
-        for (int t = 0; t < 3; t++) {
-            const int i = lane < HD / 2 ? lane : 0;
-            rin[t] = t == 0 ? rp->cs[i]
-                            : reinterpret_cast<const float2*>((t == 1 ? rp->k : rp->v) + (size_t)kvh * HD)[i];
+        for (int k = 0; k < KQ; k++) {
+            const int P = min(lane + 64 * k, NPQ - 1);
+            const float* qg = a.q + (size_t)(kvh * G + P / (HD / 2)) * HD;
+            rqv[k] = make_float2(qg[d0], qg[d1]);
         }
     }
     float4 qa[NJ][2];
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
         qa[j][0] = qa[j][1] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (m < G) {
+        if (!ROPE && m < G) {
             const float4* qp = reinterpret_cast<const float4*>(a.q + (size_t)(kvh * G + m) * HD + 32 * j + 8 * kg);
             qa[j][0] = qp[0];
             qa[j][1] = qp[1];
@@ -1001,105 +1013,80 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
     const int t1 = min(n, t0 + a.chunk);   // the block's positions: t0 .. t1 - 1
     const int te = min(t1, pw0 + PW);      // the wave's: pw0 .. te - 1
 
-    // ROPE: the rotated q rows of the group, written back in place (wave 0)
-    // once every block of the KV head has read q: by the only block, or by
-    // the merging block after every split's words have arrived
-    float4 qkeep[ROPE ? NJ : 1][2];
+    // ROPE: the rotated q rows of the group, written back in place from
+    // wave 0's copy once every block of the KV head has read q: by the only
+    // block, or by the merging block after every split's words have arrived
     auto write_q = [&]() {
-        if (ROPE && wid == 0 && m < G) {
-#pragma unroll
-            for (int j = 0; j < (ROPE ? NJ : 1); j++) {
-                float4* qp = reinterpret_cast<float4*>(const_cast<float*>(a.q) + (size_t)(kvh * G + m) * HD + 32 * j + 8 * kg);
-                qp[0] = qkeep[j][0];
-                qp[1] = qkeep[j][1];
-            }
+        if (ROPE && wid == 0) {
+            float* qg = const_cast<float*>(a.q) + (size_t)kvh * G * HD;
+            for (int o = lane * 4; o < G * HD; o += 256)
+                *reinterpret_cast<float4*>(qg + o) = *reinterpret_cast<const float4*>(&rq[0][o]);
         }
     };
     if constexpr (ROPE) {
-        // RoPE (gsd_lq_cpu_engine.c:213-256) in registers, evaluated without
-        // contraction like the reference: q's rows of the group (every block
-        // of the KV head rotates its own copy),
-        // and the new K row, which the lanes holding position pos put in
-        // place of the row they loaded and store to the cache with V's row.
-        // A lane's dims pair with dims in its own registers: interleaved,
-        // elements 2i and 2i + 1 of a step; rotate-half, element e of steps
-        // j and j + NJ / 2.
+        // RoPE (gsd_lq_cpu_engine.c:213-256), one pair per lane, evaluated
+        // without contraction like the reference (the bits of
+        // rope_kv_kernel's); the rotated q rows and the new fp16 K / V rows
+        // go through the wave's LDS to the lanes that hold them in the
+        // matrix-core layout (the lanes holding position pos put the new
+        // rows in place of the rows they loaded)
 #pragma clang fp contract(off)
-        // every element from the original values (no array indexed at run
-        // time): interleaved, partner e ^ 1 of step j, first of the pair
-        // when e is even; rotate-half, element e of step j ^ NJ / 2, first
-        // when j < NJ / 2
+        auto rot = [&](float2 x) { return make_float2(x.x * rcs_.x - x.y * rcs_.y, x.x * rcs_.y + x.y * rcs_.x); };
+#pragma unroll
+        for (int k = 0; k < KQ; k++) {
+            const int P = lane + 64 * k;
+            if (P < NPQ) {
+                const float2 y = rot(rqv[k]);
+                float* qd = &rq[wid][(P / (HD / 2)) * HD];
+                qd[d0] = y.x;
+                qd[d1] = y.y;
+            }
+        }
         if (lane < HD / 2) {
-            rcs[wid][lane] = rin[0];
-            reinterpret_cast<float2*>(&rkv[wid][0])[lane] = rin[1];
-            reinterpret_cast<float2*>(&rkv[wid][HD])[lane] = rin[2];
-        }
-        auto rope8 = [&](float (&f)[NJ][8]) {
-            float o[NJ][8];
-#pragma unroll
-            for (int j = 0; j < NJ; j++)
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const float x = f[j][e];
-                    const float pr = IL ? f[j][e ^ 1] : f[j ^ (NJ / 2)][e];
-                    const bool first = IL ? (e & 1) == 0 : j < NJ / 2;
-                    const int ci = IL ? (32 * j + 8 * kg + e) >> 1 : 32 * (j % (NJ / 2)) + 8 * kg + e;
-                    const float2 cs = rcs[wid][ci];
-                    o[j][e] = first ? x * cs.x - pr * cs.y : pr * cs.y + x * cs.x;
+            const float2 y = rot(rk);
+            rkh[wid][d0] = f2h(y.x);
+            rkh[wid][d1] = f2h(y.y);
+            rvh[wid][2 * ri] = f2h(rv.x);
+            rvh[wid][2 * ri + 1] = f2h(rv.y);
+            // the new rows to the cache: wave 0 of the block whose chunk
+            // holds pos
+            if (wid == 0 && pos >= t0 && pos < t0 + a.chunk) {
+                uint16_t* kc = const_cast<uint16_t*>(a.k_cache) + lbase + (size_t)pos * rowstride;
+                uint16_t* vc = const_cast<uint16_t*>(a.v_cache) + lbase + (size_t)pos * rowstride;
+                if (IL) {
+                    *reinterpret_cast<uint32_t*>(kc + d0) = (uint32_t)f2h(y.x) | ((uint32_t)f2h(y.y) << 16);
+                } else {
+                    kc[d0] = f2h(y.x);
+                    kc[d1] = f2h(y.y);
                 }
+                *reinterpret_cast<uint32_t*>(vc + 2 * ri) = (uint32_t)f2h(rv.x) | ((uint32_t)f2h(rv.y) << 16);
+            }
+        }
+        if (m < G) {
 #pragma unroll
-            for (int j = 0; j < NJ; j++)
-#pragma unroll
-                for (int e = 0; e < 8; e++) f[j][e] = o[j][e];
+            for (int j = 0; j < NJ; j++) {
+                const float4* qp = reinterpret_cast<const float4*>(&rq[wid][m * HD + 32 * j + 8 * kg]);
+                qa[j][0] = qp[0];
+                qa[j][1] = qp[1];
+            }
+        }
+        // (as bit blends: conditional stores of one value into whichever
+        // element matches become a run-time index, and the arrays then leave
+        // the registers)
+        auto blend = [](uint4& d, const uint4 s, bool c) {
+            const uint32_t k = c ? 0xFFFFFFFFu : 0u;
+            d = make_uint4((s.x & k) | (d.x & ~k), (s.y & k) | (d.y & ~k), (s.z & k) | (d.z & ~k), (s.w & k) | (d.w & ~k));
         };
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const uint4 kn = *reinterpret_cast<const uint4*>(&rkh[wid][32 * j + 8 * kg]);
+#pragma unroll
+            for (int grp = 0; grp < NGRP; grp++) blend(kr[grp][j], kn, pw0 + 16 * grp + m == pos);
+        }
         {
-            float f[NJ][8];
+            const uint4 vn = *reinterpret_cast<const uint4*>(&rvh[wid][vcol]);
 #pragma unroll
-            for (int j = 0; j < NJ; j++) {
-                f[j][0] = qa[j][0].x; f[j][1] = qa[j][0].y; f[j][2] = qa[j][0].z; f[j][3] = qa[j][0].w;
-                f[j][4] = qa[j][1].x; f[j][5] = qa[j][1].y; f[j][6] = qa[j][1].z; f[j][7] = qa[j][1].w;
-            }
-            rope8(f);
-#pragma unroll
-            for (int j = 0; j < NJ; j++) {
-                qa[j][0] = qkeep[j][0] = make_float4(f[j][0], f[j][1], f[j][2], f[j][3]);
-                qa[j][1] = qkeep[j][1] = make_float4(f[j][4], f[j][5], f[j][6], f[j][7]);
-            }
-        }
-        uint16_t* kc = const_cast<uint16_t*>(a.k_cache) + lbase + (size_t)pos * rowstride;
-        uint16_t* vc = const_cast<uint16_t*>(a.v_cache) + lbase + (size_t)pos * rowstride;
-        auto pack8 = [](const float (&f)[8]) {
-            return make_uint4((uint32_t)f2h(f[0]) | ((uint32_t)f2h(f[1]) << 16), (uint32_t)f2h(f[2]) | ((uint32_t)f2h(f[3]) << 16),
-                              (uint32_t)f2h(f[4]) | ((uint32_t)f2h(f[5]) << 16), (uint32_t)f2h(f[6]) | ((uint32_t)f2h(f[7]) << 16));
-        };
-#pragma unroll
-        for (int grp = 0; grp < NGRP; grp++) {
-            if (pw0 + 16 * grp + m == pos) {
-                float f[NJ][8];
-#pragma unroll
-                for (int j = 0; j < NJ; j++) {
-                    const float4* kp = reinterpret_cast<const float4*>(&rkv[wid][32 * j + 8 * kg]);
-                    const float4 k0 = kp[0], k1 = kp[1];
-                    f[j][0] = k0.x; f[j][1] = k0.y; f[j][2] = k0.z; f[j][3] = k0.w;
-                    f[j][4] = k1.x; f[j][5] = k1.y; f[j][6] = k1.z; f[j][7] = k1.w;
-                }
-                rope8(f);
-#pragma unroll
-                for (int j = 0; j < NJ; j++) {
-                    kr[grp][j] = pack8(f[j]);
-                    *reinterpret_cast<uint4*>(kc + 32 * j + 8 * kg) = kr[grp][j];
-                }
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < NV; u++) {
-            if (pw0 + RPI * u + vrow == pos) {
-                const float4* vp = reinterpret_cast<const float4*>(&rkv[wid][HD + vcol]);
-                const float4 v0 = vp[0], v1 = vp[1];
-                const float f[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-                vr[u] = pack8(f);
-                *reinterpret_cast<uint4*>(vc + vcol) = vr[u];
-            }
+            for (int u = 0; u < NV; u++) blend(vr[u], vn, pw0 + RPI * u + vrow == pos);
         }
     }
 
