@@ -170,6 +170,19 @@ def test_attention_group_sizes_vs_oracle(lib, ctx, nh, nkv, hd):
     _attention_case(lib, ctx, nh, nkv, hd, seed=ctx + hd)
 
 
+# the split merge: 16 KV heads x 17 splits (272 blocks, more than the CUs of
+# an MI355X: the last split's block merges alone), 1 slice of 64 outputs per
+# KV head (one merger), 4 slices over 24 splits (4 mergers, waves whose third
+# split is past the last), and 8 slices over 32 splits (8 mergers); each
+# twice, the second call reusing the split words of the first
+@pytest.mark.parametrize("ctx,nh,nkv,hd", [(4100, 32, 16, 64), (1000, 8, 8, 64), (3000, 16, 8, 128),
+                                           (8000, 32, 8, 128)])
+def test_attention_merge_paths_vs_oracle(lib, ctx, nh, nkv, hd):
+    banner(f"attention merge ctx {ctx} heads {nh}/{nkv} hd {hd}")
+    for rep in range(2):
+        _attention_case(lib, ctx, nh, nkv, hd, seed=ctx + nkv + rep)
+
+
 def _attention_case(lib, ctx, nh, nkv, hd, seed, ms=None):
     from gsdlq import pack
     ms = ms or ctx + 3
