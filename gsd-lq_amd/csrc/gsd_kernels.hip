@@ -1288,7 +1288,11 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
                                 ((unsigned)(wo[k] >> 32) == ep && (unsigned)(wmx[k] >> 32) == ep &&
                                  (unsigned)(wsm[k] >> 32) == ep));
             if (done) break;
-            if (spins == (1 << 16)) {
+            // (bounded, about 0.2 s: a merger may wait for blocks dispatched
+            // after it, which take the CU slots the other blocks free as
+            // they finish; kernels of other streams holding the CUs only
+            // delay that)
+            if (spins == (1 << 22)) {
                 if (a.err) *a.err = 1u;
                 break;
             }
