@@ -241,11 +241,12 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
 hipError_t launch_rope_attention(const AttnArgs& a, const float* k, const float* v, int interleaved,
                                  const float2* cs, hipStream_t stream);
 // Positions per attention split for a context of n_ctx positions: one
-// split up to 256 positions (no hand-over, no merge); beyond, enough splits
-// to spread the context over the chip (n_kv * splits ~ 256 blocks), 64, 128
-// or 256 positions each (256 is the kernels' LDS score buffer).
+// split up to 128 positions (no hand-over, no merge; the shortest chunk
+// that holds them: fewer positions per wave); beyond, enough splits to
+// spread the context over the chip (n_kv * splits ~ 256 blocks), 64, 128 or
+// 256 positions each (256 is the kernels' LDS score buffer).
 inline int attention_chunk(int n_ctx, int n_kv) {
-    if (n_ctx <= 256) return 256;
+    if (n_ctx <= 128) return n_ctx <= 64 ? 64 : 128;
     const int want = (n_ctx * n_kv + 255) / 256;
     return want <= 64 ? 64 : (want <= 128 ? 128 : 256);
 }

@@ -1249,6 +1249,67 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
     const int nm = min(nsplit, min(max(a.mergers, 1), NSL));
     const int r = nsplit - 1 - split;
     if (r >= nm) return;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(wsk, (short)0, nsplit * G * WPH * 8, 0x00020000);
+    if (nsplit <= NW && nm < NSL) {
+        // At most 8 splits and fewer mergers than slices: wave w merges slice
+        // r + nm w on its own, each lane one output over every split in order
+        // (no LDS, no barrier: a block with several slices takes them at
+        // once, where the loop below would take them one after another);
+        // polled as below.
+        const int sl = r + nm * wid;
+        if (sl < NSL) {
+            const int o = sl * 64 + lane, g2 = o / HD, d2 = o % HD;
+            int vo[NW], vml[NW];
+#pragma unroll
+            for (int s = 0; s < NW; s++) {
+                vml[s] = s < nsplit ? (s * G + g2) * WPH * 8 : 0x7FFFFFF0;
+                vo[s] = s < nsplit ? vml[s] + (2 + d2) * 8 : 0x7FFFFFF0;
+            }
+            unsigned long long wo[NW], wmx[NW], wsm[NW];
+            for (int spins = 0;; spins++) {
+#pragma unroll
+                for (int s = 0; s < NW; s++) {
+                    auto w2 = __builtin_amdgcn_raw_buffer_load_b64(rs, vo[s], 0, 16 /* sc1 */);
+                    wo[s] = ((unsigned long long)w2[1] << 32) | w2[0];
+                    w2 = __builtin_amdgcn_raw_buffer_load_b64(rs, vml[s], 0, 16);
+                    wmx[s] = ((unsigned long long)w2[1] << 32) | w2[0];
+                    w2 = __builtin_amdgcn_raw_buffer_load_b64(rs, vml[s], 8, 16);
+                    wsm[s] = ((unsigned long long)w2[1] << 32) | w2[0];
+                }
+                bool done = true;
+#pragma unroll
+                for (int s = 0; s < NW; s++)
+                    done = done && (s >= nsplit || ((unsigned)(wo[s] >> 32) == ep && (unsigned)(wmx[s] >> 32) == ep &&
+                                                    (unsigned)(wsm[s] >> 32) == ep));
+                if (done) break;
+                if (spins == (1 << 22)) {   // (bounded, as below)
+                    if (a.err) *a.err = 1u;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+            float M2 = -INFINITY;
+#pragma unroll
+            for (int s = 0; s < NW; s++)
+                if (s < nsplit) M2 = fmaxf(M2, __uint_as_float((unsigned)wmx[s]));
+            float L2 = 0.f, O2 = 0.f;
+#pragma unroll
+            for (int s = 0; s < NW; s++)
+                if (s < nsplit) {
+                    const float f = __builtin_amdgcn_exp2f(__uint_as_float((unsigned)wmx[s]) - M2);
+                    L2 = fmaf(f, __uint_as_float((unsigned)wsm[s]), L2);
+                    O2 = fmaf(f, __uint_as_float((unsigned)wo[s]), O2);
+                }
+            a.out[(size_t)(kvh * G + g2) * HD + d2] = O2 / L2;
+        }
+        // (wave 0 always has a slice: it has seen every split's words)
+        if (r == 0) {
+            if (tid == 0 && !a.epoch) a.counters[kvh] = ep;
+            write_q();
+        }
+        return;
+    }
     // Thread (wave w, lane l): output l of the slice over splits w, w + 8,
     // w + 16, w + 24; its o, max and sum words (the latter two
     // the same address across the wave) loaded together, bypassing the
@@ -1256,8 +1317,6 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
     // nsplit has this launch's epoch (bounded).  Offsets past the words
     // read 0 (buffer bounds).  Then (max, sum, o) of the wave's splits,
     // and the 8 waves' combined by wave 0 through LDS, in a fixed order.
-    const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc(wsk, (short)0, nsplit * G * WPH * 8, 0x00020000);
     constexpr int KS = kAttnDecSplits / NW;   // splits per wave
     float* mlo = reinterpret_cast<float*>(&vs[0][0]);   // [3][NW][64]
     lds_barrier();   // (every wave is past its reads of vs above)

@@ -173,10 +173,14 @@ def test_attention_group_sizes_vs_oracle(lib, ctx, nh, nkv, hd):
 # the split merge: 16 KV heads x 17 splits (272 blocks, more than the CUs of
 # an MI355X: the last split's block merges alone), 1 slice of 64 outputs per
 # KV head (one merger), 4 slices over 24 splits (4 mergers, waves whose third
-# split is past the last), and 8 slices over 32 splits (8 mergers); each
-# twice, the second call reusing the split words of the first
+# split is past the last), and 8 slices over 32 splits (8 mergers); with at
+# most 8 splits and fewer mergers than slices, every wave of a merger takes a
+# slice of its own: 8 slices over 4, 7 and 3 splits (2, 2 and 3 slices in the
+# first merger); each twice, the second call reusing the split words of the
+# first
 @pytest.mark.parametrize("ctx,nh,nkv,hd", [(4100, 32, 16, 64), (1000, 8, 8, 64), (3000, 16, 8, 128),
-                                           (8000, 32, 8, 128)])
+                                           (8000, 32, 8, 128), (200, 32, 8, 128), (400, 32, 8, 128),
+                                           (150, 16, 4, 128)])
 def test_attention_merge_paths_vs_oracle(lib, ctx, nh, nkv, hd):
     banner(f"attention merge ctx {ctx} heads {nh}/{nkv} hd {hd}")
     for rep in range(2):
