@@ -2500,6 +2500,17 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
 // ------------------------------------------------------------------------
 __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
+// Token row of prep block b of nblocks (one block per row, padded to whole
+// 16-token groups): the 16 rows of a group, whose MFMA operand fragments
+// interleave in pieces of 4-16 bytes, all on one XCD (blocks go to the 8
+// XCDs in turn), so that one L2 assembles each line before writing it back;
+// the identity unless the groups divide evenly over the XCDs.
+__device__ __forceinline__ int prep_row(int b, int nblocks) {
+    if (nblocks & 127) return b;
+    const int x = b & 7, j = b >> 3;   // the j-th block on XCD x
+    return ((j >> 4) * 8 + x) * 16 + (j & 15);
+}
+
 // X bf16 [M][cols] -> A fragments xa[(g16 * nc + c) * 4 + (h * 2 + t)][lane] (uint4
 // = (u, v) fp16 of 4 pairs), lane = (m & 15) + 16 * lg, pair 64c + 32h + 8lg + 4t + e;
 // xs[m] = the token's descale.  One block per token (padded tokens: zeros).
@@ -2548,7 +2559,7 @@ __global__ void __launch_bounds__(256) hexmm_xprep_kernel(const uint16_t* X, int
 __global__ void __launch_bounds__(512) hexmm_xprep2_kernel(const uint16_t* X, int M, int cols, uint4* xa, float* xs) {
     __shared__ float red[8];
     constexpr float kS32 = 0.866025403784438646763723170752936183f;
-    const int m = blockIdx.x, tid = threadIdx.x, wid = tid >> 6;
+    const int m = prep_row((int)blockIdx.x, (int)gridDim.x), tid = threadIdx.x, wid = tid >> 6;
     const int nc = (cols + 127) >> 7, ng8 = cols >> 3;   // 8-column groups (4 pairs)
     const bool valid = m < M;
     const uint4* xr = reinterpret_cast<const uint4*>(X + (size_t)(valid ? m : 0) * cols);
@@ -2702,7 +2713,7 @@ __global__ void __launch_bounds__(512) batch_prep2_kernel(const BatchPrep p) {
     __shared__ float red[8][2 * kMaxSeg + 2];
     constexpr float kS32 = 0.866025403784438646763723170752936183f;
     constexpr int NT = 512, NS = 2 * kMaxSeg;
-    const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int m = prep_row((int)blockIdx.x, (int)gridDim.x), tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int nc = (p.cols + 127) >> 7, np = p.cols >> 1, nv4 = p.cols >> 2;
     const bool valid = m < p.M;
     const float4* xr4 = reinterpret_cast<const float4*>(p.X + (size_t)(valid ? m : 0) * p.ldx);
