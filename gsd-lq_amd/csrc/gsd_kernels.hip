@@ -1096,7 +1096,7 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
     for (int j = 0; j < NJ; j++)
 #pragma unroll
         for (int h = 0; h < 2; h++)
-            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(qa[j][h].x), fabsf(qa[j][h].y)), fmaxf(fabsf(qa[j][h].z), fabsf(qa[j][h].w))));
+            mx = fmax_nc(mx, fmax_nc(fmax_nc(fabsf(qa[j][h].x), fabsf(qa[j][h].y)), fmax_nc(fabsf(qa[j][h].z), fabsf(qa[j][h].w))));
     mx = wave_max_valu(mx);
     int ex = 0;
     if (mx > 0.f && mx < INFINITY) (void)frexpf(mx, &ex);
@@ -1138,7 +1138,7 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
     float mw[4], lw[4];
 #pragma unroll
     for (int g = 0; g < 4; g++) {
-        mw[g] = row16_max(fmaxf(sv[0][g], sv[1][g]));
+        mw[g] = row16_max(fmax_nc(sv[0][g], sv[1][g]));
         const float mu = mw[g] == -INFINITY ? 0.f : mw[g];
         sv[0][g] = __builtin_amdgcn_exp2f(sv[0][g] - mu);
         sv[1][g] = __builtin_amdgcn_exp2f(sv[1][g] - mu);
@@ -1188,7 +1188,7 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
         for (int g = 0; g < G; g++)
 #pragma unroll
             for (int e = 0; e < 8; e++)
-                acc[g][e] += __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(acc[g][e]), 0x128, 0xF, 0xF, false));
+                acc[g][e] += __uint_as_float(__builtin_amdgcn_mov_dpp(__float_as_uint(acc[g][e]), 0x128, 0xF, 0xF, true));
     }
     if (HD == 128 || (lane & 15) < 8) {
         const int r = lane >> 4, c = HD == 128 ? (lane & 15) : (lane & 7);
@@ -1206,7 +1206,7 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
     const bool own = tid < G * HD;
     float M = -INFINITY, L = 0.f, O = 0.f;
     if (own) {
-        for (int w = 0; w < NW; w++) M = fmaxf(M, wm[w][g]);
+        for (int w = 0; w < NW; w++) M = fmax_nc(M, wm[w][g]);
         for (int w = 0; w < NW; w++) {
             const float f = __builtin_amdgcn_exp2f(wm[w][g] - M);   // (-inf: an empty wave, 0)
             const float* o = reinterpret_cast<const float*>(&vs[w][0]);
@@ -1292,7 +1292,7 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
             float M2 = -INFINITY;
 #pragma unroll
             for (int s = 0; s < NW; s++)
-                if (s < nsplit) M2 = fmaxf(M2, __uint_as_float((unsigned)wmx[s]));
+                if (s < nsplit) M2 = fmax_nc(M2, __uint_as_float((unsigned)wmx[s]));
             float L2 = 0.f, O2 = 0.f;
 #pragma unroll
             for (int s = 0; s < NW; s++)
@@ -1360,7 +1360,7 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
         float mp = -INFINITY, lp = 0.f, op = 0.f;
 #pragma unroll
         for (int k = 0; k < KS; k++)
-            if (wid + NW * k < nsplit) mp = fmaxf(mp, __uint_as_float((unsigned)wmx[k]));
+            if (wid + NW * k < nsplit) mp = fmax_nc(mp, __uint_as_float((unsigned)wmx[k]));
 #pragma unroll
         for (int k = 0; k < KS; k++)
             if (wid + NW * k < nsplit) {
@@ -1375,7 +1375,7 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
         if (wid == 0) {
             float M2 = mlo[lane];
 #pragma unroll
-            for (int w = 1; w < NW; w++) M2 = fmaxf(M2, mlo[w * 64 + lane]);
+            for (int w = 1; w < NW; w++) M2 = fmax_nc(M2, mlo[w * 64 + lane]);
             float L2 = 0.f, O2 = 0.f;
 #pragma unroll
             for (int w = 0; w < NW; w++) {
@@ -1722,7 +1722,7 @@ __device__ __forceinline__ void attn_fa_block(const FaIn a, int kvh, unsigned ta
         for (int j = 0; j < NJ; j++)
 #pragma unroll
             for (int h = 0; h < 2; h++)
-                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(qa[j][h].x), fabsf(qa[j][h].y)), fmaxf(fabsf(qa[j][h].z), fabsf(qa[j][h].w))));
+                mx = fmax_nc(mx, fmax_nc(fmax_nc(fabsf(qa[j][h].x), fabsf(qa[j][h].y)), fmax_nc(fabsf(qa[j][h].z), fabsf(qa[j][h].w))));
         mx = wave_max_valu(mx);
         int ex = 0;
         if (mx > 0.f && mx < INFINITY) (void)frexpf(mx, &ex);
@@ -1761,7 +1761,7 @@ __device__ __forceinline__ void attn_fa_block(const FaIn a, int kvh, unsigned ta
         float mw[4], lw[4];
 #pragma unroll
         for (int gg = 0; gg < 4; gg++) {
-            mw[gg] = row16_max(fmaxf(sv[0][gg], sv[1][gg]));
+            mw[gg] = row16_max(fmax_nc(sv[0][gg], sv[1][gg]));
             const float mu = mw[gg] == -INFINITY ? 0.f : mw[gg];
             sv[0][gg] = __builtin_amdgcn_exp2f(sv[0][gg] - mu);
             sv[1][gg] = __builtin_amdgcn_exp2f(sv[1][gg] - mu);
@@ -1807,7 +1807,7 @@ __device__ __forceinline__ void attn_fa_block(const FaIn a, int kvh, unsigned ta
             for (int gg = 0; gg < G; gg++)
 #pragma unroll
                 for (int e = 0; e < 8; e++)
-                    acc[gg][e] += __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(acc[gg][e]), 0x128, 0xF, 0xF, false));
+                    acc[gg][e] += __uint_as_float(__builtin_amdgcn_mov_dpp(__float_as_uint(acc[gg][e]), 0x128, 0xF, 0xF, true));
         }
         if (HD == 128 || (lane & 15) < 8) {
             const int rr = lane >> 4, c = HD == 128 ? (lane & 15) : (lane & 7);
@@ -1822,7 +1822,7 @@ __device__ __forceinline__ void attn_fa_block(const FaIn a, int kvh, unsigned ta
         // the block's (max, sum, o) per head: thread (g, d), waves in order
         if (own) {
             float M = -INFINITY, L = 0.f, O = 0.f;
-            for (int w = 0; w < NW; w++) M = fmaxf(M, wm[w][g]);
+            for (int w = 0; w < NW; w++) M = fmax_nc(M, wm[w][g]);
             for (int w = 0; w < NW; w++) {
                 const float f = __builtin_amdgcn_exp2f(wm[w][g] - M);   // (-inf: an empty wave, 0)
                 const float* o = reinterpret_cast<const float*>(&vs[w][0]);
