@@ -2584,7 +2584,7 @@ __global__ void __launch_bounds__(512) hexmm_xprep2_kernel(const uint16_t* X, in
             mx = fmaxf(mx, fmaxf(fabsf(xa_), fabsf(fmaf(kS32, xb_, 0.5f * xa_))));
         }
     }
-    mx = wave_max(mx);
+    mx = wave_max_nonneg(mx);   // (|x| >= 0; fmaxf above keeps NaN out)
     if ((tid & 63) == 0) red[wid] = mx;
     __syncthreads();
     mx = red[0];
