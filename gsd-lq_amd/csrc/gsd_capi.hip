@@ -31,6 +31,12 @@ int fail(int code, const char* fmt, ...) {
     g_err = buf;
     return code ? code : -1;
 }
+void attention_test_knobs(AttnArgs& a) {
+    const char* s = std::getenv("GSD_ATTN_TEST_SKEW");
+    a.wait_skew = s ? std::atoi(s) : 0;
+    s = std::getenv("GSD_ATTN_SPIN_LIMIT");
+    a.spin_limit = s ? std::atoi(s) : 0;
+}
 }  // namespace gsd
 
 namespace {
@@ -90,14 +96,15 @@ __attribute__((noinline)) void rope_cs(float theta, int hd, int pos, float* out 
     }
 }
 
-// Workspaces of the attention twin, one per stream (calls on different
-// streams may overlap; calls on one stream run in order): the partial words
-// and the epoch of the stream's last launch.  Every launch takes the next
-// epoch, so words a launch of another shape left behind never match.
+// Workspaces of the attention twins that a caller created for a stream
+// (gsdh_attention_workspace_create): calls on such a stream use it, calls on
+// other streams the library's per-device static scratch.  Each holds the
+// 256-byte header (device epoch word, error word) and the split words; the
+// epoch lives on the device, so the host keeps no per-launch state.
 struct AttnWs {
-    unsigned long long* ws = nullptr;
-    size_t bytes = 0;
-    unsigned epoch = 0;
+    unsigned long long* ws = nullptr;   // header + words
+    size_t bytes = 0;                   // words only
+    int dev = 0;
 };
 std::mutex g_attn_mu;
 std::map<hipStream_t, AttnWs> g_attn_ws;
@@ -144,6 +151,109 @@ int gsdh_stream_copy(void* stream, void* dst, const void* src, uint64_t nbytes) 
 }
 int gsdh_stream_sync(void* stream) {
     HIPCHK(hipStreamSynchronize(S(stream)));
+    // a stand-alone attention launch whose merge gave up waiting for a
+    // split's partials (bounded wait) left its error word set: report it
+    // here, as an asynchronous failure surfaces at the next synchronisation
+    int bad = 0;
+    int rc = attention_static_error(&bad);
+    if (rc) return rc;
+    unsigned* ew = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_attn_mu);
+        auto it = g_attn_ws.find(S(stream));
+        if (it != g_attn_ws.end()) ew = reinterpret_cast<unsigned*>(it->second.ws + 1);
+    }
+    if (ew) {
+        unsigned v = 0;
+        HIPCHK(hipMemcpy(&v, ew, 4, hipMemcpyDeviceToHost));
+        if (v) {
+            const unsigned zero = 0;
+            HIPCHK(hipMemcpy(ew, &zero, 4, hipMemcpyHostToDevice));
+            bad = 1;
+        }
+    }
+    if (bad)
+        return fail(-2, "stream_sync: an attention launch's merge timed out waiting for split partials "
+                        "(its output is undefined)");
+    return 0;
+}
+
+int gsdh_stream_create(void** stream_out) {
+    if (!stream_out) return fail(-1, "stream_create: null argument");
+    hipStream_t s = nullptr;
+    HIPCHK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    *stream_out = s;
+    return 0;
+}
+
+int gsdh_stream_destroy(void* stream) {
+    if (!stream) return 0;
+    HIPCHK(hipStreamSynchronize(S(stream)));
+    int rc = gsdh_attention_workspace_destroy(stream);
+    if (rc) return rc;
+    HIPCHK(hipStreamDestroy(S(stream)));
+    return 0;
+}
+
+int gsdh_stream_begin_capture(void* stream) {
+    HIPCHK(hipStreamBeginCapture(S(stream), hipStreamCaptureModeThreadLocal));
+    return 0;
+}
+
+int gsdh_stream_end_capture(void* stream, void** graph_exec_out) {
+    if (!graph_exec_out) return fail(-1, "stream_end_capture: null argument");
+    hipGraph_t g = nullptr;
+    HIPCHK(hipStreamEndCapture(S(stream), &g));
+    hipGraphExec_t ge = nullptr;
+    hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return fail((int)e, "hipGraphInstantiate: %s", hipGetErrorString(e));
+    *graph_exec_out = ge;
+    return 0;
+}
+
+int gsdh_graph_replay(void* graph_exec, void* stream) {
+    HIPCHK(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(graph_exec), S(stream)));
+    return 0;
+}
+
+uint64_t gsdh_attention_workspace_bytes(int n_kv_heads, int n_heads, int head_dim, int max_seq_len) {
+    if (n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads || head_dim <= 0 || max_seq_len <= 0) return 0;
+    return kAttnWsHeader + attention_ws_bytes_upto(n_kv_heads, n_heads / n_kv_heads, head_dim, max_seq_len);
+}
+
+int gsdh_attention_workspace_create(void* stream, int n_kv_heads, int n_heads, int head_dim, int max_seq_len) {
+    const uint64_t total = gsdh_attention_workspace_bytes(n_kv_heads, n_heads, head_dim, max_seq_len);
+    if (!total) return fail(-1, "attention_workspace_create: n_kv_heads %d n_heads %d head_dim %d max_seq_len %d",
+                            n_kv_heads, n_heads, head_dim, max_seq_len);
+    int rc = gsdh_attention_workspace_destroy(stream);
+    if (rc) return rc;
+    AttnWs w;
+    HIPCHK(hipGetDevice(&w.dev));
+    HIPCHK(hipMalloc(&w.ws, total));
+    w.bytes = total - kAttnWsHeader;
+    hipError_t e = launch_fill_u32(reinterpret_cast<unsigned*>(w.ws), 0u, total / 4, S(stream));
+    if (e == hipSuccess) e = hipStreamSynchronize(S(stream));
+    if (e != hipSuccess) {
+        (void)hipFree(w.ws);
+        return fail((int)e, "attention_workspace_create: %s", hipGetErrorString(e));
+    }
+    std::lock_guard<std::mutex> lk(g_attn_mu);
+    g_attn_ws[S(stream)] = w;
+    return 0;
+}
+
+int gsdh_attention_workspace_destroy(void* stream) {
+    AttnWs w;
+    {
+        std::lock_guard<std::mutex> lk(g_attn_mu);
+        auto it = g_attn_ws.find(S(stream));
+        if (it == g_attn_ws.end()) return 0;
+        w = it->second;
+        g_attn_ws.erase(it);
+    }
+    HIPCHK(hipStreamSynchronize(S(stream)));
+    HIPCHK(hipFree(w.ws));
     return 0;
 }
 
@@ -210,8 +320,9 @@ int gsdh_rope_and_store_kv(void* stream, float* q, const float* k, const float* 
 }
 
 namespace {
-// Checks a one-token attention call and fills a (positions, chunking, the
-// stream's workspace and the next epoch on it); g_attn_mu held.
+// Checks a one-token attention call and fills a (positions, chunking, and the
+// workspace: the stream's own, else the library's static scratch); nothing
+// is allocated.
 int attention_setup(void* stream, AttnArgs& a, const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
                     float* attn_out, int layer_idx, int pos, int n_heads, int n_kv_heads, int head_dim,
                     int max_seq_len, float sm_scale) {
@@ -226,33 +337,26 @@ int attention_setup(void* stream, AttnArgs& a, const float* q, const uint16_t* k
     a.sm_scale = sm_scale;
     a.chunk = attention_chunk(n, n_kv_heads);
     a.max_splits = (n + a.chunk - 1) / a.chunk;
+    attention_test_knobs(a);
     const size_t need = attention_ws_bytes(n_kv_heads, a.max_splits, G, head_dim);
-    AttnWs& w = g_attn_ws[S(stream)];
-    if (need > w.bytes || w.epoch >= 0xFFFFFFF0u) {
-        // a larger workspace (the stream's earlier launches finish first),
-        // or the epoch about to wrap: words start at zero, epochs at 1
-        if (need > w.bytes) {
-            HIPCHK(hipStreamSynchronize(S(stream)));
-            if (w.ws) HIPCHK(hipFree(w.ws));
-            w.ws = nullptr;
-            w.bytes = 0;
-            HIPCHK(hipMalloc(&w.ws, need));
-            w.bytes = need;
+    {
+        std::lock_guard<std::mutex> lk(g_attn_mu);
+        auto it = g_attn_ws.find(S(stream));
+        if (it != g_attn_ws.end()) {
+            if (need > it->second.bytes)
+                return fail(-1, "attention: %zu bytes of split partials exceed the stream's workspace (%zu bytes); "
+                                "create it for a longer context", need, it->second.bytes);
+            attention_use_ws(a, it->second.ws);
+            return 0;
         }
-        HIPCHK(launch_fill_u32(reinterpret_cast<unsigned*>(w.ws), 0u, w.bytes / 4, S(stream)));
-        w.epoch = 0;
     }
-    a.ws = w.ws;
-    a.counters = nullptr;
-    a.epoch = ++w.epoch;
-    return 0;
+    return attention_static_ws(S(stream), a, G, "attention");
 }
 }  // namespace
 
 int gsdh_gqa_attention(void* stream, const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
                        float* attn_out, int layer_idx, int pos, int n_heads, int n_kv_heads, int head_dim,
                        int max_seq_len, float sm_scale) {
-    std::lock_guard<std::mutex> lk(g_attn_mu);
     AttnArgs a;
     const int rc = attention_setup(stream, a, q, k_cache, v_cache, attn_out, layer_idx, pos, n_heads, n_kv_heads,
                                    head_dim, max_seq_len, sm_scale);
@@ -266,7 +370,6 @@ int gsdh_rope_store_gqa_attention(void* stream, float* q, const float* k, const 
                                   int n_kv_heads, int head_dim, int max_seq_len, float rope_theta, int interleaved,
                                   float sm_scale) {
     if (head_dim <= 0 || head_dim % 2 || head_dim > 256) return fail(-1, "rope: head_dim %d", head_dim);
-    std::lock_guard<std::mutex> lk(g_attn_mu);
     AttnArgs a;
     const int rc = attention_setup(stream, a, q, k_cache, v_cache, attn_out, layer_idx, pos, n_heads, n_kv_heads,
                                    head_dim, max_seq_len, sm_scale);
@@ -814,10 +917,13 @@ int issue_prefill(gsdh_model* m, int M, int p0) {
 // Prompt prompt[0..n) at positions start.. in batches of the prefill chunk;
 // with `head`, the last token's logits and the greedy step (the step state
 // then holds the first generated token at position start + n, gen_count 1).
-// `ring`: pinned host staging of >= ceil(n / chunk) step states (read by
-// the copies until the stream is synchronised).
-int run_prefill(gsdh_model* m, const int* prompt, int n, int start, bool head, int* tok_stage, StepState* st_stage) {
+// tok_stage: pinned host staging of n token ids (read by the copies until
+// the stream is synchronised).  The step state's error word is cleared
+// first and then only ever set, so a bounded wait that ran out in any
+// chunk's attention reaches the caller.
+int run_prefill(gsdh_model* m, const int* prompt, int n, int start, bool head, int* tok_stage) {
     auto& P = m->pf;
+    HIPCHK(launch_set_step(m->st, prompt[0], start, 1, m->stream));
     for (int b0 = 0; b0 < n; b0 += P.chunk) {
         const int M = std::min(P.chunk, n - b0);
         int* ts = tok_stage + b0;
@@ -826,10 +932,7 @@ int run_prefill(gsdh_model* m, const int* prompt, int n, int start, bool head, i
         int rc = issue_prefill(m, M, start + b0);
         if (rc) return rc;
     }
-    *st_stage = StepState{};
-    st_stage->token = prompt[n - 1];
-    st_stage->pos = start + n - 1;
-    HIPCHK(hipMemcpyAsync(m->st, st_stage, sizeof(StepState), hipMemcpyHostToDevice, m->stream));
+    HIPCHK(launch_set_step(m->st, prompt[n - 1], start + n - 1, 0, m->stream));
     if (head) return issue_head(m, true);
     return 0;
 }
@@ -1153,16 +1256,16 @@ int gsdh_generate_greedy(gsdh_model* m, const int* prompt, int n_prompt, int sta
         return fail(-1, "generate: positions %d..%d exceed max_seq_len %d", start_pos, start_pos + n_prompt + n_new - 1, m->c.max_seq_len);
     for (int i = 0; i < n_prompt; i++)
         if (prompt[i] < 0 || prompt[i] >= m->c.vocab) return fail(-1, "generate: prompt token %d outside vocab", prompt[i]);
-    StepState* ring = nullptr;
-    HIPCHK(hipHostMalloc((void**)&ring, sizeof(StepState) * (size_t)n_prompt + sizeof(int) * (size_t)n_prompt, 0));
+    int* tok_stage = nullptr;
+    HIPCHK(hipHostMalloc((void**)&tok_stage, sizeof(int) * (size_t)n_prompt, 0));
     int rc = 0;
     if (m->pf.batched) {
-        rc = run_prefill(m, prompt, n_prompt, start_pos, true, reinterpret_cast<int*>(ring + n_prompt), ring);
+        rc = run_prefill(m, prompt, n_prompt, start_pos, true, tok_stage);
     } else {
+        // token by token: the step state of each prompt token, its error
+        // word cleared for the first only (a wait that ran out stays set)
         for (int i = 0; i < n_prompt && !rc; i++) {
-            ring[i] = StepState{};
-            ring[i].token = prompt[i]; ring[i].pos = start_pos + i;
-            hipError_t e = hipMemcpyAsync(m->st, &ring[i], sizeof(StepState), hipMemcpyHostToDevice, m->stream);
+            hipError_t e = launch_set_step(m->st, prompt[i], start_pos + i, i == 0 ? 1 : 0, m->stream);
             if (e == hipSuccess) e = hipGraphLaunch(token_graph(m, i == n_prompt - 1, start_pos + i), m->stream);
             if (e != hipSuccess) rc = fail((int)e, "generate prefill: %s", hipGetErrorString(e));
         }
@@ -1182,7 +1285,7 @@ int gsdh_generate_greedy(gsdh_model* m, const int* prompt, int n_prompt, int sta
         else if (m->st_host[1].err) rc = fail(-2, "generate: an in-kernel wait timed out");
     }
     (void)hipStreamSynchronize(m->stream);
-    (void)hipHostFree(ring);
+    (void)hipHostFree(tok_stage);
     return rc;
 }
 
@@ -1197,7 +1300,7 @@ int gsdh_model_prefill(gsdh_model* m, const int* tokens, int n, int start_pos, i
         if (tokens[i] < 0 || tokens[i] >= m->c.vocab) return fail(-1, "prefill: token %d outside vocab %d", tokens[i], m->c.vocab);
     StepState* ring = nullptr;
     HIPCHK(hipHostMalloc((void**)&ring, sizeof(StepState) * 2 + sizeof(int) * (size_t)n, 0));
-    int rc = run_prefill(m, tokens, n, start_pos, want_logits != 0, reinterpret_cast<int*>(ring + 2), ring);
+    int rc = run_prefill(m, tokens, n, start_pos, want_logits != 0, reinterpret_cast<int*>(ring + 2));
     if (!rc && want_logits && logits_host) {
         hipError_t e = hipMemcpyAsync(logits_host, m->logits, (size_t)m->c.vocab * 4, hipMemcpyDeviceToHost, m->stream);
         if (e != hipSuccess) rc = fail((int)e, "prefill: %s", hipGetErrorString(e));
@@ -1271,6 +1374,15 @@ int gsdh_model_matmul(gsdh_model* m, int layer, int slot, const uint16_t* X, int
     a.part = nsplit > 1 ? reinterpret_cast<float*>(w + xa + xs + tk) : nullptr;
     if (t.k > 0) HIPCHK(launch_lowrank_batched(X, t.Vt, t.Sv, reinterpret_cast<float*>(w + xa + xs), M, t.k, t.cols, m->stream));
     HIPCHK(launch_hexmm(a, m->stream));
+    return 0;
+}
+
+int gsdh_matmul_plan(int M, int rows, int cols, int* tg, int* rbw, int* nsplit) {
+    if (M <= 0 || rows <= 0 || cols <= 0 || !tg || !rbw || !nsplit) return fail(-1, "matmul_plan: bad argument");
+    const MatmulPlan p = hexmm_plan(M, rows, cols);
+    *tg = p.tg;
+    *rbw = p.rbw;
+    *nsplit = p.nsplit;
     return 0;
 }
 

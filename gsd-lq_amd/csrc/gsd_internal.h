@@ -220,9 +220,26 @@ struct AttnArgs {
     // count (the epoch is the count + 1, advanced by the merging block; for
     // graph replays of one shape).  Zero ws and counters at allocation.
     unsigned long long* ws;   // [n_kv][max_splits][group][2 + hd]
-    unsigned* counters;       // [n_kv] (epoch == 0 only)
+    unsigned* counters;       // [n_kv] (epoch == 0 and dep == null only)
     unsigned* err;            // set to 1 when a wait for a partial runs out (may be null)
     unsigned epoch;
+    // Third epoch source (epoch == 0, counters == null; one-token launches
+    // with a host position): a device word, high half the epoch of the last
+    // launch on the workspace, low half an arrival count.  Every block adds
+    // one to it with a single atomic at its start (the old value gives the
+    // epoch; this launch tags its words with the next, 0 skipped), and the
+    // last block to arrive stores (next epoch << 32 | 0).  Each launch thus
+    // takes a new epoch on the device, also when a captured graph replays
+    // it, and words of earlier launches of any shape never match.  Zero at
+    // allocation.
+    unsigned long long* dep;
+    // merging blocks: polling rounds before a wait counts as timed out
+    // (0: the default bound)
+    int spin_limit;
+    // test only (0 in use): merging blocks wait for the tag epoch +
+    // wait_skew, which no split writes, so the bounded wait runs out and
+    // sets *err while every block still finishes
+    int wait_skew;
     // ntok > 1: a batch of consecutive query tokens (prefill; causal): token
     // z = grid.z index at position pos + z, q / out rows z * n_heads * hd, its
     // words at ws + z * n_kv * max_splits * group * (2 + hd); needs epoch.
@@ -240,6 +257,9 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
 // not cover (then run launch_rope_kv and launch_attention).
 hipError_t launch_rope_attention(const AttnArgs& a, const float* k, const float* v, int interleaved,
                                  const float2* cs, hipStream_t stream);
+// Polling rounds of a merging block (each ~50 ns of s_sleep plus a round
+// trip; about 0.2 s in all) before its wait counts as timed out.
+constexpr int kAttnSpinLimit = 1 << 22;
 // Positions per attention split for a context of n_ctx positions: one
 // split up to 128 positions (no hand-over, no merge; the shortest chunk
 // that holds them: fewer positions per wave); beyond, enough splits to
@@ -254,6 +274,34 @@ inline int attention_chunk(int n_ctx, int n_kv) {
 // or -1 for code 0.
 int fail(int code, const char* fmt, ...);
 size_t attention_ws_bytes(int n_kv, int max_splits, int group, int hd);
+// Workspace of a stand-alone one-token attention launch (the operator
+// twins): a 256-byte header (AttnArgs::dep at byte 0, the error word at byte
+// 8), then the split words.  Zero at allocation; never cleared after.
+constexpr size_t kAttnWsHeader = 256;
+// Split words a workspace must hold for every context of 1 .. max_ctx
+// positions (the chunking of attention_chunk), header excluded.
+size_t attention_ws_bytes_upto(int n_kv, int group, int hd, int max_ctx);
+// Fills the epoch, workspace and error fields of a one-token attention
+// launch from a workspace laid out as above (splits > 1 only: a single split
+// hands nothing over).
+inline void attention_use_ws(AttnArgs& a, unsigned long long* hdr) {
+    a.epoch = 0;
+    a.counters = nullptr;
+    a.dep = a.max_splits > 1 ? hdr : nullptr;
+    a.err = reinterpret_cast<unsigned*>(hdr + 1);
+    a.ws = hdr + kAttnWsHeader / 8;
+}
+// The library's static scratch of the current device (gsd_noalloc.hip) as a
+// one-token launch's workspace (a.n_kv, a.hd and a.max_splits set); fails
+// when the partials do not fit it.
+int attention_static_ws(hipStream_t stream, AttnArgs& a, int group, const char* who);
+// After a synchronisation: whether a merge's wait on the static scratch ran
+// out since the last check (the word is cleared).
+int attention_static_error(int* was_set);
+// Test-only settings of the stand-alone attention launches, read from the
+// environment at each call (GSD_ATTN_TEST_SKEW -> wait_skew,
+// GSD_ATTN_SPIN_LIMIT -> spin_limit); both unset in use.
+void attention_test_knobs(AttnArgs& a);
 
 // embedding row of *token_dev to fp32 x; also zeroes clear[0..nclear) (the
 // rank-k publication words of the token's matvec launches) and, when epoch
@@ -276,6 +324,8 @@ struct StepState {
 };
 hipError_t launch_argmax(const float* logits, int n, StepState* st, int* gen_tokens,
                          float* gen_margins, int advance, hipStream_t stream);
+// st->token, pos = (token, pos), gen_count = 0; err cleared only with reset_err
+hipError_t launch_set_step(StepState* st, int token, int pos, int reset_err, hipStream_t stream);
 hipError_t launch_fill_u32(unsigned* p, unsigned v, size_t n, hipStream_t stream);
 hipError_t launch_unpack(const uint8_t* codes, int64_t n, int radius, int32_t* idx,
                          int8_t* r01, hipStream_t stream);

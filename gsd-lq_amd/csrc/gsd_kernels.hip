@@ -613,6 +613,25 @@ __global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
 
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int sub = lane % LPP, prow = lane / LPP;
+    const int kvh = blockIdx.x;
+    // the epoch (used at the end).  Device word (a.dep): every block of the
+    // grid arrives before anything else, and the last to arrive advances it
+    unsigned ep0;
+    if (a.dep) {
+        __shared__ unsigned s_ep0;
+        if (tid == 0) {
+            const unsigned long long t = __hip_atomic_fetch_add(a.dep, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            unsigned e = (unsigned)(t >> 32) + 1u;
+            if (e == 0u) e = 1u;
+            if ((unsigned)t == gridDim.x * gridDim.y * gridDim.z - 1u)
+                __hip_atomic_store(a.dep, (unsigned long long)e << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_ep0 = e - 1u;
+        }
+        __syncthreads();
+        ep0 = s_ep0;
+    } else {
+        ep0 = a.epoch ? a.epoch - 1u : (a.counters ? a.counters[kvh] : 0u);
+    }
     // token z of a batch (prefill; decode: z = 0) at position pos + z
     const int z = blockIdx.z;
     const int pos = (a.pos_dev ? *a.pos_dev : a.pos) + z;
@@ -620,10 +639,8 @@ __global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
     const int nsplit = (n + a.chunk - 1) / a.chunk;
     const int split = blockIdx.y;
     if (split >= nsplit) return;
-    const int kvh = blockIdx.x;
     const float* qz = a.q + (size_t)z * a.n_heads * HD;
     float* outz = a.out + (size_t)z * a.n_heads * HD;
-    const unsigned ep0 = a.epoch ? a.epoch - 1u : a.counters[kvh];   // (used at the end)
     const int t0 = split * a.chunk;
     const int t1 = min(n, t0 + a.chunk);
     const int cn = t1 - t0;
@@ -784,18 +801,21 @@ __global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
         const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, w * 8, 0, 16 /* sc1 */);
         return ((unsigned long long)v[1] << 32) | v[0];
     };
+    // (wait_skew: a test-only offset that makes the wait run out)
+    const unsigned epw = ep + (unsigned)a.wait_skew;
+    const int lim = a.spin_limit > 0 ? a.spin_limit : kAttnSpinLimit;
     auto wait_word = [&](int w) {
         unsigned long long v;
         int spins = 0;
-        while (((v = __hip_atomic_load(wsk + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) >> 32) != ep &&
-               spins < (1 << 20)) {
-            if (++spins == (1 << 20) && a.err) *a.err = 1u;
+        while (((v = __hip_atomic_load(wsk + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) >> 32) != epw &&
+               spins < lim) {
+            if (++spins == lim && a.err) *a.err = 1u;
             __builtin_amdgcn_s_sleep(1);
         }
         return __uint_as_float((unsigned)v);
     };
     auto value = [&](unsigned long long v, int w) {
-        return (v >> 32) == ep ? __uint_as_float((unsigned)v) : wait_word(w);
+        return (v >> 32) == epw ? __uint_as_float((unsigned)v) : wait_word(w);
     };
     constexpr int SB = kAttnStage / HD;       // splits per staging batch
     constexpr int MAXI = kAttnStage / NT;     // staged words per thread
@@ -863,7 +883,8 @@ __global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
         }
         if (tid < HD) outz[(size_t)(group_base + g) * HD + tid] = O / L;
     }
-    if (back == 0 && tid == 0 && !a.epoch) a.counters[kvh] = ep;   // the next launch's epoch base (stream order)
+    // the next launch's epoch base (stream order; the counters mode only)
+    if (back == 0 && tid == 0 && a.counters && !a.epoch) a.counters[kvh] = ep;
 }
 
 // ------------------------------------------------------------------------
@@ -953,8 +974,12 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
     // this launch's epoch, read before any work: the merging block advances
     // the head's counter once it has every split's words, so each block
     // must have read it by then (a block that read it late, after a fast
-    // merger's update, would tag its words with the next launch's epoch)
-    const unsigned ep = a.epoch ? a.epoch : (a.max_splits > 1 ? a.counters[kvh] + 1u : 0u);
+    // merger's update, would tag its words with the next launch's epoch).
+    // Device word (a.dep): the block's arrival goes out first, its result
+    // is taken at the block combine below
+    unsigned long long dtk = 0;
+    if (a.dep && tid == 0) dtk = __hip_atomic_fetch_add(a.dep, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned ep = a.epoch ? a.epoch : (a.dep || a.max_splits == 1 ? 0u : a.counters[kvh] + 1u);
 
     // q (A operand source): lane l, head m = l & 15 (m < G), dims
     // 32 j + 8 (l >> 4) .. + 7; issued first, the K and V rows behind it
@@ -1199,7 +1224,18 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
             op[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
         }
     }
+    __shared__ unsigned s_ep;
+    if (a.dep && tid == 0) {
+        // the epoch of the last launch on the workspace + 1 (0 skipped); the
+        // last block to arrive (every block has read the word) advances it
+        unsigned e = (unsigned)(dtk >> 32) + 1u;
+        if (e == 0u) e = 1u;
+        s_ep = e;
+        if ((unsigned)dtk == gridDim.x * gridDim.y - 1u)
+            __hip_atomic_store(a.dep, (unsigned long long)e << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     lds_barrier();
+    if (a.dep) ep = s_ep;
 
     // the block's (max, sum, o) per head: thread (g, d), waves in order
     const int g = tid / HD, d = tid % HD;
@@ -1249,6 +1285,10 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
     const int nm = min(nsplit, min(max(a.mergers, 1), NSL));
     const int r = nsplit - 1 - split;
     if (r >= nm) return;
+    // the tag the merge waits for (wait_skew: a test-only offset that makes
+    // the wait run out) and its bound
+    const unsigned epw = ep + (unsigned)a.wait_skew;
+    const int lim = a.spin_limit > 0 ? a.spin_limit : kAttnSpinLimit;
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc(wsk, (short)0, nsplit * G * WPH * 8, 0x00020000);
     if (nsplit <= NW && nm < NSL) {
@@ -1280,10 +1320,10 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
                 bool done = true;
 #pragma unroll
                 for (int s = 0; s < NW; s++)
-                    done = done && (s >= nsplit || ((unsigned)(wo[s] >> 32) == ep && (unsigned)(wmx[s] >> 32) == ep &&
-                                                    (unsigned)(wsm[s] >> 32) == ep));
+                    done = done && (s >= nsplit || ((unsigned)(wo[s] >> 32) == epw && (unsigned)(wmx[s] >> 32) == epw &&
+                                                    (unsigned)(wsm[s] >> 32) == epw));
                 if (done) break;
-                if (spins == (1 << 22)) {   // (bounded, as below)
+                if (spins == lim) {   // (bounded, as below)
                     if (a.err) *a.err = 1u;
                     break;
                 }
@@ -1305,7 +1345,7 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
         }
         // (wave 0 always has a slice: it has seen every split's words)
         if (r == 0) {
-            if (tid == 0 && !a.epoch) a.counters[kvh] = ep;
+            if (tid == 0 && a.counters && !a.epoch) a.counters[kvh] = ep;   // (counters mode only)
             write_q();
         }
         return;
@@ -1344,14 +1384,14 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
 #pragma unroll
             for (int k = 0; k < KS; k++)
                 done = done && (wid + NW * k >= nsplit ||
-                                ((unsigned)(wo[k] >> 32) == ep && (unsigned)(wmx[k] >> 32) == ep &&
-                                 (unsigned)(wsm[k] >> 32) == ep));
+                                ((unsigned)(wo[k] >> 32) == epw && (unsigned)(wmx[k] >> 32) == epw &&
+                                 (unsigned)(wsm[k] >> 32) == epw));
             if (done) break;
             // (bounded, about 0.2 s: a merger may wait for blocks dispatched
             // after it, which take the CU slots the other blocks free as
             // they finish; kernels of other streams holding the CUs only
             // delay that)
-            if (spins == (1 << 22)) {
+            if (spins == lim) {
                 if (a.err) *a.err = 1u;
                 break;
             }
@@ -1390,7 +1430,7 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
     // (the last split's block) every split's block has read the counter
     // and q: the next launch's epoch base (stream order), q written back
     if (r == 0) {
-        if (tid == 0 && !a.epoch) a.counters[kvh] = ep;
+        if (tid == 0 && a.counters && !a.epoch) a.counters[kvh] = ep;   // (counters mode only)
         write_q();
     }
 }
@@ -1402,6 +1442,17 @@ __global__ void __launch_bounds__(512) attn_dec_kernel(const AttnArgs a) {
 template <int HD, int G, int PW, bool IL>
 __global__ void __launch_bounds__(512) attn_rope_kernel(const AttnArgs a, const AttnRope r) {
     attn_dec_body<HD, G, PW, IL ? 1 : 2>(a, &r);
+}
+
+// The step state of the next decode launch (token, position); the error word
+// is cleared only with reset_err, so a bounded wait that ran out in an
+// earlier launch of the same call stays visible to the host.
+__global__ void set_step_kernel(StepState* st, int token, int pos, int reset_err) {
+    st->token = token;
+    st->pos = pos;
+    st->gen_count = 0;
+    st->margin_bits = 0;
+    if (reset_err) st->err = 0u;
 }
 
 __global__ void embed_kernel(const uint16_t* embed, const int* token, float* x, int hidden,
@@ -3485,7 +3536,8 @@ static int attn_mergers(int blocks) {
 hipError_t launch_rope_attention(const AttnArgs& a, const float* k, const float* v, int interleaved,
                                  const float2* cs, hipStream_t st) {
     const int G = a.n_kv > 0 ? a.n_heads / a.n_kv : 0;
-    if (a.pos_dev || a.ntok > 1 || !a.ws || !a.epoch || !(G == 1 || G == 2 || G == 4) || !(a.hd == 64 || a.hd == 128) ||
+    if (a.pos_dev || a.ntok > 1 || !a.ws || (a.max_splits > 1 && !a.epoch && !a.dep) || !(G == 1 || G == 2 || G == 4) ||
+        !(a.hd == 64 || a.hd == 128) ||
         !(a.chunk == 64 || a.chunk == 128 || a.chunk == 256) || a.max_splits > kAttnDecSplits)
         return hipErrorNotSupported;
     AttnRope r{};
@@ -3518,13 +3570,26 @@ size_t attention_ws_bytes(int n_kv, int max_splits, int group, int hd) {
     return (size_t)n_kv * max_splits * group * (2 + hd) * 8;
 }
 
+size_t attention_ws_bytes_upto(int n_kv, int group, int hd, int max_ctx) {
+    int splits = 1;
+    for (int n = 1; n <= max_ctx; n++) {
+        const int c = attention_chunk(n, n_kv), s = (n + c - 1) / c;
+        if (s > splits) splits = s;
+    }
+    return attention_ws_bytes(n_kv, splits, group, hd);
+}
+
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
     // the merging block holds every split's (max, sum) in its 256-entry
     // score buffer
-    if (a.max_splits < 1 || a.max_splits > 256 || a.chunk > 256 || (!a.counters && !a.epoch) || !a.ws)
+    if (a.max_splits < 1 || a.max_splits > 256 || a.chunk > 256 || !a.ws ||
+        (a.max_splits > 1 && !a.counters && !a.epoch && !a.dep))
         return hipErrorInvalidValue;
     const int nt = a.ntok > 1 ? a.ntok : 1;
     if (nt > 1 && (!a.epoch || a.pos_dev)) return hipErrorInvalidValue;
+    // the device epoch word counts every block's arrival: no block may leave
+    // before it (a device position lets blocks past the context leave early)
+    if (a.dep && (a.pos_dev || nt > 1 || a.epoch || a.counters)) return hipErrorInvalidValue;
     const int G = a.n_heads / a.n_kv;
     // one token, G <= 4, head dim 64 / 128: the matrix-core kernel
     if (nt == 1 && (G == 1 || G == 2 || G == 4) && (a.hd == 64 || a.hd == 128) &&
@@ -3577,6 +3642,11 @@ hipError_t launch_embed(const uint16_t* embed, const int* token_dev, float* x, i
     const int n = hidden > nclear ? hidden : nclear;
     hipLaunchKernelGGL(embed_kernel, dim3((n + 255) / 256), dim3(256), 0, st, embed, token_dev, x, hidden, clear,
                        nclear, epoch);
+    return hipGetLastError();
+}
+
+hipError_t launch_set_step(StepState* stt, int token, int pos, int reset_err, hipStream_t st) {
+    hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, st, stt, token, pos, reset_err);
     return hipGetLastError();
 }
 

@@ -1,8 +1,10 @@
 // gsd_noalloc.hip -- gsdh_gqa_attention_noalloc: the decode attention twin for
 // callers that cannot allocate device memory (HIP graph capture, serving
-// loops, harnesses that forbid hipMalloc).  The split partials that
-// gsdh_gqa_attention keeps in a workspace it allocates live here in a
-// file-scope device array instead.
+// loops, harnesses that forbid hipMalloc).  Its split partials live in a
+// file-scope device array.  The operator twins gsdh_gqa_attention and
+// gsdh_rope_store_gqa_attention use the same array on streams that have no
+// workspace of their own (gsdh_attention_workspace_create), so they allocate
+// nothing either.
 #include <mutex>
 
 #include "gsd_internal.h"
@@ -12,25 +14,105 @@ using namespace gsd;
 
 namespace {
 
-// The split partial words of one launch (AttnArgs::ws).  Each GPU holds its
-// own copy until the process ends; host code reaches it only through the
-// address hipGetSymbolAddress returns on that device (NoAllocDev::ptr),
-// never through the array's name.
+// A 256-byte header (the device epoch word at byte 0, the error word at
+// byte 8) and the split partial words of one launch (AttnArgs::ws).  Each
+// GPU holds its own copy until the process ends, zero from the start; host
+// code reaches it only through the address hipGetSymbolAddress returns on
+// that device (NoAllocDev::ptr), never through the array's name.
 constexpr size_t kScratchBytes = 8u << 20;
 static __device__ __align__(256) unsigned long long scratch[kScratchBytes / 8];
 
-// Per device: the scratch address and the epoch of the last launch.  The
-// array is cleared by a fill kernel before its first launch; every launch
-// takes the next epoch, so words of earlier calls (of any shape) never match.
+// Per device: the scratch address (set once, with that device current).
+// Nothing else is kept on the host: each launch takes its epoch from the
+// header on the device, so graph replays of a captured call and calls of
+// any shape never read one another's words.
 struct NoAllocDev {
     unsigned long long* ptr = nullptr;
-    unsigned epoch = 0;
 };
 constexpr int kMaxDev = 64;
 std::mutex g_mu;
 NoAllocDev g_dev[kMaxDev];
 
+// The scratch of the current device (its address on first use).
+int scratch_ptr(hipStream_t stream, unsigned long long** out, const char* who) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail((int)e, "%s: hipGetDevice: %s", who, hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDev) return fail(-1, "%s: device %d beyond %d", who, dev, kMaxDev);
+    std::lock_guard<std::mutex> lk(g_mu);
+    NoAllocDev& d = g_dev[dev];
+    if (!d.ptr) {
+        // once per device, with that device current: the device address of
+        // this GPU's copy of the array
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return fail((int)e, "%s: hipGetSymbolAddress: %s", who, hipGetErrorString(e));
+        if (!p) return fail(-1, "%s: no device address for the scratch array", who);
+        // the array starts at zero (static storage); outside graph capture
+        // it is cleared once more by a fill kernel, stream-ordered before
+        // the first launch that uses it
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        e = hipStreamIsCapturing(stream, &cs);
+        if (e != hipSuccess) return fail((int)e, "%s: hipStreamIsCapturing: %s", who, hipGetErrorString(e));
+        if (cs == hipStreamCaptureStatusNone) {
+            e = launch_fill_u32(static_cast<unsigned*>(p), 0u, kScratchBytes / 4, stream);
+            if (e != hipSuccess) return fail((int)e, "%s: clearing the scratch: %s", who, hipGetErrorString(e));
+        }
+        d.ptr = static_cast<unsigned long long*>(p);
+    }
+    *out = d.ptr;
+    return 0;
+}
+
 }  // namespace
+
+namespace gsd {
+
+// A one-token attention launch on the current device's scratch: fills a.ws /
+// a.dep / a.err (a.max_splits set) or fails for partials beyond it.
+int attention_static_ws(hipStream_t stream, AttnArgs& a, int group, const char* who) {
+    const size_t need = attention_ws_bytes(a.n_kv, a.max_splits, group, a.hd);
+    if (need > kScratchBytes - kAttnWsHeader)
+        return fail(-1,
+                    "%s: %zu bytes of split partials (%d KV heads x %d splits x %d heads x %d dims) exceed the "
+                    "%zu-byte static scratch; give the stream a workspace (gsdh_attention_workspace_create)",
+                    who, need, a.n_kv, a.max_splits, group, a.hd, kScratchBytes - kAttnWsHeader);
+    unsigned long long* p = nullptr;
+    const int rc = scratch_ptr(stream, &p, who);
+    if (rc) return rc;
+    attention_use_ws(a, p);
+    return 0;
+}
+
+// Reads and clears the error word of the current device's scratch (after the
+// caller synchronised): 1 when a merge's bounded wait ran out since the last
+// check.  Nothing to check before the scratch's first use.
+int attention_static_error(int* was_set) {
+    *was_set = 0;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail((int)e, "hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDev) return 0;
+    unsigned long long* p = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        p = g_dev[dev].ptr;
+    }
+    if (!p) return 0;
+    unsigned* ew = reinterpret_cast<unsigned*>(p + 1);
+    unsigned v = 0;
+    e = hipMemcpy(&v, ew, 4, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return fail((int)e, "reading the attention error word: %s", hipGetErrorString(e));
+    if (v) {
+        const unsigned zero = 0;
+        e = hipMemcpy(ew, &zero, 4, hipMemcpyHostToDevice);
+        if (e != hipSuccess) return fail((int)e, "clearing the attention error word: %s", hipGetErrorString(e));
+        *was_set = 1;
+    }
+    return 0;
+}
+
+}  // namespace gsd
 
 extern "C" int gsdh_gqa_attention_noalloc(void* stream, const float* q, const uint16_t* k_cache,
                                           const uint16_t* v_cache, float* attn_out, int layer_idx, int pos,
@@ -49,37 +131,10 @@ extern "C" int gsdh_gqa_attention_noalloc(void* stream, const float* q, const ui
     a.sm_scale = sm_scale;
     a.chunk = attention_chunk(n, n_kv_heads);
     a.max_splits = (n + a.chunk - 1) / a.chunk;
-    const size_t need = attention_ws_bytes(n_kv_heads, a.max_splits, G, head_dim);
-    if (need > kScratchBytes)
-        return fail(-1,
-                    "attention_noalloc: %zu bytes of split partials (%d KV heads x %d splits x %d heads x %d dims) "
-                    "exceed the %zu-byte static scratch; use gsdh_gqa_attention",
-                    need, n_kv_heads, a.max_splits, G, head_dim, kScratchBytes);
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return fail((int)e, "attention_noalloc: hipGetDevice: %s", hipGetErrorString(e));
-    if (dev < 0 || dev >= kMaxDev) return fail(-1, "attention_noalloc: device %d beyond %d", dev, kMaxDev);
-    std::lock_guard<std::mutex> lk(g_mu);
-    NoAllocDev& d = g_dev[dev];
-    if (!d.ptr) {
-        // once per device, with that device current: the device address of
-        // this GPU's copy of the array
-        void* p = nullptr;
-        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        if (e != hipSuccess) return fail((int)e, "attention_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
-        if (!p) return fail(-1, "attention_noalloc: no device address for the scratch array");
-        d.ptr = static_cast<unsigned long long*>(p);
-        d.epoch = 0xFFFFFFF0u;   // cleared below before the first launch
-    }
-    if (d.epoch >= 0xFFFFFFF0u) {   // first call on the device, or the epoch about to wrap
-        e = launch_fill_u32(reinterpret_cast<unsigned*>(d.ptr), 0u, kScratchBytes / 4, static_cast<hipStream_t>(stream));
-        if (e != hipSuccess) return fail((int)e, "attention_noalloc: clearing the scratch: %s", hipGetErrorString(e));
-        d.epoch = 0;
-    }
-    a.ws = d.ptr;
-    a.counters = nullptr;
-    a.epoch = ++d.epoch;
-    e = launch_attention(a, static_cast<hipStream_t>(stream));
+    attention_test_knobs(a);
+    const int rc = attention_static_ws(static_cast<hipStream_t>(stream), a, G, "attention_noalloc");
+    if (rc) return rc;
+    const hipError_t e = launch_attention(a, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail((int)e, "attention_noalloc: %s", hipGetErrorString(e));
     return 0;
 }

@@ -16,9 +16,14 @@ HIP_LIB = os.path.join(PKG_DIR, "libgsdhip.so")
 PACK_LIB = os.path.join(PKG_DIR, "libgsdpack.so")
 ARCH = os.environ.get("GSD_OFFLOAD_ARCH", "gfx950")
 
-HIPCC_FLAGS = ["-O3", "-fPIC", "-shared", "-std=c++17", f"--offload-arch={ARCH}",
+HIPCC_FLAGS = ["-O3", "-fPIC", "-std=c++17", f"--offload-arch={ARCH}",
                # packed fp32 VALU ops are disabled for all device code
                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+               # a single-lane device atomic keeps its own wait: the atomic
+               # optimizer would turn it into a wave-wide form whose result
+               # is needed (s_waitcnt vmcnt(0)) right after it, ahead of the
+               # loads the attention kernels issue behind their arrival
+               "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
                "-Wall", "-Wno-unused-function"]
 GXX_FLAGS = ["-O2", "-fPIC", "-shared", "-std=c++17", "-fopenmp", "-ffp-contract=off", "-Wall"]
 
@@ -39,9 +44,16 @@ def _run(cmd):
 
 
 def build_hip(out: str = HIP_LIB) -> str:
+    """Each source compiled on its own (in parallel), then linked."""
+    import concurrent.futures
+    import tempfile
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
     tmp = out + ".tmp"
-    _run([_hipcc()] + HIPCC_FLAGS + srcs + ["-o", tmp])
+    with tempfile.TemporaryDirectory(prefix="gsdhip_") as d:
+        objs = [os.path.join(d, os.path.basename(s) + ".o") for s in srcs]
+        with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
+            list(ex.map(lambda so: _run([_hipcc()] + HIPCC_FLAGS + ["-c", so[0], "-o", so[1]]), zip(srcs, objs)))
+        _run([_hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}"] + objs + ["-o", tmp])
     os.replace(tmp, out)
     return out
 

@@ -25,6 +25,13 @@ SIGNATURES = {
     "gsdh_memcpy_h2d": [vp, vp, u64, vp],
     "gsdh_memcpy_d2h": [vp, vp, u64, vp],
     "gsdh_stream_sync": [vp],
+    "gsdh_stream_create": [ctypes.POINTER(vp)],
+    "gsdh_stream_destroy": [vp],
+    "gsdh_stream_begin_capture": [vp],
+    "gsdh_stream_end_capture": [vp, ctypes.POINTER(vp)],
+    "gsdh_graph_replay": [vp, vp],
+    "gsdh_attention_workspace_create": [vp, i32, i32, i32, i32],
+    "gsdh_attention_workspace_destroy": [vp],
     "gsdh_stream_copy": [vp, vp, vp, u64],
     "gsdh_rmsnorm": [vp, vp, vp, vp, i32, f32],
     "gsdh_vec_add": [vp, vp, vp, vp, i32],
@@ -47,6 +54,7 @@ SIGNATURES = {
     "gsdh_generate_greedy": [vp, vp, i32, i32, i32, vp, vp],
     "gsdh_model_run_linear": [vp, i32, i32],
     "gsdh_model_matmul": [vp, i32, i32, vp, i32, vp],
+    "gsdh_matmul_plan": [i32, i32, i32, ctypes.POINTER(i32), ctypes.POINTER(i32), ctypes.POINTER(i32)],
     "gsdh_model_read_codes": [vp, i32, i32, vp],
     "gsdh_model_capture_begin": [vp],
     "gsdh_model_capture_end": [vp, ctypes.POINTER(vp)],
@@ -61,6 +69,7 @@ SIGNATURES = {
     "gsdh_model_set_prefill": [vp, i32],
 }
 RESTYPES = {"gsdh_model_device_bytes": (u64, [vp]), "gsdh_model_stream": (vp, [vp]),
+            "gsdh_attention_workspace_bytes": (u64, [i32, i32, i32, i32]),
             "gsdh_model_engine": (i32, [vp]),
             "gsdh_last_error": (ctypes.c_char_p, [])}
 

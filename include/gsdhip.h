@@ -45,7 +45,22 @@ int gsdh_malloc(void** ptr, uint64_t nbytes);
 int gsdh_free(void* ptr);
 int gsdh_memcpy_h2d(void* dst, const void* src, uint64_t nbytes, void* stream);
 int gsdh_memcpy_d2h(void* dst, const void* src, uint64_t nbytes, void* stream);
+/* Waits for the stream; then returns -2 (text in gsdh_last_error) when a
+ * stand-alone attention launch on this device (the gsdh_*attention* twins
+ * below) gave up a bounded wait for a split's partials since the last check,
+ * whose output is then undefined: like a kernel fault, the asynchronous
+ * failure surfaces at the next synchronisation (the reference raises
+ * RuntimeError on launch errors, run_gpu_native_chat.py:648-649). */
 int gsdh_stream_sync(void* stream);
+/* Streams and graph capture for callers without another HIP binding (no
+ * reference counterpart; the reference's single OpenCL queue is
+ * run_gpu_native_chat.py:521).  Streams are non-blocking and of the default
+ * priority; gsdh_stream_destroy also frees the stream's attention workspace. */
+int gsdh_stream_create(void** stream_out);
+int gsdh_stream_destroy(void* stream);
+int gsdh_stream_begin_capture(void* stream);
+int gsdh_stream_end_capture(void* stream, void** graph_exec_out);
+int gsdh_graph_replay(void* graph_exec, void* stream);
 /* Plain device-to-device copy by a 16-byte streaming kernel (nbytes % 16 == 0);
  * used to calibrate HBM traffic counters against a known byte count. */
 int gsdh_stream_copy(void* stream, void* dst, const void* src, uint64_t nbytes);
@@ -89,10 +104,27 @@ int gsdh_rope_and_store_kv(void* stream, float* q, const float* k, const float* 
 
 /* gsd_cpu_gqa_attention (gsd_lq_cpu_engine.c:264-330): softmax(q.K/scale)V
  * over cached positions 0..pos, split over the context (flash-decoding);
- * head_dim must be 64, 128 or 256; n_heads/n_kv_heads must be 1, 2, 4 or 8. */
+ * head_dim must be 64, 128 or 256; n_heads/n_kv_heads must be 1, 2, 4 or 8.
+ * Allocates nothing: the split partials go to the stream's workspace when
+ * gsdh_attention_workspace_create made one, else to the library's static
+ * per-GPU scratch (the limit of gsdh_gqa_attention_noalloc below; calls on
+ * that scratch that overlap on one GPU race).  Each launch takes its epoch
+ * on the device, so a captured call replays correctly. */
 int gsdh_gqa_attention(void* stream, const float* q, const uint16_t* k_cache,
                        const uint16_t* v_cache, float* attn_out, int layer_idx, int pos,
                        int n_heads, int n_kv_heads, int head_dim, int max_seq_len, float sm_scale);
+
+/* A workspace of its own for the attention twins on `stream` (calls on
+ * different streams may then overlap), sized for contexts up to max_seq_len
+ * positions of this head shape; allocated here, once, and freed by
+ * gsdh_attention_workspace_destroy (or gsdh_stream_destroy).  The caller
+ * owns its lifetime, as it owns every buffer of the reference's engine
+ * (gsd_lq_cpu_runtime.py:91-108).  No reference counterpart.
+ * gsdh_attention_workspace_bytes: its size (0 for an invalid shape). */
+uint64_t gsdh_attention_workspace_bytes(int n_kv_heads, int n_heads, int head_dim, int max_seq_len);
+int gsdh_attention_workspace_create(void* stream, int n_kv_heads, int n_heads, int head_dim,
+                                    int max_seq_len);
+int gsdh_attention_workspace_destroy(void* stream);
 
 /* gsd_cpu_rope_and_store_kv followed by gsd_cpu_gqa_attention
  * (gsd_lq_cpu_engine.c:185-330), the two calls of one decode step's
@@ -111,15 +143,19 @@ int gsdh_rope_store_gqa_attention(void* stream, float* q, const float* k, const 
 /* gsd_cpu_gqa_attention for callers that cannot allocate device memory (code
  * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
  * No counterpart in the reference.  Same arguments and results as
- * gsdh_gqa_attention, but the split partials live in a static 8 MiB device
- * array of the library (one per GPU, kept until the process ends), so the
- * call allocates nothing.  Limit: n_kv_heads * splits * (n_heads/n_kv_heads)
- * * (head_dim + 2) * 8 bytes <= 8 MiB, splits = ceil((pos+1) / chunk) with
- * chunk = 256 up to 256 positions, else the smallest of 64, 128, 256 that is
- * >= (pos+1) * n_kv_heads / 256 (256 at most); e.g. 8 KV heads x 4 x 128
- * dims up to 32 splits (context 8192) use 1.1 MB.  Larger
- * calls fail with an error.  All calls on one GPU share the array: calls
- * that overlap on one GPU (different streams, or threads) race. */
+ * gsdh_gqa_attention, but the split partials always live in a static 8 MiB
+ * device array of the library (one per GPU, kept until the process ends),
+ * so the call allocates nothing; each launch takes its epoch from a word in
+ * that array on the device, so graph replays of a captured call are
+ * correct.  Limit: n_kv_heads * splits * (n_heads/n_kv_heads) * (head_dim +
+ * 2) * 8 bytes <= 8 MiB - 256, where n = pos + 1 positions split as: one
+ * split up to 128 positions; beyond, chunks of the smallest of 64, 128, 256
+ * that is >= ceil(n * n_kv_heads / 256) (256 at most), splits = ceil(n /
+ * chunk).  E.g. 8 KV heads x 4 x 128 dims at context 8192 (32 splits of
+ * 256) use 1.1 MB.  Larger calls fail with an error.  All calls on one GPU
+ * share the array (with gsdh_gqa_attention on streams without a workspace):
+ * calls that overlap on one GPU (different streams, or threads) race.  A
+ * merge that gave up waiting is reported by gsdh_stream_sync. */
 int gsdh_gqa_attention_noalloc(void* stream, const float* q, const uint16_t* k_cache,
                                const uint16_t* v_cache, float* attn_out, int layer_idx, int pos,
                                int n_heads, int n_kv_heads, int head_dim, int max_seq_len,
@@ -243,6 +279,12 @@ int gsdh_model_set_prefill(gsdh_model* m, int batched);
  * M <= 512 per call; the staging lives in the model's workspace (sized at
  * finalize), so the call allocates nothing and can be graph-captured. */
 int gsdh_model_matmul(gsdh_model* m, int layer, int slot, const uint16_t* X, int M, float* Y);
+/* The tiling gsdh_model_matmul and the batched prefill use for M tokens of a
+ * rows x cols tensor on the current device: token groups of 16 per block
+ * (*tg: 1, 2, 4, 8), row blocks of 16 per wave (*rbw) and column splits
+ * (*nsplit).  A diagnostic (tests name the tiles they run); no reference
+ * counterpart. */
+int gsdh_matmul_plan(int M, int rows, int cols, int* tg, int* rbw, int* nsplit);
 
 /* The codes of packed tensor (layer, slot) as the device holds them, decoded
  * back to the file's u8 [rows][cols/2] order on the device by the same tile

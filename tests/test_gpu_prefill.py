@@ -67,15 +67,89 @@ def turbo_7b():
     model.close()
 
 
-@pytest.mark.parametrize("name,M", [("attn_q", 16), ("ffn_gate", 128), ("ffn_down", 16), ("attn_k", 512),
-                                    ("attn_output", 37)])
+def plan(lib, M, rows, cols):
+    tg, rbw, ns = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    lib.gsdh_matmul_plan(M, rows, cols, ctypes.byref(tg), ctypes.byref(rbw), ctypes.byref(ns))
+    return tg.value, rbw.value, ns.value
+
+
+def group_tokens(M):
+    """One token in every 16-token group (a different lane of each), and the
+    last token: every token group of a tile and every A-fragment row."""
+    return sorted({16 * g + (g % 16) for g in range((M + 15) // 16) if 16 * g + (g % 16) < M} | {M - 1})
+
+
+C5_TENSORS = ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")
+
+
+# Every (tensor, M) pair of the C5 benchmark (the 7 Turbo tensors of a
+# Mistral-7B layer at M = 16 / 128 / 512), whose plans on a 256-CU MI355X
+# are: one token group with 8, 5 or 16 column splits (M = 16), one group
+# unsplit (q / o / down at 128, k / v at 512), four groups (gate / up at
+# 128, q / o / down at 512), eight groups with two row blocks per wave
+# (gate / up at 512); plus a padded token count.  Every output row of each
+# checked token is compared, so every row block of every wave is.
+@pytest.mark.parametrize("M", [16, 128, 512])
+@pytest.mark.parametrize("name", C5_TENSORS)
 def test_matmul_7b_turbo(turbo_7b, name, M):
     bank, model = turbo_7b
-    banner(f"prefill matmul 7B turbo {name} M={M}")
     t = bank.packed[(0, name)]
-    toks = sorted({0, 1, M // 2, M - 1})
-    worst = check(model, t, 0, SLOTS[name], M, seed=7 + M, tokens=toks)
+    pl = plan(model.cl.lib, M, t["rows"], t["cols"])
+    banner(f"prefill matmul 7B turbo {name} M={M} plan (tg, rbw, nsplit) = {pl}")
+    worst = check(model, t, 0, SLOTS[name], M, seed=7 + M + SLOTS[name], tokens=group_tokens(M))
     print(f"[gpu-test] worst rel L2 {worst:.2e}", flush=True)
+
+
+def test_matmul_7b_turbo_padded(turbo_7b):
+    bank, model = turbo_7b
+    banner("prefill matmul 7B turbo attn_output M=37")
+    check(model, bank.packed[(0, "attn_output")], 0, SLOTS["attn_output"], 37, seed=44, tokens=group_tokens(37))
+
+
+def test_matmul_7b_turbo_plans(turbo_7b):
+    """The C5 pairs above reach every tile shape of the batched kernel."""
+    bank, model = turbo_7b
+    seen = {plan(model.cl.lib, M, *layer_shape(n)) for n in C5_TENSORS for M in (16, 128, 512)}
+    assert {(8, 2, 1), (4, 1, 1), (1, 1, 1)} <= seen, seen
+    assert any(s > 1 for _, _, s in seen), seen
+
+
+def layer_shape(name):
+    H, F, KV = 4096, 14336, 1024
+    return {"attn_q": (H, H), "attn_k": (KV, H), "attn_v": (KV, H), "attn_output": (H, H),
+            "ffn_gate": (F, H), "ffn_up": (F, H), "ffn_down": (H, F)}[name]
+
+
+def test_prefill_7b_turbo_chunks(turbo_7b):
+    """The batched prefill forward of the 7B Turbo layer (32 / 8 heads of
+    128, ffn 14336, vocab 32768): 130 tokens (a 128-token chunk: gate / up on
+    four-group tiles, q / o / down on one group; then a 2-token chunk on
+    column-split tiles), then 64 more after that prefix (gate / up on
+    two-group tiles), against the oracle's token-by-token forward."""
+    import bench
+    bank, model = turbo_7b
+    banner("batched prefill 7B turbo: 130 tokens, then 64 more")
+    lib = model.cl.lib
+    for M in (128, 2, 64):
+        print(f"[gpu-test] chunk {M}: gate/up plan {plan(lib, M, 14336, 4096)}, q plan {plan(lib, M, 4096, 4096)}, "
+              f"down plan {plan(lib, M, 4096, 14336)}", flush=True)
+    ref = O.OracleModel(bench.BankSource(bank, 1), kind="port", max_seq_len=256, rope_interleaved=1)
+    toks = np.random.default_rng(130).integers(0, model.vocab_size, 194).tolist()
+    got = model.prefill(toks[:130], 0)
+    want = None
+    for pos in range(130):
+        want = ref.forward_token(toks[pos], pos, return_logits=pos == 129)
+    e = rel_l2(got, want)
+    print(f"[prefill-parity] 7B turbo 130 tokens: last-position logits rel L2 {e:.2e}", flush=True)
+    assert e < 1e-3
+    _kv_close(model, ref, [0], [0, 64, 127, 128, 129])
+    got = model.prefill(toks[130:], 130)
+    for pos in range(130, 194):
+        want = ref.forward_token(toks[pos], pos, return_logits=pos == 193)
+    e = rel_l2(got, want)
+    print(f"[prefill-parity] 7B turbo +64 tokens: last-position logits rel L2 {e:.2e}", flush=True)
+    assert e < 1e-3
+    _kv_close(model, ref, [0], [130, 161, 193])
 
 
 def _small_model(spec):
