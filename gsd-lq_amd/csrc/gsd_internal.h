@@ -224,14 +224,17 @@ struct AttnArgs {
     unsigned* err;            // set to 1 when a wait for a partial runs out (may be null)
     unsigned epoch;
     // Third epoch source (epoch == 0, counters == null; one-token launches
-    // with a host position): a device word, high half the epoch of the last
-    // launch on the workspace, low half an arrival count.  Every block adds
-    // one to it with a single atomic at its start (the old value gives the
-    // epoch; this launch tags its words with the next, 0 skipped), and the
-    // last block to arrive stores (next epoch << 32 | 0).  Each launch thus
-    // takes a new epoch on the device, also when a captured graph replays
-    // it, and words of earlier launches of any shape never match.  Zero at
-    // allocation.
+    // with a host position): device words dep[0] = the epoch of the last
+    // launch on the workspace (low half), dep[2] = KV heads merged in this
+    // launch.  Every block reads dep[0] at its start and tags its words with
+    // the next epoch (0 skipped); the merging block of each KV head's last
+    // split, once every split's words are in (so every block of the head has
+    // read dep[0]), adds one to dep[2], and the last head to do so clears
+    // dep[2] and stores the new epoch.  Each launch thus takes a new epoch on
+    // the device, also when a captured graph replays it, and words of earlier
+    // launches of any shape never match.  n_kv atomics per launch: one per
+    // block on a single word (an arrival count) serialised for microseconds.
+    // Zero at allocation.
     unsigned long long* dep;
     // merging blocks: polling rounds before a wait counts as timed out
     // (0: the default bound)
@@ -275,8 +278,9 @@ inline int attention_chunk(int n_ctx, int n_kv) {
 int fail(int code, const char* fmt, ...);
 size_t attention_ws_bytes(int n_kv, int max_splits, int group, int hd);
 // Workspace of a stand-alone one-token attention launch (the operator
-// twins): a 256-byte header (AttnArgs::dep at byte 0, the error word at byte
-// 8), then the split words.  Zero at allocation; never cleared after.
+// twins): a 256-byte header (AttnArgs::dep: the epoch word at byte 0 and the
+// head count at byte 16; the error word at byte 8), then the split words.
+// Zero at allocation; never cleared after.
 constexpr size_t kAttnWsHeader = 256;
 // Split words a workspace must hold for every context of 1 .. max_ctx
 // positions (the chunking of attention_chunk), header excluded.

@@ -614,21 +614,14 @@ __global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int sub = lane % LPP, prow = lane / LPP;
     const int kvh = blockIdx.x;
-    // the epoch (used at the end).  Device word (a.dep): every block of the
-    // grid arrives before anything else, and the last to arrive advances it
+    // the epoch (used at the end).  Device word (a.dep): the epoch of the
+    // last launch on the workspace, read by every wave (a vector value: its
+    // wait falls at the first use, at the end); this launch's is the next
+    // (0 skipped)
     unsigned ep0;
     if (a.dep) {
-        __shared__ unsigned s_ep0;
-        if (tid == 0) {
-            const unsigned long long t = __hip_atomic_fetch_add(a.dep, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            unsigned e = (unsigned)(t >> 32) + 1u;
-            if (e == 0u) e = 1u;
-            if ((unsigned)t == gridDim.x * gridDim.y * gridDim.z - 1u)
-                __hip_atomic_store(a.dep, (unsigned long long)e << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            s_ep0 = e - 1u;
-        }
-        __syncthreads();
-        ep0 = s_ep0;
+        const unsigned e = (unsigned)__hip_atomic_load(a.dep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ep0 = e == 0xFFFFFFFFu ? 0u : e;
     } else {
         ep0 = a.epoch ? a.epoch - 1u : (a.counters ? a.counters[kvh] : 0u);
     }
@@ -819,6 +812,7 @@ __global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
     };
     constexpr int SB = kAttnStage / HD;       // splits per staging batch
     constexpr int MAXI = kAttnStage / NT;     // staged words per thread
+    unsigned long long hcnt = ~0ull;          // a.dep: the heads done before this one
     for (int g = back; g < G; g += nsplit) {
         __syncthreads();   // (LDS reuse across heads)
         // one round trip: the (max, sum) words of every split and the first
@@ -858,6 +852,10 @@ __global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
         }
         stage_put(0);
         __syncthreads();
+        // (a.dep: every split's words of the head are in, so every block of
+        // the head has read the epoch: the head counts itself done)
+        if (a.dep && back == 0 && g == 0 && tid == 0)
+            hcnt = __hip_atomic_fetch_add(a.dep + 2, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (wid == 0) {
             float M = -INFINITY;
             for (int sp = lane; sp < nsplit; sp += 64) M = fmaxf(M, sc[0][sp]);
@@ -885,6 +883,12 @@ __global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
     }
     // the next launch's epoch base (stream order; the counters mode only)
     if (back == 0 && tid == 0 && a.counters && !a.epoch) a.counters[kvh] = ep;
+    // a.dep: the last KV head done advances the epoch (every block of the
+    // launch has read it by then) and clears the count
+    if (a.dep && back == 0 && tid == 0 && hcnt == (unsigned long long)a.n_kv - 1ull) {
+        __hip_atomic_store(a.dep + 2, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.dep, (unsigned long long)ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 // ------------------------------------------------------------------------
@@ -975,10 +979,10 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
     // the head's counter once it has every split's words, so each block
     // must have read it by then (a block that read it late, after a fast
     // merger's update, would tag its words with the next launch's epoch).
-    // Device word (a.dep): the block's arrival goes out first, its result
-    // is taken at the block combine below
-    unsigned long long dtk = 0;
-    if (a.dep && tid == 0) dtk = __hip_atomic_fetch_add(a.dep, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Device word (a.dep): the epoch of the last launch on the workspace,
+    // loaded by every wave first of all and taken at the block combine
+    unsigned dlast = 0;
+    if (a.dep) dlast = (unsigned)__hip_atomic_load(a.dep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     unsigned ep = a.epoch ? a.epoch : (a.dep || a.max_splits == 1 ? 0u : a.counters[kvh] + 1u);
 
     // q (A operand source): lane l, head m = l & 15 (m < G), dims
@@ -1224,18 +1228,11 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
             op[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
         }
     }
-    __shared__ unsigned s_ep;
-    if (a.dep && tid == 0) {
-        // the epoch of the last launch on the workspace + 1 (0 skipped); the
-        // last block to arrive (every block has read the word) advances it
-        unsigned e = (unsigned)(dtk >> 32) + 1u;
-        if (e == 0u) e = 1u;
-        s_ep = e;
-        if ((unsigned)dtk == gridDim.x * gridDim.y - 1u)
-            __hip_atomic_store(a.dep, (unsigned long long)e << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (a.dep) {   // this launch's epoch: the next (0 skipped)
+        ep = (unsigned)__builtin_amdgcn_readfirstlane((int)dlast) + 1u;
+        if (ep == 0u) ep = 1u;
     }
     lds_barrier();
-    if (a.dep) ep = s_ep;
 
     // the block's (max, sum, o) per head: thread (g, d), waves in order
     const int g = tid / HD, d = tid % HD;
@@ -1289,6 +1286,15 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
     // the wait run out) and its bound
     const unsigned epw = ep + (unsigned)a.wait_skew;
     const int lim = a.spin_limit > 0 ? a.spin_limit : kAttnSpinLimit;
+    unsigned long long hcnt = ~0ull;   // a.dep: the heads done before this one
+    // a.dep: the last KV head done advances the epoch (every block of the
+    // launch has read it by then) and clears the count
+    auto head_done = [&]() {
+        if (a.dep && tid == 0 && hcnt == (unsigned long long)a.n_kv - 1ull) {
+            __hip_atomic_store(a.dep + 2, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(a.dep, (unsigned long long)ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    };
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc(wsk, (short)0, nsplit * G * WPH * 8, 0x00020000);
     if (nsplit <= NW && nm < NSL) {
@@ -1329,6 +1335,10 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
                 }
                 __builtin_amdgcn_s_sleep(2);
             }
+            // (a.dep: wave 0 of the last split's block has seen every
+            // split's words, so every block of the head has read the epoch)
+            if (a.dep && r == 0 && tid == 0)
+                hcnt = __hip_atomic_fetch_add(a.dep + 2, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             float M2 = -INFINITY;
 #pragma unroll
             for (int s = 0; s < NW; s++)
@@ -1346,6 +1356,7 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
         // (wave 0 always has a slice: it has seen every split's words)
         if (r == 0) {
             if (tid == 0 && a.counters && !a.epoch) a.counters[kvh] = ep;   // (counters mode only)
+            head_done();
             write_q();
         }
         return;
@@ -1412,6 +1423,10 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
         mlo[(1 * NW + wid) * 64 + lane] = lp;
         mlo[(2 * NW + wid) * 64 + lane] = op;
         lds_barrier();
+        // (a.dep: every wave has seen its splits' words, so every block of
+        // the head has read the epoch)
+        if (a.dep && r == 0 && sl == 0 && tid == 0)
+            hcnt = __hip_atomic_fetch_add(a.dep + 2, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (wid == 0) {
             float M2 = mlo[lane];
 #pragma unroll
@@ -1431,6 +1446,7 @@ __device__ __forceinline__ void attn_dec_body(const AttnArgs& a, const AttnRope*
     // and q: the next launch's epoch base (stream order), q written back
     if (r == 0) {
         if (tid == 0 && a.counters && !a.epoch) a.counters[kvh] = ep;   // (counters mode only)
+        head_done();
         write_q();
     }
 }
