@@ -257,35 +257,26 @@ def bench_prefill(bank, ms=(16, 128, 512), reps=3):
 
 def bench_decode(bank, n_prompt=64, n_new=128):
     """Greedy decode tok/s of a 32-layer 7B-shaped model (layers are copies of
-    the bank's distinct layers, each copy its own HBM allocation), for the
-    default engine (a HIP graph of per-phase launches) and for the
-    one-launch-per-token persistent kernel; weight_GBs = packed weight bytes
+    the bank's distinct layers, each copy its own HBM allocation): one HIP
+    graph of per-phase launches per token; weight_GBs = packed weight bytes
     streamed per token x tok/s."""
     model = build_model(bank, 32, max_seq=n_prompt + n_new + 8)
     prompt = np.random.default_rng(4).integers(0, V, n_prompt).tolist()
     wbytes = 32 * bank.layer_bytes[0] + alg_bytes(bank.packed["lm"])
     out = {"n_prompt": n_prompt, "n_new": n_new, "weight_bytes_per_token": wbytes}
-    first = None
-    for eng in ("graph", "persistent"):
-        model.set_engine(eng)
-        model.generate_greedy(prompt[:8], 4)   # warm
-        t0 = time.time()
-        toks, _ = model.generate_greedy(prompt, n_new)
-        total = time.time() - t0
-        # decode-only rate: n_new steps after a 1-token prefill
-        t0 = time.time()
-        model.generate_greedy(prompt[:1], n_new)
-        dec = time.time() - t0
-        sfx = "" if eng == "graph" else "_persistent_engine"
-        out["decode_tok_s" + sfx] = round(n_new / dec, 1)
-        out["weight_GBs" + sfx] = round(wbytes * n_new / dec / 1e9, 1)
-        out["prompt_plus_decode_s" + sfx] = round(total, 3)
-        if first is None:
-            first = toks
-        else:
-            out["engines_agree"] = toks == first
+    model.generate_greedy(prompt[:8], 4)   # warm
+    t0 = time.time()
+    model.generate_greedy(prompt, n_new)
+    total = time.time() - t0
+    # decode-only rate: n_new steps after a 1-token prefill
+    t0 = time.time()
+    model.generate_greedy(prompt[:1], n_new)
+    dec = time.time() - t0
+    out["decode_tok_s"] = round(n_new / dec, 1)
+    out["weight_GBs"] = round(wbytes * n_new / dec / 1e9, 1)
+    out["frac_hbm"] = round(wbytes * n_new / dec / 1e9 / HBM_PEAK_GBS, 4)
+    out["prompt_plus_decode_s"] = round(total, 3)
     # the 64-token prompt alone: batched prefill vs one decode step per token
-    model.set_engine("graph")
     for batched, key in ((True, "prefill_batched"), (False, "prefill_token_by_token")):
         model.set_prefill(batched)
         model.prefill(prompt, 0, return_logits=False) if batched else None

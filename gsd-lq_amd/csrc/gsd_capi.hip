@@ -482,18 +482,6 @@ struct gsdh_model {
     hipGraphExec_t g_full = nullptr, g_prefill = nullptr;
     hipGraphExec_t g_full_s[kShortTiers] = {}, g_prefill_s[kShortTiers] = {};
     hipGraph_t capture_graph = nullptr;
-    // persistent token kernel (one launch per token): device layer table,
-    // hand-off words, per-block top-2 words and launch counters, and the
-    // graphs of its two variants (with / without the head)
-    TokArgs tok{};
-    TokLayer* tok_layers = nullptr;
-    HexSeg* tok_head = nullptr;
-    unsigned long long* tok_words = nullptr;
-    unsigned long long* tok_top = nullptr;
-    unsigned* tok_epoch = nullptr;
-    hipGraphExec_t gt_full = nullptr, gt_prefill = nullptr;
-    bool tok_ok = false;
-    int engine = GSDH_ENGINE_GRAPH;
     size_t dev_bytes = 0;
     bool finalized = false;
     std::vector<void*> allocs;
@@ -681,73 +669,9 @@ int issue_token(gsdh_model* m, bool with_head, int short_chunk) {
 }
 
 hipGraphExec_t token_graph(const gsdh_model* m, bool with_head, int pos) {
-    if (m->engine == GSDH_ENGINE_PERSISTENT) return with_head ? m->gt_full : m->gt_prefill;
     for (int t = 0; t < kShortTiers; t++)
         if (pos < kShortChunk[t]) return with_head ? m->g_full_s[t] : m->g_prefill_s[t];
     return with_head ? m->g_full : m->g_prefill;
-}
-
-// Persistent token kernel set-up: every tensor must share one codebook
-// radius and the shape must fit the kernel (tok_supported); otherwise the
-// model keeps the graph of per-phase launches only.
-int setup_token_kernel(gsdh_model* m) {
-    const auto& c = m->c;
-    const int radius = m->slot(0, GSDH_LM_HEAD).radius;
-    for (int l = 0; l < c.n_layers; l++)
-        for (int s = 0; s < 7; s++)
-            if (m->slot(l, s).radius != radius) return 0;
-    const int n_pts = 3 * radius * radius + 3 * radius + 1;
-    if (!tok_supported(n_pts, c.hidden, c.ffn, c.n_heads, c.n_kv_heads, c.head_dim)) return 0;
-    const int grid = tok_grid();
-    if (grid <= 0) return 0;
-    std::vector<TokLayer> tl((size_t)c.n_layers);
-    for (int l = 0; l < c.n_layers; l++) {
-        for (int s = 0; s < 7; s++) fill_seg(tl[l].w[s], m->slot(l, s), m, nullptr);
-        tl[l].norm[0] = m->norm(l, 0);
-        tl[l].norm[1] = m->norm(l, 1);
-    }
-    HexSeg head{};
-    fill_seg(head, m->slot(0, GSDH_LM_HEAD), m, m->logits);
-    const TokWords wo = tok_words(c.hidden, c.ffn, c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq_len);
-    int rc = 0;
-    auto A = [&](void** p, size_t n) { if (!rc) rc = dalloc(m, p, n); };
-    A((void**)&m->tok_layers, tl.size() * sizeof(TokLayer));
-    A((void**)&m->tok_head, sizeof(HexSeg));
-    A((void**)&m->tok_words, (size_t)c.n_layers * wo.total * 8);
-    A((void**)&m->tok_top, (size_t)grid * 4 * 8);
-    A((void**)&m->tok_epoch, (size_t)grid * 4);
-    if (rc) return rc;
-    HIPCHK(hipMemcpy(m->tok_layers, tl.data(), tl.size() * sizeof(TokLayer), hipMemcpyHostToDevice));
-    HIPCHK(hipMemcpy(m->tok_head, &head, sizeof(HexSeg), hipMemcpyHostToDevice));
-    // words and counters start at zero (epoch 0 never matches a launch)
-    HIPCHK(launch_fill_u32((unsigned*)m->tok_words, 0u, (size_t)c.n_layers * wo.total * 2, m->stream));
-    HIPCHK(launch_fill_u32((unsigned*)m->tok_top, 0u, (size_t)grid * 8, m->stream));
-    HIPCHK(launch_fill_u32(m->tok_epoch, 0u, (size_t)grid, m->stream));
-    HIPCHK(hipStreamSynchronize(m->stream));
-    TokArgs& a = m->tok;
-    a.layers = m->tok_layers; a.head = m->tok_head; a.out_norm = m->norm(-1, 0); a.embed = m->embed;
-    a.fields = m->fields[radius]; a.words = m->tok_words; a.top = m->tok_top; a.epoch = m->tok_epoch;
-    a.k_cache = m->kc; a.v_cache = m->vc; a.cs = m->cs; a.st = m->st; a.gen_tok = m->gen_tok;
-    a.gen_margin = m->gen_margin; a.logits = m->logits; a.wo = wo;
-    a.n_layers = c.n_layers; a.hidden = c.hidden; a.ffn = c.ffn; a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads;
-    a.hd = c.head_dim; a.max_seq = c.max_seq_len; a.vocab = c.vocab; a.interleaved = c.rope_interleaved;
-    a.eps = c.rms_eps; a.sm_scale = 1.0f / (float)std::sqrt((double)c.head_dim); a.n_pts = n_pts;
-    for (int wh = 0; wh < 2; wh++) {
-        hipGraph_t g = nullptr;
-        HIPCHK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
-        hipError_t e = launch_token(a, wh, m->stream);
-        hipError_t e2 = hipStreamEndCapture(m->stream, &g);
-        if (e != hipSuccess || e2 != hipSuccess) {
-            if (g) (void)hipGraphDestroy(g);
-            return fail((int)(e != hipSuccess ? e : e2), "token kernel capture: %s",
-                        hipGetErrorString(e != hipSuccess ? e : e2));
-        }
-        e = hipGraphInstantiate(wh ? &m->gt_full : &m->gt_prefill, g, nullptr, nullptr, 0);
-        (void)hipGraphDestroy(g);
-        if (e != hipSuccess) return fail((int)e, "hipGraphInstantiate: %s", hipGetErrorString(e));
-    }
-    m->tok_ok = true;
-    return 0;
 }
 
 // Staging bytes of one gsdh_model_matmul call (bf16 X, single fp16 operand
@@ -1057,7 +981,7 @@ int gsdh_model_create(const gsdh_model_config* cfg, gsdh_model** out) {
 int gsdh_model_destroy(gsdh_model* m) {
     if (!m) return 0;
     if (m->stream) (void)hipStreamSynchronize(m->stream);
-    for (hipGraphExec_t g : {m->g_full, m->g_prefill, m->gt_full, m->gt_prefill})
+    for (hipGraphExec_t g : {m->g_full, m->g_prefill})
         if (g) (void)hipGraphExecDestroy(g);
     for (int t = 0; t < kShortTiers; t++)
         for (hipGraphExec_t g : {m->g_full_s[t], m->g_prefill_s[t]})
@@ -1205,28 +1129,12 @@ int gsdh_model_finalize(gsdh_model* m) {
         rc = capture(m, true, kShortChunk[t], &m->g_full_s[t]);
         if (!rc) rc = capture(m, false, kShortChunk[t], &m->g_prefill_s[t]);
     }
-    if (!rc) rc = setup_token_kernel(m);
     if (!rc) rc = setup_batched(m);
     if (rc) return rc;
     HIPCHK(hipStreamSynchronize(m->stream));
     m->finalized = true;
     return 0;
 }
-
-int gsdh_model_set_engine(gsdh_model* m, int engine) {
-    if (!m || !m->finalized) return fail(-1, "set_engine: model not finalized");
-    if (engine == GSDH_ENGINE_GRAPH) {
-        m->engine = engine;
-        return 0;
-    }
-    if (engine != GSDH_ENGINE_PERSISTENT) return fail(-1, "set_engine: unknown engine %d", engine);
-    if (!m->tok_ok) return fail(-1, "set_engine: this model cannot run the persistent token kernel "
-                                   "(mixed codebook radii, head_dim, vector length or LDS)");
-    m->engine = engine;
-    return 0;
-}
-
-int gsdh_model_engine(gsdh_model* m) { return m ? m->engine : -1; }
 
 uint64_t gsdh_model_device_bytes(gsdh_model* m) { return m ? m->dev_bytes : 0; }
 

@@ -340,59 +340,4 @@ hipError_t launch_tile_codes(const HexSeg& s, int cols, uint8_t* out, hipStream_
 
 int device_cu_count();
 
-// ---------------------------------------------------------------------------
-// Persistent token kernel: one launch runs a whole token (embedding row, every
-// layer, and with the head the final norm, logits and greedy argmax).  One
-// block of 512 threads per CU (two waves per SIMD, 256 registers each), all
-// resident at once.  The phases of a layer
-// (q/k/v, attention, o, gate/up, down) hand their output vectors to each
-// other through 64-bit words (epoch << 32 | float bits) written with one
-// device-scope store each and read with device-coherent loads: a reader
-// waits until a word carries the launch's epoch, so no barrier, fence or
-// clearing is needed between phases or launches.  Every wait is bounded
-// (StepState::err is set when one runs out).
-// ---------------------------------------------------------------------------
-constexpr int kTokThreads = 512;
-constexpr int kTokMaxCols = 14336;   // longest input vector of a projection (14 word pairs per thread)
-constexpr int kTokChunk = 256;       // attention positions per work item
-
-struct TokLayer {
-    HexSeg w[7];                 // q, k, v, o, gate, up, down (tiled layout; out unused)
-    const float* norm[2];        // attention / FFN RMSNorm weights
-};
-
-// word offsets of one layer's vectors
-struct TokWords {
-    int q, k, v, att, mid, h, x, part, total;
-};
-TokWords tok_words(int hidden, int ffn, int n_heads, int n_kv, int hd, int max_seq);
-
-struct TokArgs {
-    const TokLayer* layers;      // device array [n_layers]
-    const HexSeg* head;          // device copy of the lm_head segment
-    const float* out_norm;
-    const uint16_t* embed;       // fp16 [vocab][hidden]
-    const uint32_t* fields;      // codebook (r0, r1) fp16 pairs shared by every tensor
-    unsigned long long* words;   // [n_layers][TokWords::total]
-    unsigned long long* top;     // [grid][4] head top-2 words
-    unsigned* epoch;             // [grid] launch counters, one per block
-    uint16_t* k_cache;
-    uint16_t* v_cache;
-    const float2* cs;            // [max_seq][hd/2] RoPE (cos, sin)
-    StepState* st;
-    int* gen_tok;
-    float* gen_margin;
-    float* logits;
-    TokWords wo;
-    int n_layers, hidden, ffn, n_heads, n_kv, hd, max_seq, vocab, interleaved;
-    float eps, sm_scale;
-    int n_pts;
-};
-// Whether a model of this shape can run the persistent kernel (codebook size,
-// head dim, vector lengths, LDS), and the grid it runs with.
-bool tok_supported(int n_pts, int hidden, int ffn, int n_heads, int n_kv, int hd);
-int tok_grid();
-// with_head: final norm, logits and the greedy step
-hipError_t launch_token(const TokArgs& a, int with_head, hipStream_t stream);
-
 }  // namespace gsd

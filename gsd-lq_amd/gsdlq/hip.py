@@ -49,7 +49,6 @@ SIGNATURES = {
     "gsdh_model_set_norm": [vp, i32, i32, vp],
     "gsdh_model_set_hex": [vp, i32, i32, i32, i32, i32, i32, vp, vp, vp, vp, vp, i64, vp, vp, vp],
     "gsdh_model_finalize": [vp],
-    "gsdh_model_set_engine": [vp, i32],
     "gsdh_forward_token": [vp, i32, i32, i32, vp, ctypes.POINTER(i32)],
     "gsdh_generate_greedy": [vp, vp, i32, i32, i32, vp, vp],
     "gsdh_model_run_linear": [vp, i32, i32],
@@ -70,7 +69,6 @@ SIGNATURES = {
 }
 RESTYPES = {"gsdh_model_device_bytes": (u64, [vp]), "gsdh_model_stream": (vp, [vp]),
             "gsdh_attention_workspace_bytes": (u64, [i32, i32, i32, i32]),
-            "gsdh_model_engine": (i32, [vp]),
             "gsdh_last_error": (ctypes.c_char_p, [])}
 
 

@@ -253,8 +253,6 @@ class GPUMistralV2Model:
         packed_bits += bits
         packed_w += self.lm_head["rows"] * self.lm_head["cols"]
         lib.gsdh_model_finalize(self._m)
-        if os.environ.get("GSD_ENGINE"):
-            self.set_engine(os.environ["GSD_ENGINE"])
         hdr_bpw = getattr(src, "header", {}).get("avg_bpw") if hasattr(src, "header") else None
         self.avg_bpw = float(hdr_bpw) if hdr_bpw is not None else packed_bits / max(packed_w, 1)
         dev = int(lib.gsdh_model_device_bytes(self._m))
@@ -295,22 +293,6 @@ class GPUMistralV2Model:
         info = {"rows": rows, "cols": cols, "k_dim": k, "radius": radius,
                 "n_pts": _codebook.n_points(radius), "nk": nk}
         return info, bits
-
-    # -- token engine -----------------------------------------------------
-    ENGINES = {"graph": 0, "persistent": 1}
-
-    @property
-    def engine(self) -> str:
-        """'graph' (one launch per fused phase, the default) or 'persistent'
-        (one launch per token; set_engine('persistent') on a model that
-        qualifies)."""
-        e = int(self.cl.lib.gsdh_model_engine(self._m))
-        return {v: k for k, v in self.ENGINES.items()}[e]
-
-    def set_engine(self, name: str) -> None:
-        if name not in self.ENGINES:
-            raise ValueError(f"engine {name!r}: expected one of {sorted(self.ENGINES)}")
-        self.cl.lib.gsdh_model_set_engine(self._m, self.ENGINES[name])
 
     # -- decode -----------------------------------------------------------
     def forward_token(self, token_id: int, pos: int, return_logits: bool = True):

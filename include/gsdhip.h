@@ -210,26 +210,12 @@ int gsdh_model_set_hex(gsdh_model* m, int layer, int slot, int radius, int rows,
                        const uint16_t* Vt);
 
 /* After every tensor is set: checks completeness, builds the RoPE tables and
- * the per-token HIP graphs of both engines (below). */
+ * the per-token HIP graphs that forward_token / generate_greedy replay: one
+ * launch per fused phase (q/k/v + RoPE + KV append with the decode attention
+ * of short contexts, attention, o, gate/up + SwiGLU, down, head, argmax), in
+ * place of the reference's per-token sequence of OpenCL launches
+ * (run_gpu_native_chat.py:892-969). */
 int gsdh_model_finalize(gsdh_model* m);
-
-/* Token engines of forward_token / generate_greedy.  Both replace the
- * reference's per-token sequence of OpenCL launches
- * (run_gpu_native_chat.py:892-969):
- *   GSDH_ENGINE_GRAPH      - a HIP graph of one launch per fused phase
- *                            (q/k/v + RoPE + KV append, attention, o,
- *                            gate/up + SwiGLU, down, head, argmax);
- *   GSDH_ENGINE_PERSISTENT - one launch per token: a persistent kernel of one
- *                            block per CU whose phases hand vectors to each
- *                            other through epoch-tagged words.  Needs one
- *                            codebook radius for every tensor, head_dim 64 or
- *                            128 and vectors of at most 14336 elements.
- *                            Same results; currently slower than GRAPH.
- * finalize selects GRAPH; set_engine fails for PERSISTENT on a model that
- * does not qualify.  gsdh_model_engine returns the engine in use. */
-enum { GSDH_ENGINE_GRAPH = 0, GSDH_ENGINE_PERSISTENT = 1 };
-int gsdh_model_set_engine(gsdh_model* m, int engine);
-int gsdh_model_engine(gsdh_model* m);
 
 /* Device bytes held by the model (weights + KV cache + activations). */
 uint64_t gsdh_model_device_bytes(gsdh_model* m);

@@ -25,25 +25,18 @@ def _spec(**kw):
     return synth.SynthSpec(**base)
 
 
-ENGINES = ("persistent", "graph")
-
-
-def _models(spec, max_seq=256, interleaved=1, engine="graph"):
+def _models(spec, max_seq=256, interleaved=1):
     from gsdlq import synth
     import run_gpu_native_chat as chat
     src = synth.SynthSource(spec)
     gpu = chat.GPUMistralV2Model(src, rope_interleaved=interleaved, max_seq_len=max_seq, verbose=False)
-    assert gpu.engine == "graph"
-    gpu.set_engine(engine)   # every model here qualifies for the one-launch token kernel
-    assert gpu.engine == engine
     ref = O.OracleModel(src, kind="port", max_seq_len=max_seq, rope_interleaved=interleaved)
     return gpu, ref
 
 
-@pytest.mark.parametrize("engine", ENGINES)
-def test_tiny_model_golden(golden, engine):
-    banner(f"tiny model vs reference-engine golden ({engine})")
-    gpu, _ = _models(_spec(), engine=engine)
+def test_tiny_model_golden(golden):
+    banner("tiny model vs reference-engine golden")
+    gpu, _ = _models(_spec())
     prompt = golden["tiny_prompt"].tolist()
     for pos, t in enumerate(prompt):
         lg = gpu.forward_token(t, pos)
@@ -59,16 +52,15 @@ def test_tiny_model_golden(golden, engine):
     gpu.close()
 
 
-@pytest.mark.parametrize("engine", ENGINES)
 @pytest.mark.parametrize("mode,kpr,il,shape", [
     ("turbo", 0, 1, dict()),
     ("precision", 3, 1, dict()),
     ("precision", 0, 0, dict(n_heads=8, n_kv_heads=8, head_dim=32 * 2)),
     ("turbo", 1, 1, dict(n_layers=3, hidden=512, ffn=1344, n_heads=8, n_kv_heads=2, head_dim=128, vocab=1000)),
 ])
-def test_model_stepwise_vs_oracle(mode, kpr, il, shape, engine):
-    banner(f"stepwise model {mode} kinks {kpr} interleaved {il} {shape} ({engine})")
-    gpu, ref = _models(_spec(mode=mode, kinks_per_row=kpr, **shape), interleaved=il, engine=engine)
+def test_model_stepwise_vs_oracle(mode, kpr, il, shape):
+    banner(f"stepwise model {mode} kinks {kpr} interleaved {il} {shape}")
+    gpu, ref = _models(_spec(mode=mode, kinks_per_row=kpr, **shape), interleaved=il)
     rng = np.random.default_rng(3)
     toks = rng.integers(0, gpu.vocab_size, 40).tolist()
     for pos, t in enumerate(toks):
@@ -121,8 +113,8 @@ def test_device_codes_bit_exact(mode, shape):
 @pytest.mark.parametrize("radius", [5, 7])
 def test_model_generic_codebook_vs_oracle(radius):
     """Codebooks other than radius 6 / 8 run the generic-codebook matvec
-    (7-bit tiles at radius 5, u8 tiles at radius 7), graph engine."""
-    banner(f"stepwise model radius {radius} (graph)")
+    (7-bit tiles at radius 5, u8 tiles at radius 7), ."""
+    banner(f"stepwise model radius {radius}")
     gpu, ref = _models(_spec(mode="precision", kinks_per_row=2, codebook_radius=radius))
     rng = np.random.default_rng(30 + radius)
     toks = rng.integers(0, gpu.vocab_size, 10).tolist()
@@ -136,8 +128,8 @@ def test_model_generic_codebook_vs_oracle(radius):
 @pytest.mark.parametrize("k_dim", [1, 3])
 def test_model_rank_sizes_vs_oracle(k_dim):
     """Rank 1 runs the matvec's in-block projection with one row per tensor;
-    rank 3 the launches whose projections leading blocks publish (graph engine)."""
-    banner(f"stepwise model precision rank {k_dim} (graph)")
+    rank 3 the launches whose projections leading blocks publish ."""
+    banner(f"stepwise model precision rank {k_dim}")
     gpu, ref = _models(_spec(mode="precision", kinks_per_row=1, k_dim=k_dim))
     rng = np.random.default_rng(11 + k_dim)
     toks = rng.integers(0, gpu.vocab_size, 12).tolist()
@@ -157,8 +149,8 @@ def test_model_rank_sizes_vs_oracle(k_dim):
 ])
 def test_model_uneven_units_vs_oracle(mode, shape):
     """Launches with more row-block units than blocks, not a multiple of them
-    (blocks with one unit more than others), graph engine."""
-    banner(f"stepwise model {mode} {shape} uneven units (graph)")
+    (blocks with one unit more than others), ."""
+    banner(f"stepwise model {mode} {shape} uneven units")
     gpu, ref = _models(_spec(mode=mode, kinks_per_row=2, n_layers=1, vocab=1000, **shape), max_seq=64)
     rng = np.random.default_rng(41)
     toks = rng.integers(0, gpu.vocab_size, 8).tolist()
@@ -171,10 +163,9 @@ def test_model_uneven_units_vs_oracle(mode, shape):
     gpu.close()
 
 
-@pytest.mark.parametrize("engine", ENGINES)
-def test_generate_greedy_matches_oracle(engine):
-    banner(f"generate_greedy vs oracle ({engine})")
-    gpu, ref = _models(_spec(mode="turbo", kinks_per_row=1), engine=engine)
+def test_generate_greedy_matches_oracle():
+    banner("generate_greedy vs oracle")
+    gpu, ref = _models(_spec(mode="turbo", kinks_per_row=1))
     prompt = [1, 5, 9, 200, 33, 2]
     toks, margins = gpu.generate_greedy(prompt, 24)
     want, wm = ref.generate_greedy(prompt, 24)
@@ -187,15 +178,13 @@ def test_generate_greedy_matches_oracle(engine):
     gpu.close()
 
 
-@pytest.mark.parametrize("engine", ENGINES)
-def test_decode_across_short_context_switch(engine):
-    """Below 256 positions attention is one split (graph engine: one block per
-    KV head and no merge launch; persistent engine: one item per query head
-    and no merge step), later ones are split and merged: decoding through the
-    switch matches the oracle token for token, and forward_token agrees on
-    both sides of it."""
-    banner(f"greedy decode across position 256 ({engine})")
-    gpu, ref = _models(_spec(mode="precision", kinks_per_row=1), max_seq=512, engine=engine)
+def test_decode_across_short_context_switch():
+    """Below 256 positions attention is one split (one block per KV head and
+    no merge), later ones are split and merged: decoding through the switch
+    matches the oracle token for token, and forward_token agrees on both
+    sides of it."""
+    banner("greedy decode across position 256")
+    gpu, ref = _models(_spec(mode="precision", kinks_per_row=1), max_seq=512)
     rng = np.random.default_rng(20)     # smallest oracle margin 6e-3 over the 48 steps
     prompt = rng.integers(0, gpu.vocab_size, 230).tolist()
     toks, margins = gpu.generate_greedy(prompt, 48)
@@ -310,7 +299,7 @@ _LONG = {}
 
 def _long_oracle():
     """Oracle greedy run through positions 0 .. 4113 of an 8192-position model
-    (computed once for both engines)."""
+    (computed once)."""
     if not _LONG:
         from gsdlq import synth
         spec = _spec(mode="precision", kinks_per_row=1, n_layers=1)
@@ -328,8 +317,7 @@ def _long_oracle():
 LONG_SEED = 5
 
 
-@pytest.mark.parametrize("engine", ENGINES)
-def test_decode_past_2048_to_4096(engine):
+def test_decode_past_2048_to_4096():
     """A model with an 8192-position cache decodes through positions 2048
     (the reference's fixed cache size) and 4096: 4090 prompt tokens, then 24
     greedy steps equal to the oracle's (heap score buffer), and forward_token
@@ -337,9 +325,8 @@ def test_decode_past_2048_to_4096(engine):
     from gsdlq import synth
     import run_gpu_native_chat as chat
     L = _long_oracle()
-    banner(f"decode to position 4113 of an 8192-position cache ({engine})")
+    banner("decode to position 4113 of an 8192-position cache")
     gpu = chat.GPUMistralV2Model(synth.SynthSource(L["spec"]), max_seq_len=8192, verbose=False)
-    gpu.set_engine(engine)
     toks, margins = gpu.generate_greedy(L["prompt"], 24)
     assert toks == L["toks"]
     assert np.allclose(margins, L["margins"], rtol=1e-2, atol=1e-4)
