@@ -211,9 +211,11 @@ MFMA_F16_PEAK_TFLOPS = 2500.0   # MI355X dense fp16 / bf16 matrix peak
 
 def bench_prefill(bank, ms=(16, 128, 512), reps=3):
     """Batched projection (prefill) over the bank's Turbo layer sets: for each
-    M, the 7 tensors of every distinct layer through gsdh_model_matmul,
-    graph-captured; FLOPs = 2*M*rows*cols, bytes = packed weights + bf16 X +
-    fp32 Y.  Roofline: MFMA (fp16 dense peak) for M >= 128, HBM for M = 16."""
+    M, the 7 tensors of every distinct layer (q/k/v and gate/up each sharing
+    one operand prep of their common input: gsdh_model_matmul_shared; o and
+    down alone), graph-captured; FLOPs = 2*M*rows*cols, bytes = packed
+    weights + bf16 X + fp32 Y.  Roofline: MFMA (fp16 dense peak) for M >=
+    128, HBM for M = 16."""
     model = build_model(bank, bank.n)
     lib = model.cl.lib
     shapes = [(t, bank.packed[(0, t)]["rows"], bank.packed[(0, t)]["cols"]) for t in layer_shapes()]
@@ -231,9 +233,11 @@ def bench_prefill(bank, ms=(16, 128, 512), reps=3):
     out = {}
     flops_layer = sum(2 * r * c for _, r, c in shapes)
     wbytes_layer = bank.layer_bytes[0]
+    groups = [("attn_q", "attn_k", "attn_v"), ("attn_output",), ("ffn_gate", "ffn_up"), ("ffn_down",)]
+    garg = [((ctypes.c_int * len(g))(*[slot[t] for t in g]), (ctypes.c_void_p * len(g))(*[y] * len(g))) for g in groups]
     for M in ms:
-        issue = lambda: [lib.gsdh_model_matmul(model._m, l, slot[t], x, M, y)
-                         for l in range(bank.n) for t, _, _ in shapes]
+        issue = lambda: [lib.gsdh_model_matmul_shared(model._m, l, sl, len(sl), x, M, ys)
+                         for l in range(bank.n) for sl, ys in garg]
         issue()                                   # workspace for this M, outside the capture
         lib.gsdh_stream_sync(lib.gsdh_model_stream(model._m))
         ge = capture(model, issue)

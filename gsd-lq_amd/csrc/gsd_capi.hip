@@ -675,14 +675,15 @@ hipGraphExec_t token_graph(const gsdh_model* m, bool with_head, int pos) {
 }
 
 // Staging bytes of one gsdh_model_matmul call (bf16 X, single fp16 operand
-// rounding): A fragments, descales, rank-k values, split partials.
+// rounding): A fragments, descales, rank-k values (one slot per tensor of a
+// shared-input call), split partials.
 size_t matmul_ws_need(int M, int rows, int cols) {
     const size_t xa = (hexmm_xa_bytes(M, cols) + 255) / 256 * 256;
     const size_t xs = ((size_t)(M + 15) / 16 * 16 * 4 + 255) / 256 * 256;
     const size_t tk = ((size_t)M * kMaxRank * 4 + 255) / 256 * 256;
     const MatmulPlan plan = hexmm_plan(M, rows, cols);
     const size_t pt = plan.nsplit > 1 ? (size_t)plan.nsplit * ((M + 15) / 16 * 16) * rows * 4 : 0;
-    return xa + xs + tk + pt;
+    return xa + xs + kMaxSeg * tk + pt;
 }
 
 size_t split_part_bytes(int M, int rows, int cols) {
@@ -1251,37 +1252,58 @@ int gsdh_model_read_codes(gsdh_model* m, int layer, int slot, uint8_t* codes_out
 }
 
 int gsdh_model_matmul(gsdh_model* m, int layer, int slot, const uint16_t* X, int M, float* Y) {
-    if (!m || !X || !Y) return fail(-1, "matmul: null argument");
-    if (slot < 0 || slot > GSDH_LM_HEAD) return fail(-1, "matmul: slot %d", slot);
-    if (slot != GSDH_LM_HEAD && (layer < 0 || layer >= m->c.n_layers)) return fail(-1, "matmul: layer %d", layer);
+    return gsdh_model_matmul_shared(m, layer, &slot, 1, X, M, &Y);
+}
+
+int gsdh_model_matmul_shared(gsdh_model* m, int layer, const int* slots, int n, const uint16_t* X, int M,
+                             float* const* Y) {
+    if (!m || !X || !slots || !Y) return fail(-1, "matmul: null argument");
+    if (n < 1 || n > kMaxSeg) return fail(-1, "matmul: %d tensors (1..%d share one input)", n, kMaxSeg);
     if (M <= 0) return fail(-1, "matmul: M %d", M);
-    const HexDev& t = m->slot(layer, slot);
-    if (!t.set) return fail(-1, "matmul: layer %d slot %d not set", layer, slot);
     if (!m->finalized) return fail(-1, "matmul: model not finalized");
     if (M > kMatmulMaxM) return fail(-1, "matmul: M %d > %d tokens per call (split the batch)", M, kMatmulMaxM);
-    const size_t xa = (hexmm_xa_bytes(M, t.cols) + 255) / 256 * 256;
+    const HexDev* ts[kMaxSeg] = {};
+    for (int i = 0; i < n; i++) {
+        const int slot = slots[i];
+        if (slot < 0 || slot > GSDH_LM_HEAD) return fail(-1, "matmul: slot %d", slot);
+        if (slot != GSDH_LM_HEAD && (layer < 0 || layer >= m->c.n_layers)) return fail(-1, "matmul: layer %d", layer);
+        if (!Y[i]) return fail(-1, "matmul: null output %d", i);
+        ts[i] = &m->slot(layer, slot);
+        if (!ts[i]->set) return fail(-1, "matmul: layer %d slot %d not set", layer, slot);
+        if (ts[i]->cols != ts[0]->cols) return fail(-1, "matmul: tensors of %d and %d columns do not share an input",
+                                                    ts[0]->cols, ts[i]->cols);
+        if (matmul_ws_need(M, ts[i]->rows, ts[i]->cols) > m->mm_ws_bytes)
+            return fail(-1, "matmul: staging for %d tokens exceeds the model's workspace", M);
+    }
+    const int cols = ts[0]->cols;
+    const size_t xa = (hexmm_xa_bytes(M, cols) + 255) / 256 * 256;
     const size_t xs = ((size_t)(M + 15) / 16 * 16 * 4 + 255) / 256 * 256;
     const size_t tk = ((size_t)M * kMaxRank * 4 + 255) / 256 * 256;
-    const MatmulPlan plan = hexmm_plan(M, t.rows, t.cols);
-    const int nsplit = plan.nsplit;
-    if (matmul_ws_need(M, t.rows, t.cols) > m->mm_ws_bytes)
-        return fail(-1, "matmul: staging for %d tokens exceeds the model's workspace", M);
     char* w = static_cast<char*>(m->mm_ws);
-    MatmulArgs a{};
-    fill_seg(a.w, t, m, nullptr);
-    a.X = X;
-    a.xa = reinterpret_cast<uint4*>(w);
-    a.xs = reinterpret_cast<float*>(w + xa);
-    a.tmp_k = t.k > 0 ? reinterpret_cast<float*>(w + xa + xs) : nullptr;
-    a.Y = Y;
-    a.M = M;
-    a.cols = t.cols;
-    a.nsplit = nsplit;
-    a.tg = plan.tg;
-    a.rbw = plan.rbw;
-    a.part = nsplit > 1 ? reinterpret_cast<float*>(w + xa + xs + tk) : nullptr;
-    if (t.k > 0) HIPCHK(launch_lowrank_batched(X, t.Vt, t.Sv, reinterpret_cast<float*>(w + xa + xs), M, t.k, t.cols, m->stream));
-    HIPCHK(launch_hexmm(a, m->stream));
+    // X's operands once for every tensor of the call
+    HIPCHK(launch_hexmm_xprep(X, M, cols, reinterpret_cast<uint4*>(w), reinterpret_cast<float*>(w + xa), m->stream));
+    for (int i = 0; i < n; i++) {
+        const HexDev& t = *ts[i];
+        const MatmulPlan plan = hexmm_plan(M, t.rows, t.cols);
+        float* tmp = reinterpret_cast<float*>(w + xa + xs + (size_t)i * tk);
+        MatmulArgs a{};
+        fill_seg(a.w, t, m, nullptr);
+        a.X = X;
+        a.xa = reinterpret_cast<uint4*>(w);
+        a.xs = reinterpret_cast<float*>(w + xa);
+        a.tmp_k = t.k > 0 ? tmp : nullptr;
+        a.Y = Y[i];
+        a.M = M;
+        a.cols = t.cols;
+        a.nsplit = plan.nsplit;
+        a.tg = plan.tg;
+        a.rbw = plan.rbw;
+        a.prepped = 1;
+        // (split partials of the tensors in turn: stream order keeps them apart)
+        a.part = plan.nsplit > 1 ? reinterpret_cast<float*>(w + xa + xs + kMaxSeg * tk) : nullptr;
+        if (t.k > 0) HIPCHK(launch_lowrank_batched(X, t.Vt, t.Sv, tmp, M, t.k, t.cols, m->stream));
+        HIPCHK(launch_hexmm(a, m->stream));
+    }
     return 0;
 }
 

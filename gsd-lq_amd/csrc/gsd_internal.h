@@ -138,7 +138,13 @@ struct MatmulArgs {
     int hl;
     const float* Xf;
     int accumulate;
+    // hl == 0: xa / xs already hold X's operands (an earlier launch_hexmm of
+    // the same X, or launch_hexmm_xprep): the operand prep is skipped
+    int prepped;
 };
+// The single-rounding fp16 operands of bf16 X [M][cols] into xa / xs (the
+// prep launch_hexmm runs first), for several tensors that read the same X.
+hipError_t launch_hexmm_xprep(const uint16_t* X, int M, int cols, uint4* xa, float* xs, hipStream_t stream);
 size_t hexmm_xa_bytes(int M, int cols, int hl = 0);
 // Operands of M tokens for the batched projections that share one input
 // (q/k/v, gate/up, o, down): x' = rmsnorm(x) * norm_w (as

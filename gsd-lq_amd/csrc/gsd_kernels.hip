@@ -3468,19 +3468,24 @@ hipError_t launch_embed_rows(const uint16_t* embed, const int* tokens, int M, fl
     return hipGetLastError();
 }
 
+hipError_t launch_hexmm_xprep(const uint16_t* X, int M, int cols, uint4* xa, float* xs, hipStream_t st) {
+    if (M <= 0 || cols <= 0 || cols % 64 || !X || !xa || !xs) return hipErrorInvalidValue;
+    if (cols <= 16384 && (reinterpret_cast<uintptr_t>(X) & 15) == 0)
+        hipLaunchKernelGGL(hexmm_xprep2_kernel, dim3(((M + 15) / 16) * 16), dim3(512), 0, st, X, M, cols, xa, xs);
+    else
+        hipLaunchKernelGGL(hexmm_xprep_kernel, dim3(((M + 15) / 16) * 16), dim3(256), 0, st, X, M, cols, xa, xs);
+    return hipGetLastError();
+}
+
 hipError_t launch_hexmm(const MatmulArgs& a, hipStream_t st) {
     if (a.hl) return hipErrorInvalidValue;
     if (a.M <= 0 || a.cols <= 0 || a.cols % 64 || !a.w.codes_t || !a.w.scales_t || !a.w.fields) return hipErrorInvalidValue;
     if (a.nsplit < 1 || (a.nsplit > 1 && !a.part)) return hipErrorInvalidValue;
     if (a.w.k > 0 && (!a.tmp_k || !a.w.U)) return hipErrorInvalidValue;
-    if (a.cols <= 16384 && (reinterpret_cast<uintptr_t>(a.X) & 15) == 0)
-        hipLaunchKernelGGL(hexmm_xprep2_kernel, dim3(((a.M + 15) / 16) * 16), dim3(512), 0, st, a.X, a.M, a.cols, a.xa,
-                           a.xs);
-    else
-        hipLaunchKernelGGL(hexmm_xprep_kernel, dim3(((a.M + 15) / 16) * 16), dim3(256), 0, st, a.X, a.M, a.cols, a.xa,
-                           a.xs);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (!a.prepped) {
+        const hipError_t e = launch_hexmm_xprep(a.X, a.M, a.cols, a.xa, a.xs, st);
+        if (e != hipSuccess) return e;
+    }
     if (a.w.n_pts == 217) return launch_hexmm_tb<217>(a, st);
     if (a.w.n_pts == 127) return launch_hexmm_tb<127>(a, st);
     return launch_hexmm_tb<0>(a, st);

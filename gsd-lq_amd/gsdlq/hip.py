@@ -53,6 +53,7 @@ SIGNATURES = {
     "gsdh_generate_greedy": [vp, vp, i32, i32, i32, vp, vp],
     "gsdh_model_run_linear": [vp, i32, i32],
     "gsdh_model_matmul": [vp, i32, i32, vp, i32, vp],
+    "gsdh_model_matmul_shared": [vp, i32, ctypes.POINTER(i32), i32, vp, i32, ctypes.POINTER(vp)],
     "gsdh_matmul_plan": [i32, i32, i32, ctypes.POINTER(i32), ctypes.POINTER(i32), ctypes.POINTER(i32)],
     "gsdh_model_read_codes": [vp, i32, i32, vp],
     "gsdh_model_capture_begin": [vp],

@@ -265,6 +265,12 @@ int gsdh_model_set_prefill(gsdh_model* m, int batched);
  * M <= 512 per call; the staging lives in the model's workspace (sized at
  * finalize), so the call allocates nothing and can be graph-captured. */
 int gsdh_model_matmul(gsdh_model* m, int layer, int slot, const uint16_t* X, int M, float* Y);
+/* The same for n <= 3 tensors of `layer` that read the same X (q, k, v or
+ * gate, up): X's operands are prepared once, then each tensor's projection
+ * runs into Y[i] (device fp32 [M][rows_i]).  Equal to n gsdh_model_matmul
+ * calls, bit for bit. */
+int gsdh_model_matmul_shared(gsdh_model* m, int layer, const int* slots, int n, const uint16_t* X, int M,
+                             float* const* Y);
 /* The tiling gsdh_model_matmul and the batched prefill use for M tokens of a
  * rows x cols tensor on the current device: token groups of 16 per block
  * (*tg: 1, 2, 4, 8), row blocks of 16 per wave (*rbw) and column splits

@@ -114,6 +114,42 @@ def test_matmul_7b_turbo_plans(turbo_7b):
     assert any(s > 1 for _, _, s in seen), seen
 
 
+@pytest.mark.parametrize("names,M", [(("attn_q", "attn_k", "attn_v"), 128), (("ffn_gate", "ffn_up"), 512),
+                                     (("attn_q", "attn_k", "attn_v"), 16)])
+def test_matmul_shared_input_equals_separate_calls(turbo_7b, names, M):
+    """gsdh_model_matmul_shared (one operand prep for tensors that read the
+    same X) gives the separate calls' outputs bit for bit, and the oracle's."""
+    bank, model = turbo_7b
+    lib = model.cl.lib
+    banner(f"shared-input matmul {names} M={M}")
+    rng = np.random.default_rng(60 + M)
+    cols = bank.packed[(0, names[0])]["cols"]
+    xb, xf = bf16(rng.standard_normal((M, cols)).astype(np.float32))
+    dx = D(xb)
+    rows = [bank.packed[(0, n)]["rows"] for n in names]
+    ys = [E(M * r * 4) for r in rows]
+    sl = (ctypes.c_int * len(names))(*[SLOTS[n] for n in names])
+    yp = (ctypes.c_void_p * len(names))(*[y.ptr.value for y in ys])
+    lib.gsdh_model_matmul_shared(model._m, 0, sl, len(names), dx.ptr, M, yp)
+    lib.gsdh_stream_sync(lib.gsdh_model_stream(model._m))
+    got = [H(y, np.float32, M * r).reshape(M, r) for y, r in zip(ys, rows)]
+    for n, r, g in zip(names, rows, got):
+        want = run_matmul(model, 0, SLOTS[n], xb, M, r)
+        assert np.array_equal(g, want), n
+        for m in (0, M - 1):
+            assert rel_l2(g[m], O.hex2d_matvec(xf[m], bank.packed[(0, n)])) < 1e-3, (n, m)
+
+
+def test_matmul_shared_rejects_mixed_inputs(turbo_7b):
+    from gsdlq.hip import HipError
+    bank, model = turbo_7b
+    buf = E(1 << 20)
+    sl = (ctypes.c_int * 2)(SLOTS["attn_q"], SLOTS["ffn_down"])
+    yp = (ctypes.c_void_p * 2)(buf.ptr.value, buf.ptr.value)
+    with pytest.raises(HipError, match="share an input"):
+        model.cl.lib.gsdh_model_matmul_shared(model._m, 0, sl, 2, buf.ptr, 4, yp)
+
+
 def layer_shape(name):
     H, F, KV = 4096, 14336, 1024
     return {"attn_q": (H, H), "attn_k": (KV, H), "attn_v": (KV, H), "attn_output": (H, H),
