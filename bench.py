@@ -456,8 +456,12 @@ def bench_attention(ctxs=(512, 2048, 8192), reps=20):
     the two reference calls in one (gsd_lq_cpu_engine.c:185-330 computes the
     same).
     Enough layers are rotated that the caches exceed 512 MB (beyond the
-    Infinity Cache); the launches of all layers are captured in one graph on
-    the stream of a small model context and timed with HIP events there.
+    Infinity Cache), at most 512 (below ctx 256 the caches are smaller); the
+    launches of all layers are captured in one graph on the stream of a small
+    model context and timed with HIP events there.  (rocprofv3's kernel trace
+    of a graph of 1024 of these launches, 672 bytes of kernel arguments each,
+    ended in a host segmentation fault before any kernel ran; graphs of up to
+    512 trace normally.)
     Algorithmic bytes per layer: K + V read (ctx * 8 * 128 * 2 * 2) + the
     4096-byte append + q and the output (2 * 4 * 4096)."""
     import run_gpu_native_chat as chat
@@ -474,7 +478,7 @@ def bench_attention(ctxs=(512, 2048, 8192), reps=20):
     res = {}
     for ctx in ctxs:
         kv_layer = ctx * n_kv * hd * 2 * 2
-        L = max(4, -(-(512 << 20) // kv_layer))
+        L = min(512, max(4, -(-(512 << 20) // kv_layer)))
         bufs = {}
         sizes = {"kc": L * kv_layer // 2, "vc": L * kv_layer // 2, "q": L * n_heads * hd * 4,
                  "k": L * n_kv * hd * 4, "v": L * n_kv * hd * 4, "out": L * n_heads * hd * 4}
@@ -501,7 +505,7 @@ def bench_attention(ctxs=(512, 2048, 8192), reps=20):
                                                   at("out", l, n_heads * hd), l, pos, n_heads, n_kv, hd, ctx,
                                                   ctypes.c_float(theta), 1, ctypes.c_float(sm_scale))
 
-        run()                                    # sizes the attention workspace outside the capture
+        run()                                    # warm-up, outside the capture
         lib.gsdh_stream_sync(sp)
         ge = capture(model, run)
         time_graph(model, ge, 2)
