@@ -259,12 +259,14 @@ def bench_prefill(bank, ms=(16, 128, 512), reps=3):
     return out
 
 
-def bench_decode(bank, n_prompt=64, n_new=128):
+def bench_decode(bank, n_prompt=64, n_new=128, long_prompt=1024):
     """Greedy decode tok/s of a 32-layer 7B-shaped model (layers are copies of
     the bank's distinct layers, each copy its own HBM allocation): one HIP
     graph of per-phase launches per token; weight_GBs = packed weight bytes
-    streamed per token x tok/s."""
-    model = build_model(bank, 32, max_seq=n_prompt + n_new + 8)
+    streamed per token x tok/s.  Then the 64-token prompt alone (batched
+    prefill and one decode step per token) and a `long_prompt`-token prompt
+    through the batched prefill (chunks of 512 tokens)."""
+    model = build_model(bank, 32, max_seq=max(n_prompt + n_new, long_prompt) + 8)
     prompt = np.random.default_rng(4).integers(0, V, n_prompt).tolist()
     wbytes = 32 * bank.layer_bytes[0] + alg_bytes(bank.packed["lm"])
     out = {"n_prompt": n_prompt, "n_new": n_new, "weight_bytes_per_token": wbytes}
@@ -296,6 +298,16 @@ def bench_decode(bank, n_prompt=64, n_new=128):
         out[key + "_ms"] = round(dt * 1e3, 2)
         out[key + "_tok_s"] = round(n_prompt / dt, 1)
     model.set_prefill(True)
+    if long_prompt:
+        lp = np.random.default_rng(5).integers(0, V, long_prompt).tolist()
+        model.prefill(lp, 0, return_logits=False)
+        reps = 3
+        t0 = time.time()
+        for _ in range(reps):
+            model.prefill(lp, 0)
+        dt = (time.time() - t0) / reps
+        out[f"prefill_{long_prompt}_ms"] = round(dt * 1e3, 2)
+        out[f"prefill_{long_prompt}_tok_s"] = round(long_prompt / dt, 1)
     model.close()
     return out
 

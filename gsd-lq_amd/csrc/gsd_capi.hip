@@ -365,6 +365,24 @@ int gsdh_gqa_attention(void* stream, const float* q, const uint16_t* k_cache, co
     return 0;
 }
 
+int gsdh_prefill_attention(void* stream, const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                           float* attn_out, int layer_idx, int pos0, int n_tokens, int n_heads, int n_kv_heads,
+                           int head_dim, int max_seq_len, float sm_scale) {
+    if (n_tokens < 0 || pos0 < 0 || layer_idx < 0 || max_seq_len <= 0 || pos0 + n_tokens > max_seq_len)
+        return fail(-1, "prefill_attention: %d tokens at %d, max_seq_len %d", n_tokens, pos0, max_seq_len);
+    if (n_kv_heads <= 0 || n_heads % n_kv_heads || 8 % (n_heads / n_kv_heads))
+        return fail(-1, "prefill_attention: %d query heads over %d KV heads", n_heads, n_kv_heads);
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+        return fail(-1, "prefill_attention: head_dim %d not in {64,128,256}", head_dim);
+    if (n_tokens && (!q || !k_cache || !v_cache || !attn_out)) return fail(-1, "prefill_attention: null buffer");
+    PrefillAttn a{};
+    a.q = q; a.k_cache = k_cache; a.v_cache = v_cache; a.out = attn_out; a.layer = layer_idx; a.p0 = pos0;
+    a.M = n_tokens; a.n_heads = n_heads; a.n_kv = n_kv_heads; a.hd = head_dim; a.max_seq = max_seq_len;
+    a.sm_scale = sm_scale;
+    HIPCHK(launch_prefill_attention(a, S(stream)));
+    return 0;
+}
+
 int gsdh_rope_store_gqa_attention(void* stream, float* q, const float* k, const float* v, uint16_t* k_cache,
                                   uint16_t* v_cache, float* attn_out, int layer_idx, int pos, int n_heads,
                                   int n_kv_heads, int head_dim, int max_seq_len, float rope_theta, int interleaved,
@@ -410,8 +428,10 @@ int gsdh_greedy_argmax(void* stream, const float* logits, int n, int* token_out,
 // ---------------------------------------------------------------------------
 namespace {
 constexpr int kMatmulMaxM = 512;    // tokens per gsdh_model_matmul call
-constexpr int kPrefillChunk = 128;  // prompt tokens per batched prefill pass
-constexpr int kPrefillAttnChunk = 256;   // positions per attention split in prefill
+// prompt tokens per batched prefill pass: the projections' matrix-core tiles
+// need a few hundred tokens to pass the latency bound (7B Turbo layer set:
+// 1.6 us per token at 128 tokens, 0.78 at 512)
+constexpr int kPrefillChunk = 512;
 }  // namespace
 
 struct HexDev {
@@ -457,10 +477,7 @@ struct gsdh_model {
         float* tmp = nullptr;                     // rank-k values [kMaxSeg][chunk][kMaxRank]
         float* part = nullptr;                    // split partials
         size_t part_bytes = 0;
-        unsigned long long* ws = nullptr;         // attention split words [chunk][n_kv][splits][G][2 + hd]
-        size_t ws_bytes = 0;
-        unsigned epoch = 0;                       // last attention epoch on ws
-        int chunk = 0, splits = 0;
+        int chunk = 0;
         bool batched = true;                      // generate_greedy prefills in batches
     } pf;
     unsigned long long* pub = nullptr;   // rank-k publication words, one range per matvec launch
@@ -709,8 +726,6 @@ int setup_batched(gsdh_model* m) {
     const int Mc = kPrefillChunk, Mp = (Mc + 15) / 16 * 16;
     const int maxc = std::max(std::max(c.hidden, c.ffn), qd);
     P.chunk = Mc;
-    P.splits = (c.max_seq_len + kPrefillAttnChunk - 1) / kPrefillAttnChunk;
-    P.ws_bytes = attention_ws_bytes(c.n_kv_heads, P.splits, c.n_heads / c.n_kv_heads, c.head_dim) * Mc;
     P.part_bytes = part;
     int rc = 0;
     auto A = [&](void** p, size_t n) { if (!rc) rc = dalloc(m, p, n); };
@@ -729,11 +744,7 @@ int setup_batched(gsdh_model* m) {
     A((void**)&P.xs, (size_t)Mp * 4);
     A((void**)&P.tmp, (size_t)kMaxSeg * Mc * kMaxRank * 4);
     A((void**)&P.part, part);
-    A((void**)&P.ws, P.ws_bytes);
-    if (rc) return rc;
-    HIPCHK(launch_fill_u32(reinterpret_cast<unsigned*>(P.ws), 0u, P.ws_bytes / 4, m->stream));
-    P.epoch = 0;
-    return 0;
+    return rc;
 }
 
 // One batched projection of the prepared operands (launch_batch_prep) into Y
@@ -799,20 +810,12 @@ int issue_prefill(gsdh_model* m, int M, int p0) {
         r.n_heads = c.n_heads; r.n_kv = c.n_kv_heads; r.hd = c.head_dim; r.max_seq = c.max_seq_len;
         r.interleaved = c.rope_interleaved;
         HIPCHK(launch_rope_kv_rows(P.Q, P.K, P.V, r, M, m->stream));
-        {   // causal attention of the M tokens over the cache
-            AttnArgs a{};
-            a.q = P.Q; a.k_cache = m->kc; a.v_cache = m->vc; a.out = P.A; a.pos_dev = nullptr; a.pos = p0;
-            a.layer = l; a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.hd = c.head_dim; a.max_seq = c.max_seq_len;
+        {   // causal attention of the M tokens over the cache (matrix cores)
+            PrefillAttn a{};
+            a.q = P.Q; a.k_cache = m->kc; a.v_cache = m->vc; a.out = P.A; a.layer = l; a.p0 = p0; a.M = M;
+            a.n_heads = c.n_heads; a.n_kv = c.n_kv_heads; a.hd = c.head_dim; a.max_seq = c.max_seq_len;
             a.sm_scale = 1.0f / (float)std::sqrt((double)c.head_dim);
-            a.chunk = kPrefillAttnChunk;
-            a.max_splits = (p0 + M + kPrefillAttnChunk - 1) / kPrefillAttnChunk;
-            a.ws = P.ws; a.counters = nullptr; a.err = &m->st->err; a.ntok = M;
-            if (P.epoch >= 0xFFFFFFF0u) {
-                HIPCHK(launch_fill_u32(reinterpret_cast<unsigned*>(P.ws), 0u, P.ws_bytes / 4, m->stream));
-                P.epoch = 0;
-            }
-            a.epoch = ++P.epoch;
-            HIPCHK(launch_attention(a, m->stream));
+            HIPCHK(launch_prefill_attention(a, m->stream));
         }
         {   // x += W_o attn
             const HexDev* ts[1] = {to};

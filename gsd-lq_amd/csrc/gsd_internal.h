@@ -259,6 +259,21 @@ struct AttnArgs {
     int mergers;
 };
 hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
+// Causal attention of M consecutive prompt tokens on the matrix cores:
+// token t (query rows q[t][n_heads][hd], RoPE applied; its K/V rows already
+// in the cache at p0 + t) over cache positions 0 .. p0 + t, out[t][n_heads][hd].
+// Group sizes 1, 2, 4, 8; head dims 64, 128, 256; p0 + M <= max_seq.  No
+// workspace, no waits between blocks.
+struct PrefillAttn {
+    const float* q;
+    const uint16_t* k_cache;
+    const uint16_t* v_cache;
+    float* out;
+    int layer, p0, M, n_heads, n_kv, hd, max_seq;
+    float sm_scale;
+    int log2g;   // set by the launcher
+};
+hipError_t launch_prefill_attention(const PrefillAttn& a, hipStream_t stream);
 // RoPE + K/V append at a.pos fused into the one-token attention launch
 // (host position; k, v: the new rows before RoPE; cs: (cos, sin) of pos,
 // hd / 2 pairs): q is rotated in place, the cache rows written, out as

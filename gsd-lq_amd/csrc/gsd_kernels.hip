@@ -3149,6 +3149,213 @@ __global__ void __launch_bounds__(256) hexmm_reduce_kernel(const MatmulArgs a) {
     a.Y[i] = a.accumulate ? a.Y[i] + y : y;
 }
 
+// ------------------------------------------------------------------------
+// Causal attention of a batch of prompt tokens on the matrix cores.  Each
+// token computes what the reference's one-token attention computes
+// (gsd_lq_cpu_engine.c:264-330; the reference prefills token by token,
+// run_gpu_native_chat.py:1128-1130): token t of the batch sits at position
+// p0 + t and attends over cache positions 0 .. p0 + t.
+// Block: KV head blockIdx.y and 64 query rows, T = 64 / G consecutive tokens
+// x the G query heads of the KV head (row r: token t0 + r / G, head
+// kvh * G + r % G); wave w holds rows 16w .. 16w + 15, one per lane column
+// (lane & 15).  Positions pass through LDS in chunks of 32, K as rows
+// [pos][HD] and V transposed [HD][pos] (rows padded against bank conflicts),
+// double-buffered with the next chunk's loads in flight.  Per chunk a wave
+// forms S^T = K Q^T (two 16-position tiles; A: K rows, B: the lane's query
+// row as fp16 high + low parts after a per-row power-of-two scale, so the
+// scores keep ~22 bits), the online softmax of each query row (base-2
+// exponent: the scale carries log2 e), and O^T += V^T P^T (A: V^T, B: the
+// probabilities, high + low parts).  The k index of the second product runs
+// over the chunk's positions in the order the score tiles leave them in a
+// lane of group g = lane >> 4 (4g .. 4g+3, then 16+4g .. 16+4g+3), and the
+// V^T fragments are read in that order.  Positions past the block's last
+// token are staged as zeros: cache rows past the context may hold anything,
+// and a zero probability times a NaN would still be NaN.
+template <int HD>
+__global__ void __launch_bounds__(256) attn_prefill_kernel(const PrefillAttn a) {
+    constexpr int KS = HD + 8;    // K row stride, halves (16 bytes of padding)
+    constexpr int VS = 36;        // V^T row stride, halves (32 positions + 4)
+    constexpr int NKS = HD / 32;  // k steps of the scores
+    constexpr int NDT = HD / 16;  // 16-dimension tiles of the output
+    constexpr int D8 = HD / 8;    // 16-byte pieces of a cache row
+    constexpr int NK = HD / 64;   // K pieces per thread and chunk (32 * D8 / 256)
+    constexpr int NVU = 16 * D8;  // V units: 16 position pairs x D8 pieces
+    constexpr int NV = (NVU + 255) / 256;
+    __shared__ __attribute__((aligned(16))) uint16_t kl[2][32 * KS];
+    __shared__ __attribute__((aligned(16))) uint16_t vl[2][HD * VS];
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int n = lane & 15, g = lane >> 4;
+    const int lg = a.log2g, G = 1 << lg, T = 64 >> lg;
+    const int grp = (int)gridDim.x - 1 - (int)blockIdx.x;   // the longest blocks first
+    const int kvh = (int)blockIdx.y;
+    const int t0 = grp * T;
+    const int r = 16 * wid + n;
+    const int t = t0 + (r >> lg), head = kvh * G + (r & (G - 1));
+    const bool valid = t < a.M;
+    const int limit = a.p0 + t;   // last position of this row
+    const int maxpos = a.p0 + min(t0 + T, a.M) - 1;
+    const int nch = maxpos / 32 + 1;
+
+    // the row's query: B fragments of k step ks = dims 32 ks + 8 g .. + 7
+    half8v qh[NKS], ql[NKS];
+    float down;
+    {
+        const float qs = a.sm_scale * 1.44269504088896340736f;
+        const float* qr = a.q + ((size_t)(valid ? t : 0) * a.n_heads + head) * HD + 8 * g;
+        float qv[NKS][8];
+        float mx = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ks++) {
+            float4 f0 = make_float4(0.f, 0.f, 0.f, 0.f), f1 = f0;
+            if (valid) {
+                f0 = *reinterpret_cast<const float4*>(qr + 32 * ks);
+                f1 = *reinterpret_cast<const float4*>(qr + 32 * ks + 4);
+            }
+            const float v8[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                qv[ks][j] = v8[j] * qs;
+                mx = fmaxf(mx, fabsf(qv[ks][j]));
+            }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        int ex = 0;
+        if (mx > 0.f && mx < INFINITY) (void)frexpf(mx, &ex);
+        const float up = ldexpf(1.f, 14 - ex);
+        down = ldexpf(1.f, ex - 14);
+#pragma unroll
+        for (int ks = 0; ks < NKS; ks++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float x = qv[ks][j] * up;
+                const _Float16 h = (_Float16)x;
+                qh[ks][j] = h;
+                ql[ks][j] = (_Float16)(x - (float)h);
+            }
+    }
+
+    const size_t rstride = (size_t)a.n_kv * HD;   // halves from one position to the next
+    const size_t lbase = ((size_t)a.layer * a.max_seq * a.n_kv + kvh) * HD;
+    const uint16_t* kbase = a.k_cache + lbase;
+    const uint16_t* vbase = a.v_cache + lbase;
+    uint4 kr[NK], vr[NV][2];
+    const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
+    auto fetch = [&](int c) {
+        const int c0 = 32 * c;
+#pragma unroll
+        for (int i = 0; i < NK; i++) {
+            const int idx = tid + 256 * i, p = c0 + idx / D8;
+            kr[i] = p <= maxpos ? *reinterpret_cast<const uint4*>(kbase + (size_t)p * rstride + (idx % D8) * 8) : z4;
+        }
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int idx = tid + 256 * i, p = c0 + 2 * (idx / D8);
+            const bool ok = idx < NVU;
+            const size_t off = (size_t)p * rstride + (idx % D8) * 8;
+            vr[i][0] = ok && p <= maxpos ? *reinterpret_cast<const uint4*>(vbase + off) : z4;
+            vr[i][1] = ok && p + 1 <= maxpos ? *reinterpret_cast<const uint4*>(vbase + off + rstride) : z4;
+        }
+    };
+    auto put = [&](int b) {
+#pragma unroll
+        for (int i = 0; i < NK; i++) {
+            const int idx = tid + 256 * i;
+            *reinterpret_cast<uint4*>(&kl[b][(idx / D8) * KS + (idx % D8) * 8]) = kr[i];
+        }
+        uint32_t* vw = reinterpret_cast<uint32_t*>(&vl[b][0]);
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int idx = tid + 256 * i;
+            if (idx < NVU) {
+                const int j = idx / D8, d0 = (idx % D8) * 8;
+                const uint32_t e0[4] = {vr[i][0].x, vr[i][0].y, vr[i][0].z, vr[i][0].w};
+                const uint32_t e1[4] = {vr[i][1].x, vr[i][1].y, vr[i][1].z, vr[i][1].w};
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const uint32_t lo = (e0[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+                    const uint32_t hi = (e1[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+                    vw[((d0 + e) * VS) / 2 + j] = lo | (hi << 16);
+                }
+            }
+        }
+    };
+
+    float4v o[NDT];
+#pragma unroll
+    for (int d = 0; d < NDT; d++) o[d] = float4v{0.f, 0.f, 0.f, 0.f};
+    float mrun = -INFINITY, lsum = 0.f;
+    fetch(0);
+    put(0);
+    __syncthreads();
+    for (int c = 0; c < nch; c++) {
+        if (c + 1 < nch) fetch(c + 1);
+        const uint16_t* kb = kl[c & 1];
+        const uint16_t* vb = vl[c & 1];
+        float4v sa = {0.f, 0.f, 0.f, 0.f}, sb = sa;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ks++) {
+            const half8v ka = *reinterpret_cast<const half8v*>(kb + n * KS + 32 * ks + 8 * g);
+            const half8v kb2 = *reinterpret_cast<const half8v*>(kb + (16 + n) * KS + 32 * ks + 8 * g);
+            sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[ks], sa, 0, 0, 0);
+            sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[ks], sa, 0, 0, 0);
+            sb = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb2, qh[ks], sb, 0, 0, 0);
+            sb = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb2, ql[ks], sb, 0, 0, 0);
+        }
+        // lane: positions c0 + 4g + i (tile a) and c0 + 16 + 4g + i (tile b) of row n
+        const int pa = 32 * c + 4 * g;
+        float s[8];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            s[i] = pa + i <= limit ? sa[i] * down : -INFINITY;
+            s[4 + i] = pa + 16 + i <= limit ? sb[i] * down : -INFINITY;
+        }
+        float mc = s[0];
+#pragma unroll
+        for (int i = 1; i < 8; i++) mc = fmaxf(mc, s[i]);
+        mc = fmaxf(mc, __shfl_xor(mc, 16, 64));
+        mc = fmaxf(mc, __shfl_xor(mc, 32, 64));
+        // position 0 is in every row's range, so the running maximum is
+        // finite from the first chunk on (alpha = 0 there)
+        const float mnew = fmaxf(mrun, mc);
+        const float alpha = exp2f(mrun - mnew);
+        mrun = mnew;
+        half8v ph, pl;
+        float ps = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float pj = exp2f(s[j] - mnew);
+            ps += pj;
+            const _Float16 h = (_Float16)pj;
+            ph[j] = h;
+            pl[j] = (_Float16)(pj - (float)h);
+        }
+        lsum = lsum * alpha + ps;
+#pragma unroll
+        for (int d = 0; d < NDT; d++) {
+            o[d] *= alpha;
+            const uint16_t* vrow = vb + (d * 16 + n) * VS;
+            const uint2 lo4 = *reinterpret_cast<const uint2*>(vrow + 4 * g);
+            const uint2 hi4 = *reinterpret_cast<const uint2*>(vrow + 16 + 4 * g);
+            const u32x4v vw = {lo4.x, lo4.y, hi4.x, hi4.y};
+            const half8v va = __builtin_bit_cast(half8v, vw);
+            o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph, o[d], 0, 0, 0);
+            o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl, o[d], 0, 0, 0);
+        }
+        if (c + 1 < nch) put((c + 1) & 1);
+        __syncthreads();
+    }
+    float l = lsum + __shfl_xor(lsum, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    if (valid) {
+        const float inv = 1.0f / l;
+        float* out = a.out + ((size_t)t * a.n_heads + head) * HD + 4 * g;
+#pragma unroll
+        for (int d = 0; d < NDT; d++)
+            *reinterpret_cast<float4*>(out + 16 * d) = make_float4(o[d][0] * inv, o[d][1] * inv, o[d][2] * inv, o[d][3] * inv);
+    }
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------------
@@ -3655,6 +3862,26 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
     }
 #undef GSD_ATTN_G
 #undef GSD_ATTN_L
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill_attention(const PrefillAttn& a, hipStream_t st) {
+    if (a.M <= 0) return hipSuccess;
+    if (!a.q || !a.k_cache || !a.v_cache || !a.out || a.n_kv <= 0 || a.n_heads % a.n_kv || a.p0 < 0 || a.layer < 0 ||
+        a.p0 + a.M > a.max_seq)
+        return hipErrorInvalidValue;
+    const int G = a.n_heads / a.n_kv;
+    if (G != 1 && G != 2 && G != 4 && G != 8) return hipErrorInvalidValue;
+    PrefillAttn b = a;
+    b.log2g = G == 1 ? 0 : (G == 2 ? 1 : (G == 4 ? 2 : 3));
+    const int T = 64 / G;
+    const dim3 grid((a.M + T - 1) / T, a.n_kv);
+    switch (a.hd) {
+        case 64: hipLaunchKernelGGL((attn_prefill_kernel<64>), grid, dim3(256), 0, st, b); break;
+        case 128: hipLaunchKernelGGL((attn_prefill_kernel<128>), grid, dim3(256), 0, st, b); break;
+        case 256: hipLaunchKernelGGL((attn_prefill_kernel<256>), grid, dim3(256), 0, st, b); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

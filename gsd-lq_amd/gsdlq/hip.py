@@ -42,6 +42,7 @@ SIGNATURES = {
     "gsdh_gqa_attention": [vp] + [vp] * 4 + [i32] * 6 + [f32],
     "gsdh_rope_store_gqa_attention": [vp] + [vp] * 6 + [i32] * 6 + [f32, i32, f32],
     "gsdh_gqa_attention_noalloc": [vp] + [vp] * 4 + [i32] * 6 + [f32],
+    "gsdh_prefill_attention": [vp] + [vp] * 4 + [i32] * 7 + [f32],
     "gsdh_unpack_codes": [vp, vp, i64, i32, vp, vp],
     "gsdh_model_create": [vp, ctypes.POINTER(vp)],
     "gsdh_model_destroy": [vp],

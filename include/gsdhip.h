@@ -140,6 +140,20 @@ int gsdh_rope_store_gqa_attention(void* stream, float* q, const float* k, const 
                                   int layer_idx, int pos, int n_heads, int n_kv_heads, int head_dim,
                                   int max_seq_len, float rope_theta, int interleaved, float sm_scale);
 
+/* gsd_cpu_gqa_attention (gsd_lq_cpu_engine.c:264-330) for n_tokens
+ * consecutive prompt tokens at once, on the matrix cores: token t (query rows
+ * q[t][n_heads][head_dim], RoPE applied, its K/V rows already stored at
+ * position pos0 + t) attends over cache positions 0 .. pos0 + t, and
+ * attn_out[t][n_heads][head_dim] is what gsdh_gqa_attention at pos0 + t
+ * returns (to fp32 rounding).  The reference prefills token by token
+ * (run_gpu_native_chat.py:1128-1130); this is the batched form the model's
+ * prefill uses.  head_dim 64, 128 or 256; n_heads/n_kv_heads 1, 2, 4 or 8;
+ * pos0 + n_tokens <= max_seq_len.  No workspace, nothing allocated. */
+int gsdh_prefill_attention(void* stream, const float* q, const uint16_t* k_cache,
+                           const uint16_t* v_cache, float* attn_out, int layer_idx, int pos0,
+                           int n_tokens, int n_heads, int n_kv_heads, int head_dim, int max_seq_len,
+                           float sm_scale);
+
 /* gsd_cpu_gqa_attention for callers that cannot allocate device memory (code
  * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
  * No counterpart in the reference.  Same arguments and results as

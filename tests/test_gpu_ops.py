@@ -264,6 +264,56 @@ def test_rope_store_attention_equals_two_calls(lib, ctx, nh, nkv, hd, il):
     assert np.array_equal(o0.view(np.uint32), o1.view(np.uint32)), rel_l2(o1, o0)
 
 
+@pytest.mark.parametrize("p0,M,nh,nkv,hd,layers,ms", [
+    (0, 512, 32, 8, 128, 1, 600),     # the 7B shape, a prompt's first 512 tokens
+    (512, 512, 32, 8, 128, 2, 1100),  # its next 512 (layer 1 of 2)
+    (37, 40, 8, 4, 64, 1, 96),        # 2 query heads per KV head, ragged groups
+    (70, 9, 8, 1, 256, 1, 90),        # 8 per KV head, head dim 256
+    (5, 70, 4, 4, 128, 1, 80),        # 1 per KV head
+    (0, 1, 32, 8, 128, 1, 8),         # one token at position 0
+    (100, 28, 16, 4, 128, 1, 128),    # the batch ends at the last cache row
+])
+def test_prefill_attention_vs_oracle(lib, p0, M, nh, nkv, hd, layers, ms):
+    """gsdh_prefill_attention: token t at position p0 + t over positions
+    0 .. p0 + t, against the oracle's one-token attention at that position,
+    for every token; cache rows past the batch hold NaN, which must not
+    reach the output.  Then the last token against gsdh_gqa_attention."""
+    banner(f"prefill attention p0 {p0} M {M} heads {nh}/{nkv} hd {hd}")
+    from gsdlq import pack
+    layer = layers - 1
+    n = layers * ms * nkv * hd
+    kc = pack.synth_f16(81, p0 + M, n, 1.0).reshape(layers, ms, nkv * hd)
+    vc = pack.synth_f16(82, p0 + M, n, 1.0).reshape(layers, ms, nkv * hd)
+    kc[layer, p0 + M:] = 0x7E00   # fp16 NaN past the context
+    vc[layer, p0 + M:] = 0x7E00
+    q = np.random.default_rng(p0 + M).standard_normal((M, nh * hd)).astype(np.float32)
+    sc = 1.0 / float(np.sqrt(hd))
+    want = np.zeros((M, nh * hd), np.float32)
+    ref = O.load("port")
+    for t in range(M):
+        ref.gsd_cpu_gqa_attention(O.P(q[t]), O.P(kc), O.P(vc), O.P(want[t]), layer, p0 + t, nh, nkv, hd, ms, sc)
+    dq, dk, dv, out = D(q), D(kc), D(vc), E(M * nh * hd * 4)
+    lib.gsdh_prefill_attention(None, p(dq), p(dk), p(dv), p(out), layer, p0, M, nh, nkv, hd, ms, sc)
+    got = H(out, np.float32, M * nh * hd).reshape(M, nh * hd)
+    assert np.isfinite(got).all()
+    worst = max(rel_l2(got[t], want[t]) for t in range(M))
+    assert worst < 1e-4, worst   # fp16 high + low operands: ~1e-6 measured
+    one = E(nh * hd * 4)
+    lib.gsdh_gqa_attention(None, p(D(q[M - 1])), p(dk), p(dv), p(one), layer, p0 + M - 1, nh, nkv, hd, ms, sc)
+    assert rel_l2(got[M - 1], H(one, np.float32, nh * hd)) < 1e-4
+
+
+def test_prefill_attention_rejects_bad_shapes(lib):
+    from gsdlq.hip import HipError
+    y = E(64)
+    with pytest.raises(HipError, match="max_seq_len"):
+        lib.gsdh_prefill_attention(None, p(y), p(y), p(y), p(y), 0, 100, 29, 32, 8, 128, 128, 0.088)
+    with pytest.raises(HipError, match="head_dim"):
+        lib.gsdh_prefill_attention(None, p(y), p(y), p(y), p(y), 0, 0, 4, 32, 8, 96, 128, 0.1)
+    with pytest.raises(HipError, match="query heads"):
+        lib.gsdh_prefill_attention(None, p(y), p(y), p(y), p(y), 0, 0, 4, 48, 3, 128, 128, 0.088)
+
+
 def test_attention_shape_changes_between_calls(lib):
     """One call per shape, in an order whose split-word regions overlap: 8 KV
     heads, then 2 KV heads of 256 dims, then 8 KV heads again (a word left by

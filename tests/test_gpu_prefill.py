@@ -62,7 +62,7 @@ def turbo_7b():
     sys.path.insert(0, ROOT)
     import bench
     bank = bench.LayerBank("turbo", 1)
-    model = bench.build_model(bank, 1)
+    model = bench.build_model(bank, 1, max_seq=640)
     yield bank, model
     model.close()
 
@@ -158,34 +158,34 @@ def layer_shape(name):
 
 def test_prefill_7b_turbo_chunks(turbo_7b):
     """The batched prefill forward of the 7B Turbo layer (32 / 8 heads of
-    128, ffn 14336, vocab 32768): 130 tokens (a 128-token chunk: gate / up on
-    four-group tiles, q / o / down on one group; then a 2-token chunk on
-    column-split tiles), then 64 more after that prefix (gate / up on
-    two-group tiles), against the oracle's token-by-token forward."""
+    128, ffn 14336, vocab 32768): 514 tokens (a 512-token chunk: eight-group
+    tiles with two row blocks per wave; then a 2-token chunk on column-split
+    tiles), then 64 more after that prefix (two-group tiles), against the
+    oracle's token-by-token forward."""
     import bench
     bank, model = turbo_7b
-    banner("batched prefill 7B turbo: 130 tokens, then 64 more")
+    banner("batched prefill 7B turbo: 514 tokens, then 64 more")
     lib = model.cl.lib
-    for M in (128, 2, 64):
+    for M in (512, 2, 64):
         print(f"[gpu-test] chunk {M}: gate/up plan {plan(lib, M, 14336, 4096)}, q plan {plan(lib, M, 4096, 4096)}, "
               f"down plan {plan(lib, M, 4096, 14336)}", flush=True)
-    ref = O.OracleModel(bench.BankSource(bank, 1), kind="port", max_seq_len=256, rope_interleaved=1)
-    toks = np.random.default_rng(130).integers(0, model.vocab_size, 194).tolist()
-    got = model.prefill(toks[:130], 0)
+    ref = O.OracleModel(bench.BankSource(bank, 1), kind="port", max_seq_len=640, rope_interleaved=1)
+    toks = np.random.default_rng(130).integers(0, model.vocab_size, 578).tolist()
+    got = model.prefill(toks[:514], 0)
     want = None
-    for pos in range(130):
-        want = ref.forward_token(toks[pos], pos, return_logits=pos == 129)
+    for pos in range(514):
+        want = ref.forward_token(toks[pos], pos, return_logits=pos == 513)
     e = rel_l2(got, want)
-    print(f"[prefill-parity] 7B turbo 130 tokens: last-position logits rel L2 {e:.2e}", flush=True)
+    print(f"[prefill-parity] 7B turbo 514 tokens: last-position logits rel L2 {e:.2e}", flush=True)
     assert e < 1e-3
-    _kv_close(model, ref, [0], [0, 64, 127, 128, 129])
-    got = model.prefill(toks[130:], 130)
-    for pos in range(130, 194):
-        want = ref.forward_token(toks[pos], pos, return_logits=pos == 193)
+    _kv_close(model, ref, [0], [0, 256, 511, 512, 513])
+    got = model.prefill(toks[514:], 514)
+    for pos in range(514, 578):
+        want = ref.forward_token(toks[pos], pos, return_logits=pos == 577)
     e = rel_l2(got, want)
     print(f"[prefill-parity] 7B turbo +64 tokens: last-position logits rel L2 {e:.2e}", flush=True)
     assert e < 1e-3
-    _kv_close(model, ref, [0], [130, 161, 193])
+    _kv_close(model, ref, [0], [514, 545, 577])
 
 
 def _small_model(spec):
@@ -276,7 +276,7 @@ def _kv_close(gpu, ref, layers, positions):
 
 PREFILL_CASES = [
     ("precision", 2, 1, 40, dict()),
-    ("turbo", 0, 1, 300, dict()),                        # three chunks (128, 128, 44)
+    ("turbo", 0, 1, 1100, dict()),                       # three chunks (512, 512, 76)
     ("precision", 1, 0, 33, dict(n_heads=8, n_kv_heads=8)),          # half-split RoPE, group size 1
     ("turbo", 1, 1, 130, dict(n_layers=1, hidden=512, ffn=1344, n_heads=8, n_kv_heads=2, head_dim=128,
                               vocab=1000)),              # ragged ffn, group size 4, hd 128
@@ -288,7 +288,7 @@ PREFILL_CASES = [
 @pytest.mark.parametrize("mode,kpr,il,n,shape", PREFILL_CASES)
 def test_prefill_vs_oracle(mode, kpr, il, n, shape):
     banner(f"batched prefill {mode} kinks {kpr} interleaved {il} n {n} {shape}")
-    gpu, ref = _pair(_spec(mode=mode, kinks_per_row=kpr, **shape), il=il)
+    gpu, ref = _pair(_spec(mode=mode, kinks_per_row=kpr, **shape), max_seq=max(512, n + 8), il=il)
     toks = np.random.default_rng(n).integers(0, gpu.vocab_size, n).tolist()
     got = gpu.prefill(toks, 0)
     want = None
