@@ -104,6 +104,11 @@ struct HexArgs {
         int ub1, ub2;          // first units of segments 1 and 2
         int units_q, units_r;  // units of matvec block b: units_q + (b < units_r)
         int nw;                // matvec waves per block (blocks may be larger: fa)
+        // paired gate/up launches: blocks b < su take, after their units_q
+        // whole units, half of unit su_u0 + b / 2 (rows 8 (b & 1) .. + 7 of
+        // gate and up; all waves of the block over the columns), so that
+        // every block streams the same bytes (0: no half units)
+        int su, su_u0;
     } mv;
 };
 

@@ -1984,9 +1984,9 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     if constexpr (FA) bdim = (unsigned)a.mv.nw * 64u;
     int cols0 = a.cols, epi0 = a.epilogue;
     int P = a.mv.P, wrl = a.mv.wr_log2, nunits = a.mv.nunits, ub1 = a.mv.ub1, ub2 = a.mv.ub2;
-    int units_q = a.mv.units_q, units_r = a.mv.units_r;
+    int units_q = a.mv.units_q, units_r = a.mv.units_r, su = a.mv.su, su_u0 = a.mv.su_u0;
     __asm__ volatile("" : "+s"(bdim), "+s"(cols0), "+s"(epi0), "+s"(P), "+s"(wrl), "+s"(nunits), "+s"(ub1), "+s"(ub2),
-                     "+s"(units_q), "+s"(units_r));
+                     "+s"(units_q), "+s"(units_r), "+s"(su), "+s"(su_u0));
     const int epi = EPI >= 0 ? EPI : epi0;
     const int NW = (int)(bdim >> 6);
     const int nc = (cols0 + 127) >> 7;
@@ -2029,8 +2029,17 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     // block's surplus loads meet on the same few HBM channels).
     // P >= 1 chunks per wave and unit (WR divides nc)
     const int u0 = (int)blockIdx.x - nlead;
-    const int my_units = u0 < nunits ? units_q + (u0 < units_r ? 1 : 0) : 0;
-    const int nsteps = P * my_units;
+    const int my_full = u0 < nunits ? units_q + (u0 < units_r ? 1 : 0) : 0;
+    // half units (paired launches with a shared codebook and ranks 0 or 2):
+    // the block's last unit is then rows 8 hs .. 8 hs + 7 of gate and of up
+    // of unit su_unit, in the 16 columns of the matrix-core tile (lanes
+    // 0-7: gate, 8-15: up), and each wave takes P / 2 of its chunks (group
+    // 0 the first half, group 1 the second: every chunk once)
+    constexpr bool kSU = TB > 0 && EPI == kEpiSwiGLU && (LR == 0 || LR == 3);
+    const bool has_su = kSU && u0 < su;
+    const int my_units = my_full + (has_su ? 1 : 0);
+    const int su_unit = su_u0 + (u0 >> 1), hs = u0 & 1;
+    const int nsteps = P * my_full + (has_su ? P >> 1 : 0);
     // code tiles: 7-bit for codebooks of at most 128 points (TB > 0: known
     // here; TB == 0: per segment, bit g of b7m)
     constexpr bool kB7 = TB > 0 && TB <= 128;
@@ -2040,10 +2049,32 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     auto seg_b7 = [&](int g) { return TB > 0 ? kB7 : ((b7m >> g) & 1u) != 0; };
     const uint32_t lof8 = tile_lane_off(false, lane), lof7 = tile_lane_off(true, lane);
     int lk = 0, lj = 0, lts = tile_bytes(kB7);
-    uint32_t lof = kB7 ? lof7 : lof8;
+    uint32_t lof = kB7 ? lof7 : lof8, lso = (uint32_t)(lane & 15);
+    int lP = P, lp0 = 0;   // steps of the loaded unit, and its first local chunk
     const unsigned char* lcb = nullptr;
     const uint32_t* lsb = nullptr;
+    // half unit: gate and up tiles addressed from the lower of the two
+    // bases with a per-lane 32-bit offset (the launcher checks that both
+    // tensors lie within 4 GiB of it); lane l loads the word of row
+    // 8 hs + (l & 7) of its tensor (l & 8: up), in the lane slot of that row
     auto lset = [&](int k) {
+        if (kSU && has_su && min(k, my_units - 1) == my_full) {
+            const unsigned char* c0p = reinterpret_cast<const unsigned char*>(kseg[0].codes_t);
+            const unsigned char* c1p = reinterpret_cast<const unsigned char*>(kseg[1].codes_t);
+            const uint32_t* s0p = kseg[0].scales_t;
+            const uint32_t* s1p = kseg[1].scales_t;
+            const unsigned char* cb = c0p < c1p ? c0p : c1p;
+            const uint32_t* sb = s0p < s1p ? s0p : s1p;
+            const bool upl = (lane & 8) != 0;
+            const int rl = 8 * hs + (lane & 7);
+            lcb = cb + (size_t)su_unit * nc * lts;
+            lsb = sb + (size_t)su_unit * nc * 16;
+            lof = (uint32_t)((upl ? c1p : c0p) - cb) + tile_lane_off(kB7, (lane & 48) | rl);
+            lso = (uint32_t)((upl ? s1p : s0p) - sb) + (uint32_t)rl;
+            lP = P >> 1;
+            lp0 = grp * (P >> 1);
+            return;
+        }
         const int uu = min(u0 + min(k, max(my_units - 1, 0)) * nblk, nunits - 1);
         const int g = seg_of(uu);
         const int rb = paired ? uu : uu - ubase(g);
@@ -2055,10 +2086,10 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
         lsb = kseg[g].scales_t + (size_t)rb * nc * 16;
     };
     auto lissue = [&](uint4& cw, uint32_t& sw) {
-        const int c = wr + lj * WR;
+        const int c = wr + (lj + lp0) * WR;
         cw = tile_load(lcb + (size_t)c * lts + lof);
-        sw = lsb[c * 16 + (lane & 15)];
-        if (++lj == P) {
+        sw = lsb[c * 16 + lso];
+        if (++lj == lP) {
             lj = 0;
             lset(++lk);
         }
@@ -2236,6 +2267,15 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
 #pragma unroll
         for (int k = 0; k < kMv4PreUnits; k++) {
             if (k >= my_units) break;
+            if (kSU && has_su && k == my_full) {
+                if constexpr (LR == 3) {   // U row (an fp16 pair) of the lane's gate or up row
+                    const int r = min(su_unit * 16 + 8 * hs + (lane & 7), kseg[0].rows - 1);
+                    const uint32_t* u0p = reinterpret_cast<const uint32_t*>(kseg[0].U);
+                    const uint32_t* u1p = reinterpret_cast<const uint32_t*>(kseg[1].U);
+                    eup[k][0] = ((lane & 8) ? u1p : u0p)[r];
+                }
+                break;
+            }
             const int uu = u0 + k * nblk;
             const int g = seg_of(uu);
             const int prow = (paired ? uu : uu - ubase(g)) * 16 + lane;
@@ -2392,7 +2432,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     };
 
     int rbuf = 0, uk = 0;   // uk: the block's unit ordinal (epilogue input slot)
-    auto unit_end = [&](int u, float& acc) {
+    auto unit_end = [&](int u, float& acc, bool half) {
         const int g = seg_of(u);
         if (lane < 16) red[rbuf][wid][lane] = acc * down;
         acc = 0.f;
@@ -2423,98 +2463,124 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                     have |= 0x100u;
                 }
             }
-            float fin0 = 0.f, fin1 = 0.f;
-#pragma unroll
-            for (int gi = 0; gi < 2; gi++) {
-                if (gi >= G) break;
-                const int sg_i = paired ? gi : g;
-                KSeg& sg = kseg[sg_i];
-                const int rb = paired ? u : u - ubase(sg_i);
-                const int row = rb * 16 + lane;
+            if (kSU && half) {
+                // half unit: lane l holds row 8 hs + (l & 7) of gate (l < 8)
+                // or up (l >= 8), the sum over every wave's own chunks
                 float t = 0.f;
-                for (int w = 0; w < WR; w++) t += red[rbuf][gi * WR + w][lane];
+                for (int w = 0; w < NW; w++) t += red[rbuf][w][lane];
                 t *= inv;
-                if (row < sg.rows) {
-                    if (sg.row_ptr) {
-                        const uint32_t e = sg.row_ptr[row + 1];
-                        for (uint32_t i = sg.row_ptr[row]; i < e; i++) t += sg.kdel[i] * xnorm(a, sg.kcols[i], inv);
+                const int sg = lane >> 3;
+                const int row = u * 16 + 8 * hs + (lane & 7);
+                if (row < kseg[0].rows) {
+                    const uint32_t* rp = sg ? kseg[1].row_ptr : kseg[0].row_ptr;
+                    if (rp) {
+                        const uint16_t* kcl = sg ? kseg[1].kcols : kseg[0].kcols;
+                        const float* kdl = sg ? kseg[1].kdel : kseg[0].kdel;
+                        const uint32_t e = rp[row + 1];
+                        for (uint32_t i = rp[row]; i < e; i++) t += kdl[i] * xnorm(a, kcl[i], inv);
                     }
-                    if (LR > 0 && (kR2 || sg.k > 0)) {
-                        if (LR == 2 && !((have >> sg_i) & 1u)) {
-                            // bounded wait for the published rank-k words of
-                            // this segment (normally already there)
-                            int off = 0;
-                            for (int g2 = 0; g2 < sg_i; g2++)
-                                if (!a.seg[g2].tmp_k && a.seg[g2].k > 0) off += a.seg[g2].k;
-                            int spins = 0;
-                            for (int jj = 0; jj < sg.k; jj++) {
-                                unsigned long long wv;
-                                while (((wv = __hip_atomic_load(&a.pub[off + jj], __ATOMIC_RELAXED,
-                                                                __HIP_MEMORY_SCOPE_AGENT)) >> 32) == 0 &&
-                                       spins < (1 << 20)) {
-                                    if (++spins == (1 << 20)) *a.err = 1u;
-                                    __builtin_amdgcn_s_sleep(1);
-                                }
-                                tkl[sg_i][jj] = __uint_as_float((unsigned)wv);
-                            }
-                            have |= 1u << sg_i;
-                        }
-                        if (kIn || sg.k <= 2) {   // prefetched factors, same order as below
-                            // (the asm keeps the use, and the wait for the
-                            // load, inside this branch: hoisted, it would wait
-                            // for the code loads in flight in every launch)
-                            uint32_t uw = lup[uk][gi][lane];
-                            if (!kR2 && sg.k == 1) uw >>= 16 * (row & 1);   // U[row] of the aligned pair
-                            t += h2f((uint16_t)(uw & 0xFFFFu)) * tkl[sg_i][0];
-                            if (kR2 || sg.k == 2) t += h2f((uint16_t)(uw >> 16)) * tkl[sg_i][1];
-                        } else {
-                            const uint16_t* up_ = sg.U + (size_t)row * sg.k;
-                            for (int jj = 0; jj < sg.k; jj++) t += h2f(up_[jj]) * tkl[sg_i][jj];
-                        }
+                    if constexpr (LR == 3) {
+                        const uint32_t uw = lup[uk][0][lane];
+                        t += h2f((uint16_t)(uw & 0xFFFFu)) * tkl[sg][0];
+                        t += h2f((uint16_t)(uw >> 16)) * tkl[sg][1];
                     }
                 }
-                if (gi == 0) fin0 = t;
-                else fin1 = t;
-            }
-            KSeg& s0 = kseg[paired ? 0 : g];
-            const int row = (paired ? u : u - ubase(g)) * 16 + lane;
-            if (paired) {
-                if (row < s0.rows) s0.out[row] = (fin0 / (1.0f + expf(-fin0))) * fin1;
-            } else if (epi == kEpiStore) {
-                if (row < s0.rows) s0.out[row] = fin0;
-            } else if (epi == kEpiResidual) {
-                if (row < s0.rows) a.resid[row] = lpre[kHasPre ? uk : 0][lane] + fin0;
+                const float upv = __shfl_xor(t, 8, 64);   // lanes 0-7: the up row's value
+                if (lane < 8 && row < kseg[0].rows) kseg[0].out[row] = (t / (1.0f + expf(-t))) * upv;
             } else {
-                // kEpiRopeKV: rows 2i, 2i+1 of a head are one rotation pair
-                // (interleaved RoPE, gsd_lq_cpu_engine.c:213-256) in lanes
-                // 2i, 2i+1; evaluated without contraction like the reference
-#pragma clang fp contract(off)
-                const RopeKV& r = a.rope;
-                const float partner = __shfl_xor(fin0, 1, 64);
-                const size_t base = ((size_t)r.layer * r.max_seq + (size_t)rpos) * (size_t)r.n_kv * r.hd;
-                const bool odd = (lane & 1) != 0;
-                const float x0 = odd ? partner : fin0, x1 = odd ? fin0 : partner;
-                const float2 cs = lcs[kHasCs ? uk : 0][lane];
-                const float y = g == 2 ? fin0 : (odd ? (x0 * cs.y + x1 * cs.x) : (x0 * cs.x - x1 * cs.y));
-                if (row < s0.rows) {
-                    if (g == 2) r.v_cache[base + row] = f2h(y);
-                    else if (g == 0) s0.out[row] = y;
-                    else r.k_cache[base + row] = f2h(y);
+                float fin0 = 0.f, fin1 = 0.f;
+    #pragma unroll
+                for (int gi = 0; gi < 2; gi++) {
+                    if (gi >= G) break;
+                    const int sg_i = paired ? gi : g;
+                    KSeg& sg = kseg[sg_i];
+                    const int rb = paired ? u : u - ubase(sg_i);
+                    const int row = rb * 16 + lane;
+                    float t = 0.f;
+                    for (int w = 0; w < WR; w++) t += red[rbuf][gi * WR + w][lane];
+                    t *= inv;
+                    if (row < sg.rows) {
+                        if (sg.row_ptr) {
+                            const uint32_t e = sg.row_ptr[row + 1];
+                            for (uint32_t i = sg.row_ptr[row]; i < e; i++) t += sg.kdel[i] * xnorm(a, sg.kcols[i], inv);
+                        }
+                        if (LR > 0 && (kR2 || sg.k > 0)) {
+                            if (LR == 2 && !((have >> sg_i) & 1u)) {
+                                // bounded wait for the published rank-k words of
+                                // this segment (normally already there)
+                                int off = 0;
+                                for (int g2 = 0; g2 < sg_i; g2++)
+                                    if (!a.seg[g2].tmp_k && a.seg[g2].k > 0) off += a.seg[g2].k;
+                                int spins = 0;
+                                for (int jj = 0; jj < sg.k; jj++) {
+                                    unsigned long long wv;
+                                    while (((wv = __hip_atomic_load(&a.pub[off + jj], __ATOMIC_RELAXED,
+                                                                    __HIP_MEMORY_SCOPE_AGENT)) >> 32) == 0 &&
+                                           spins < (1 << 20)) {
+                                        if (++spins == (1 << 20)) *a.err = 1u;
+                                        __builtin_amdgcn_s_sleep(1);
+                                    }
+                                    tkl[sg_i][jj] = __uint_as_float((unsigned)wv);
+                                }
+                                have |= 1u << sg_i;
+                            }
+                            if (kIn || sg.k <= 2) {   // prefetched factors, same order as below
+                                // (the asm keeps the use, and the wait for the
+                                // load, inside this branch: hoisted, it would wait
+                                // for the code loads in flight in every launch)
+                                uint32_t uw = lup[uk][gi][lane];
+                                if (!kR2 && sg.k == 1) uw >>= 16 * (row & 1);   // U[row] of the aligned pair
+                                t += h2f((uint16_t)(uw & 0xFFFFu)) * tkl[sg_i][0];
+                                if (kR2 || sg.k == 2) t += h2f((uint16_t)(uw >> 16)) * tkl[sg_i][1];
+                            } else {
+                                const uint16_t* up_ = sg.U + (size_t)row * sg.k;
+                                for (int jj = 0; jj < sg.k; jj++) t += h2f(up_[jj]) * tkl[sg_i][jj];
+                            }
+                        }
+                    }
+                    if (gi == 0) fin0 = t;
+                    else fin1 = t;
                 }
-                if constexpr (FA) {
-                    // the same values for the attention blocks: q rows as
-                    // fp32, K / V rows as the cache's fp16 pairs (rows 2i,
-                    // 2i + 1 in the even lane's word)
-                    const uint32_t hp = (uint32_t)f2h(y) | ((uint32_t)f2h(__shfl_xor(y, 1, 64)) << 16);
-                    const unsigned long long tag = (unsigned long long)fa_tag << 32;
-                    const int qd = r.n_heads * r.hd, kvd = r.n_kv * r.hd;
+                KSeg& s0 = kseg[paired ? 0 : g];
+                const int row = (paired ? u : u - ubase(g)) * 16 + lane;
+                if (paired) {
+                    if (row < s0.rows) s0.out[row] = (fin0 / (1.0f + expf(-fin0))) * fin1;
+                } else if (epi == kEpiStore) {
+                    if (row < s0.rows) s0.out[row] = fin0;
+                } else if (epi == kEpiResidual) {
+                    if (row < s0.rows) a.resid[row] = lpre[kHasPre ? uk : 0][lane] + fin0;
+                } else {
+                    // kEpiRopeKV: rows 2i, 2i+1 of a head are one rotation pair
+                    // (interleaved RoPE, gsd_lq_cpu_engine.c:213-256) in lanes
+                    // 2i, 2i+1; evaluated without contraction like the reference
+    #pragma clang fp contract(off)
+                    const RopeKV& r = a.rope;
+                    const float partner = __shfl_xor(fin0, 1, 64);
+                    const size_t base = ((size_t)r.layer * r.max_seq + (size_t)rpos) * (size_t)r.n_kv * r.hd;
+                    const bool odd = (lane & 1) != 0;
+                    const float x0 = odd ? partner : fin0, x1 = odd ? fin0 : partner;
+                    const float2 cs = lcs[kHasCs ? uk : 0][lane];
+                    const float y = g == 2 ? fin0 : (odd ? (x0 * cs.y + x1 * cs.x) : (x0 * cs.x - x1 * cs.y));
                     if (row < s0.rows) {
-                        if (g == 0)
-                            __hip_atomic_store(a.fa.words + row, tag | __float_as_uint(y), __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-                        else if (!odd)
-                            __hip_atomic_store(a.fa.words + qd + (g == 2 ? kvd / 2 : 0) + (row >> 1), tag | hp,
-                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        if (g == 2) r.v_cache[base + row] = f2h(y);
+                        else if (g == 0) s0.out[row] = y;
+                        else r.k_cache[base + row] = f2h(y);
+                    }
+                    if constexpr (FA) {
+                        // the same values for the attention blocks: q rows as
+                        // fp32, K / V rows as the cache's fp16 pairs (rows 2i,
+                        // 2i + 1 in the even lane's word)
+                        const uint32_t hp = (uint32_t)f2h(y) | ((uint32_t)f2h(__shfl_xor(y, 1, 64)) << 16);
+                        const unsigned long long tag = (unsigned long long)fa_tag << 32;
+                        const int qd = r.n_heads * r.hd, kvd = r.n_kv * r.hd;
+                        if (row < s0.rows) {
+                            if (g == 0)
+                                __hip_atomic_store(a.fa.words + row, tag | __float_as_uint(y), __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+                            else if (!odd)
+                                __hip_atomic_store(a.fa.words + qd + (g == 2 ? kvd / 2 : 0) + (row >> 1), tag | hp,
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        }
                     }
                 }
             }
@@ -2526,12 +2592,18 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     float acc = 0.f;
     int cj = 0, ck = 0, cu = u0;
     int cg = seg_of(min(u0, nunits - 1));
+    int cP = P, cp0 = 0;   // steps of the computed unit, and its first local chunk
     auto cadvance = [&]() {
-        if (++cj == P) {
-            if (ck < my_units) unit_end(cu, acc);
+        if (++cj == cP) {
+            if (ck < my_units) unit_end(cu, acc, kSU && has_su && ck == my_full);
             cj = 0;
             ++ck;
             cu += nblk;
+            if (kSU && has_su && ck == my_full) {
+                cu = su_unit;
+                cP = P >> 1;
+                cp0 = grp * (P >> 1);
+            }
             cg = seg_of(min(cu, nunits - 1));
         }
     };
@@ -2542,7 +2614,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     for (int s = 0; s < nsteps; s += kMv4Depth) {
 #pragma unroll
         for (int i = 0; i < kMv4Depth; i++) {
-            step(cg, cj, cw[i], sw[i], acc);
+            step(cg, cj + cp0, cw[i], sw[i], acc);
             lissue(cw[i], sw[i]);
             cadvance();
         }
@@ -3397,6 +3469,22 @@ hipError_t launch_hexmv(const HexArgs& a, hipStream_t st) {
 #undef GSD_HEXMV_DISPATCH
 }
 
+// Half units of a paired launch (GSD_GATEUP_HALVES=0 turns them off, to
+// compare the two plans), and whether gate's and up's tiles and scales lie
+// within 4 GiB of the lower base, as the kernel's 32-bit lane offsets need.
+static bool half_units_on() {
+    const char* e = std::getenv("GSD_GATEUP_HALVES");
+    return !(e && e[0] == '0');
+}
+static bool half_units_reach(const HexArgs& a) {
+    const HexSeg &g = a.seg[0], &u = a.seg[1];
+    const uint64_t nrb = (uint64_t)(g.rows + 15) / 16, nc = (uint64_t)(a.cols + 127) / 128;
+    const uint64_t tb = g.n_pts <= 128 ? kTile7 : kTileU8;
+    auto span = [](uint64_t p, uint64_t q, uint64_t n) { return (p > q ? p : q) + n - (p < q ? p : q); };
+    return span((uint64_t)(uintptr_t)g.codes_t, (uint64_t)(uintptr_t)u.codes_t, nrb * nc * tb) < (1ull << 32) &&
+           span((uint64_t)(uintptr_t)g.scales_t, (uint64_t)(uintptr_t)u.scales_t, nrb * nc * 64) < (1ull << 32);
+}
+
 template <int TB, int LR, int EPI>
 hipError_t launch_hexmv4_t(const HexArgs& a0, hipStream_t st, int nw, size_t lds, int nunits, int nlead) {
     static int per_cu = 0;
@@ -3425,6 +3513,18 @@ hipError_t launch_hexmv4_t(const HexArgs& a0, hipStream_t st, int nw, size_t lds
     HexArgs a = a0;
     a.mv.units_q = nunits / grid;
     a.mv.units_r = nunits % grid;
+    a.mv.su = 0;
+    a.mv.su_u0 = 0;
+    if constexpr (TB > 0 && EPI == kEpiSwiGLU && (LR == 0 || LR == 3)) {
+        // the last, partial round of units as half units on twice the
+        // blocks (gate/up 7B: 896 units on 256 blocks, 3.5 each)
+        const int R = nunits % grid;
+        if (R > 0 && 2 * R <= grid && a.mv.P % 2 == 0 && half_units_on() && half_units_reach(a)) {
+            a.mv.units_r = 0;
+            a.mv.su = 2 * R;
+            a.mv.su_u0 = a.mv.units_q * grid;
+        }
+    }
     hipLaunchKernelGGL((hexmv4_kernel<TB, LR, EPI>), dim3(grid + nlead), dim3(nw * 64), lds, st, a);
     return hipGetLastError();
 }

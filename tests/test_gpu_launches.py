@@ -134,6 +134,40 @@ def test_gate_up_launch_full_shape(layer7b):
     _check(f"{mode} gate/up (2x14336x4096) + SwiGLU", got, g)
 
 
+@pytest.mark.parametrize("mode", ["turbo", "precision"])
+@pytest.mark.parametrize("halves", ["1", "0"])
+def test_gate_up_half_units_ragged(mode, halves, monkeypatch):
+    """gate/up 2 x 5056 x 2048: 316 units on a 256-CU device's 256 blocks,
+    the last 60 as half units on 120 blocks (rows 8h .. 8h + 7 of gate and
+    up per block, each wave one of its two chunks); and the same launch with
+    the half units off (GSD_GATEUP_HALVES=0)."""
+    from gsdlq import synth
+    import run_gpu_native_chat as chat
+    monkeypatch.setenv("GSD_GATEUP_HALVES", halves)
+    banner(f"gate/up 2x5056x2048 {mode}, half units {halves}")
+    spec = synth.SynthSpec(n_layers=1, hidden=2048, ffn=5056, n_heads=16, n_kv_heads=4, head_dim=128, vocab=512,
+                           mode=mode, kinks_per_row=2)
+    src = synth.SynthSource(spec)
+    gpu = chat.GPUMistralV2Model(src, max_seq_len=16, verbose=False)
+    ref = O.OracleModel(src, kind="port", max_seq_len=16)
+    try:
+        x = np.random.default_rng(107).standard_normal(gpu.hidden).astype(np.float32)
+        _put(gpu, "x", x)
+        gpu.cl.lib.gsdh_model_run_linear(gpu._m, 0, 4)
+        got = _get(gpu, "h", gpu.ffn_size)
+        ly = ref.layers[0]
+        xb = _rmsnorm(ref, x, ly["ffn_norm"])
+        g = np.empty(gpu.ffn_size, np.float32)
+        u = np.empty(gpu.ffn_size, np.float32)
+        ref.matvec(xb, ly["gate"], g)
+        ref.matvec(xb, ly["up"], u)
+        ref.lib.gsd_cpu_swiglu(O.P(g), O.P(u), O.P(g), gpu.ffn_size)
+        _check(f"{mode} gate/up 2x5056x2048 halves {halves}", got, g)
+        assert rel_l2(got[4096:], g[4096:]) < GUARD   # the rows of the last round
+    finally:
+        gpu.close()
+
+
 def test_down_launch_full_shape(layer7b):
     mode, gpu, ref = layer7b
     rng = np.random.default_rng(104)
