@@ -254,10 +254,6 @@ struct AttnArgs {
     // wait_skew, which no split writes, so the bounded wait runs out and
     // sets *err while every block still finishes
     int wait_skew;
-    // ntok > 1: a batch of consecutive query tokens (prefill; causal): token
-    // z = grid.z index at position pos + z, q / out rows z * n_heads * hd, its
-    // words at ws + z * n_kv * max_splits * group * (2 + hd); needs epoch.
-    int ntok;
     // one-token matrix-core kernel: blocks that merge a KV head's splits
     // (0 or 1: the last split's; up to 8 when every block of the grid is
     // resident at once; set by the launcher)

@@ -625,15 +625,13 @@ __global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
     } else {
         ep0 = a.epoch ? a.epoch - 1u : (a.counters ? a.counters[kvh] : 0u);
     }
-    // token z of a batch (prefill; decode: z = 0) at position pos + z
-    const int z = blockIdx.z;
-    const int pos = (a.pos_dev ? *a.pos_dev : a.pos) + z;
+    const int pos = a.pos_dev ? *a.pos_dev : a.pos;
     const int n = pos + 1;
     const int nsplit = (n + a.chunk - 1) / a.chunk;
     const int split = blockIdx.y;
     if (split >= nsplit) return;
-    const float* qz = a.q + (size_t)z * a.n_heads * HD;
-    float* outz = a.out + (size_t)z * a.n_heads * HD;
+    const float* qz = a.q;
+    float* outz = a.out;
     const int t0 = split * a.chunk;
     const int t1 = min(n, t0 + a.chunk);
     const int cn = t1 - t0;
@@ -766,7 +764,7 @@ __global__ void __launch_bounds__(NW * 64) attn_kernel(const AttnArgs a) {
     // no fence, and the merge reads spread over G blocks
     const unsigned ep = ep0 + 1u;
     const unsigned long long tag = (unsigned long long)ep << 32;
-    unsigned long long* wsk = a.ws + ((size_t)z * a.n_kv + kvh) * a.max_splits * G * (2 + HD);
+    unsigned long long* wsk = a.ws + (size_t)kvh * a.max_splits * G * (2 + HD);
     {
         unsigned long long* wsb = wsk + (size_t)split * G * (2 + HD);
         for (int i = tid; i < G * HD; i += NT) {
@@ -3864,7 +3862,7 @@ static int attn_mergers(int blocks) {
 hipError_t launch_rope_attention(const AttnArgs& a, const float* k, const float* v, int interleaved,
                                  const float2* cs, hipStream_t st) {
     const int G = a.n_kv > 0 ? a.n_heads / a.n_kv : 0;
-    if (a.pos_dev || a.ntok > 1 || !a.ws || (a.max_splits > 1 && !a.epoch && !a.dep) || !(G == 1 || G == 2 || G == 4) ||
+    if (a.pos_dev || !a.ws || (a.max_splits > 1 && !a.epoch && !a.dep) || !(G == 1 || G == 2 || G == 4) ||
         !(a.hd == 64 || a.hd == 128) ||
         !(a.chunk == 64 || a.chunk == 128 || a.chunk == 256) || a.max_splits > kAttnDecSplits)
         return hipErrorNotSupported;
@@ -3913,14 +3911,13 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
     if (a.max_splits < 1 || a.max_splits > 256 || a.chunk > 256 || !a.ws ||
         (a.max_splits > 1 && !a.counters && !a.epoch && !a.dep))
         return hipErrorInvalidValue;
-    const int nt = a.ntok > 1 ? a.ntok : 1;
-    if (nt > 1 && (!a.epoch || a.pos_dev)) return hipErrorInvalidValue;
-    // the device epoch word counts every block's arrival: no block may leave
-    // before it (a device position lets blocks past the context leave early)
-    if (a.dep && (a.pos_dev || nt > 1 || a.epoch || a.counters)) return hipErrorInvalidValue;
+    // the device epoch advances once every KV head's last split has merged:
+    // the launch's split count must be the host's (a device position lets
+    // blocks past the context leave early)
+    if (a.dep && (a.pos_dev || a.epoch || a.counters)) return hipErrorInvalidValue;
     const int G = a.n_heads / a.n_kv;
     // one token, G <= 4, head dim 64 / 128: the matrix-core kernel
-    if (nt == 1 && (G == 1 || G == 2 || G == 4) && (a.hd == 64 || a.hd == 128) &&
+    if ((G == 1 || G == 2 || G == 4) && (a.hd == 64 || a.hd == 128) &&
         (a.chunk == 64 || a.chunk == 128 || a.chunk == 256) && a.max_splits <= kAttnDecSplits) {
         const dim3 grid(a.n_kv, a.max_splits);
         AttnArgs b = a;
@@ -3941,7 +3938,7 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
 #undef GSD_ATTN_P
         return hipGetLastError();
     }
-    const dim3 grid(a.n_kv, a.max_splits, nt);
+    const dim3 grid(a.n_kv, a.max_splits);
     // 16 waves for up to 4 query heads per KV head (8 would not fit the
     // registers of 16), else 4
 #define GSD_ATTN_L(HD, GG) \
