@@ -416,6 +416,8 @@ def probe(kind: str, n: int, ctx: int = 8192, m: int = 128):
     'copy' = a 256 MiB device copy (the calibration of FETCH/WRITE_SIZE),
     'attn' = RoPE + K/V append and decode attention at context `ctx`,
     'prefill' = the batched projection of 8 Turbo layer sets for `m` tokens,
+    'prompt' = an `m`-token prompt through the batched prefill of the 32-layer
+    7B Precision model, `n` times,
     'decode' = `n` greedy tokens of the 32-layer 7B Precision model."""
     from gsdlq import hip
     lib = hip.lib()
@@ -426,6 +428,18 @@ def probe(kind: str, n: int, ctx: int = 8192, m: int = 128):
     if kind == "prefill":
         r = bench_prefill(LayerBank("turbo", 8), ms=(m,), reps=n)
         print(f"[probe] prefill M {m}: {r}", flush=True)
+        return
+    if kind == "prompt":
+        bank = LayerBank("precision", 3)
+        model = build_model(bank, 32, max_seq=m + 8)
+        toks = np.random.default_rng(5).integers(0, V, m).tolist()
+        model.prefill(toks, 0, return_logits=False)   # warm
+        t0 = time.time()
+        for _ in range(n):
+            model.prefill(toks, 0)
+        dt = (time.time() - t0) / n
+        model.close()
+        print(f"[probe] {m}-token prompt, 32-layer 7B Precision: {dt * 1e3:.2f} ms ({m / dt:.0f} tok/s)", flush=True)
         return
     if kind == "decode":
         bank = LayerBank("precision", 3)
@@ -569,10 +583,10 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-attention", action="store_true")
     ap.add_argument("--no-c1", action="store_true")
-    ap.add_argument("--probe", choices=["gateup", "copy", "attn", "prefill", "decode"],
+    ap.add_argument("--probe", choices=["gateup", "copy", "attn", "prefill", "prompt", "decode"],
                     help="run one kernel for rocprofv3 counters")
     ap.add_argument("--ctx", type=int, default=8192, help="--probe attn: context length")
-    ap.add_argument("--m", type=int, default=128, help="--probe prefill: tokens")
+    ap.add_argument("--m", type=int, default=128, help="--probe prefill / prompt: tokens")
     a = ap.parse_args()
     if a.probe:
         probe(a.probe, max(a.steps, 1), a.ctx, a.m)

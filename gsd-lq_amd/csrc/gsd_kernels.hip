@@ -2028,12 +2028,14 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     // P >= 1 chunks per wave and unit (WR divides nc)
     const int u0 = (int)blockIdx.x - nlead;
     const int my_full = u0 < nunits ? units_q + (u0 < units_r ? 1 : 0) : 0;
-    // half units (paired launches with a shared codebook and ranks 0 or 2):
+    // half units (paired launches with a shared codebook and no rank-k term;
+    // with the rank-2 term the extra cursor state spilled scalar registers
+    // and the launch ran ~3 us slower in decode):
     // the block's last unit is then rows 8 hs .. 8 hs + 7 of gate and of up
     // of unit su_unit, in the 16 columns of the matrix-core tile (lanes
     // 0-7: gate, 8-15: up), and each wave takes P / 2 of its chunks (group
     // 0 the first half, group 1 the second: every chunk once)
-    constexpr bool kSU = TB > 0 && EPI == kEpiSwiGLU && (LR == 0 || LR == 3);
+    constexpr bool kSU = TB > 0 && EPI == kEpiSwiGLU && LR == 0;
     const bool has_su = kSU && u0 < su;
     const int my_units = my_full + (has_su ? 1 : 0);
     const int su_unit = su_u0 + (u0 >> 1), hs = u0 & 1;
@@ -2265,15 +2267,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
 #pragma unroll
         for (int k = 0; k < kMv4PreUnits; k++) {
             if (k >= my_units) break;
-            if (kSU && has_su && k == my_full) {
-                if constexpr (LR == 3) {   // U row (an fp16 pair) of the lane's gate or up row
-                    const int r = min(su_unit * 16 + 8 * hs + (lane & 7), kseg[0].rows - 1);
-                    const uint32_t* u0p = reinterpret_cast<const uint32_t*>(kseg[0].U);
-                    const uint32_t* u1p = reinterpret_cast<const uint32_t*>(kseg[1].U);
-                    eup[k][0] = ((lane & 8) ? u1p : u0p)[r];
-                }
-                break;
-            }
+            if (kSU && has_su && k == my_full) break;   // (a half unit has no epilogue inputs)
             const int uu = u0 + k * nblk;
             const int g = seg_of(uu);
             const int prow = (paired ? uu : uu - ubase(g)) * 16 + lane;
@@ -2476,11 +2470,6 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                         const float* kdl = sg ? kseg[1].kdel : kseg[0].kdel;
                         const uint32_t e = rp[row + 1];
                         for (uint32_t i = rp[row]; i < e; i++) t += kdl[i] * xnorm(a, kcl[i], inv);
-                    }
-                    if constexpr (LR == 3) {
-                        const uint32_t uw = lup[uk][0][lane];
-                        t += h2f((uint16_t)(uw & 0xFFFFu)) * tkl[sg][0];
-                        t += h2f((uint16_t)(uw >> 16)) * tkl[sg][1];
                     }
                 }
                 const float upv = __shfl_xor(t, 8, 64);   // lanes 0-7: the up row's value
@@ -3513,7 +3502,7 @@ hipError_t launch_hexmv4_t(const HexArgs& a0, hipStream_t st, int nw, size_t lds
     a.mv.units_r = nunits % grid;
     a.mv.su = 0;
     a.mv.su_u0 = 0;
-    if constexpr (TB > 0 && EPI == kEpiSwiGLU && (LR == 0 || LR == 3)) {
+    if constexpr (TB > 0 && EPI == kEpiSwiGLU && LR == 0) {
         // the last, partial round of units as half units on twice the
         // blocks (gate/up 7B: 896 units on 256 blocks, 3.5 each)
         const int R = nunits % grid;

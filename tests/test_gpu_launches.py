@@ -137,10 +137,11 @@ def test_gate_up_launch_full_shape(layer7b):
 @pytest.mark.parametrize("mode", ["turbo", "precision"])
 @pytest.mark.parametrize("halves", ["1", "0"])
 def test_gate_up_half_units_ragged(mode, halves, monkeypatch):
-    """gate/up 2 x 5056 x 2048: 316 units on a 256-CU device's 256 blocks,
-    the last 60 as half units on 120 blocks (rows 8h .. 8h + 7 of gate and
-    up per block, each wave one of its two chunks); and the same launch with
-    the half units off (GSD_GATEUP_HALVES=0)."""
+    """gate/up 2 x 5056 x 2048: 316 units on a 256-CU device's 256 blocks;
+    in Turbo mode the last 60 as half units on 120 blocks (rows 8h .. 8h + 7
+    of gate and up per block, each wave one of its two chunks), in Precision
+    mode (rank-2 term: no half units) 3 or 4 units per block; and the same
+    launch with the half units off (GSD_GATEUP_HALVES=0)."""
     from gsdlq import synth
     import run_gpu_native_chat as chat
     monkeypatch.setenv("GSD_GATEUP_HALVES", halves)
