@@ -703,8 +703,8 @@ size_t matmul_ws_need(int M, int rows, int cols) {
     return xa + xs + kMaxSeg * tk + pt;
 }
 
-size_t split_part_bytes(int M, int rows, int cols) {
-    const MatmulPlan plan = hexmm_plan(M, rows, cols);
+size_t split_part_bytes(int M, int rows, int cols) {   // the prefill's (high + low operands)
+    const MatmulPlan plan = hexmm_plan(M, rows, cols, true);
     return plan.nsplit > 1 ? (size_t)plan.nsplit * ((M + 15) / 16 * 16) * rows * 4 : 0;
 }
 
@@ -753,7 +753,7 @@ int issue_mm(gsdh_model* m, const HexDev& t, int M, int cols, const float* tmp, 
     auto& P = m->pf;
     MatmulArgs a{};
     fill_seg(a.w, t, m, nullptr);
-    const MatmulPlan plan = hexmm_plan(M, t.rows, cols);
+    const MatmulPlan plan = hexmm_plan(M, t.rows, cols, true);
     if (plan.nsplit > 1 && split_part_bytes(M, t.rows, cols) > P.part_bytes)
         return fail(-1, "prefill: split partials of %d tokens exceed the workspace", M);
     a.xa = P.xa; a.xs = P.xs; a.Xf = P.xn; a.hl = 1; a.accumulate = accumulate ? 1 : 0;

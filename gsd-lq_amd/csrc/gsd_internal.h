@@ -184,7 +184,8 @@ hipError_t launch_embed_rows(const uint16_t* embed, const int* tokens, int M, fl
 struct MatmulPlan {
     int tg, rbw, nsplit;
 };
-MatmulPlan hexmm_plan(int M, int rows, int cols);
+// hl: operands as high + low fp16 parts (the model's prefill).
+MatmulPlan hexmm_plan(int M, int rows, int cols, bool hl = false);
 hipError_t launch_hexmm(const MatmulArgs& a, hipStream_t stream);
 // tmp[m][j] = S[j] * sum_c bf16(X[m][c]) * Vt[j][c]
 hipError_t launch_lowrank_batched(const uint16_t* X, const uint16_t* Vt, const float* S, float* tmp,

@@ -3680,7 +3680,7 @@ hipError_t launch_hexmm_t(const MatmulArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
-MatmulPlan hexmm_plan(int M, int rows, int cols) {
+MatmulPlan hexmm_plan(int M, int rows, int cols, bool hl) {
     // fewest token tiles (largest tg: the weights are decoded once per token
     // tile) that still give about 3/4 of a block per CU; when no tiling does,
     // split the columns (at least 4 chunks per split, partials within twice
@@ -3689,6 +3689,18 @@ MatmulPlan hexmm_plan(int M, int rows, int cols) {
     const int ncu = device_cu_count() > 0 ? device_cu_count() : 256;
     MatmulPlan p{1, 1, 1};
     int tiles = 0;
+    // high + low operands (two matrix-core products per step) from 256
+    // tokens on: the eight-group tile, its columns split until the grid
+    // fills the chip, where the rule below would take fewer token groups
+    // per tile (7B prompt of 1024 tokens: 54.4 -> 51.1 ms; the single-
+    // operand projection measured 3 % slower this way)
+    if (hl && ng >= 16) {
+        const int t8 = ((nrb + 15) / 16) * ((ng + 7) / 8);
+        if (4 * t8 < 3 * ncu) {
+            const int s = std::min((ncu + t8 - 1) / t8, std::max(1, nc / 4));
+            return MatmulPlan{8, 2, s};
+        }
+    }
     for (int tg = 8; tg >= 1; tg >>= 1) {
         if (tg > 1 && tg > ng) continue;
         const int rbw = tg == 8 ? 2 : 1;
