@@ -2299,20 +2299,41 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     // (the field tables are padded to 256 entries), issued after the code
     // loads: a scalar wait is for every scalar read in flight, so issued
     // earlier it would hold up the reads of the code pointers
-    uint32_t fv[16];
+    // The residual launches run 8 waves for a single unit per block (o:
+    // 4096 x 4096), fewer than the 14 slices of the radius-8 table: there
+    // a wave also reads slice wid + 8 in the same round trip (one entry at a
+    // time, the remainder took ~11 dependent reads: o 5.66 -> 5.28 us).  Not
+    // compiled into the other launches (16 more scalar registers: the head
+    // launch ran 4 us slower with them).
+    constexpr bool k2S = TB > 128 && EPI == kEpiResidual;
+    uint32_t fv[16], fv2[k2S ? 16 : 1];
+    const bool two = k2S && NW * 16 < TB && (wid + NW) * 16 < TB;
     if (TB > 0 && wid * 16 < TB) {
         KU32* fp = (KU32*)a.seg[0].fields + wid * 16;
 #pragma unroll
         for (int j = 0; j < 16; j++) fv[j] = fp[j];
+        if constexpr (k2S) {
+            if (two) {
+#pragma unroll
+                for (int j = 0; j < 16; j++) fv2[j] = fp[NW * 16 + j];
+            }
+        }
     }
     if (TB > 0) {
         if (wid * 16 < TB) {
 #pragma unroll
             for (int j = 0; j < 16; j++) stab[(wid * 16 + j) * 64 + lane] = fv[j];
+            if constexpr (k2S) {
+                if (two) {
+#pragma unroll
+                    for (int j = 0; j < 16; j++) stab[((wid + NW) * 16 + j) * 64 + lane] = fv2[j];
+                }
+            }
         }
-        // fewer than TB / 16 waves: the remaining slices, one entry at a time
+        // fewer than TB / 16 waves (TB / 32 with the second slice): the
+        // remaining slices, one entry at a time
         KU32* f = (KU32*)a.seg[0].fields;
-        for (int e = NW * 16 + wid; e < TB; e += NW) stab[e * 64 + lane] = f[e];
+        for (int e = (k2S ? 2 : 1) * NW * 16 + wid; e < TB; e += NW) stab[e * 64 + lane] = f[e];
     } else {
         for (int g = 0; g < a.nseg; g++) {
             uint32_t* t = reinterpret_cast<uint32_t*>(dyn + toff(g));
