@@ -294,6 +294,34 @@ def test_greedy_7b_precision_128_steps():
     gpu.close()
 
 
+def test_7b_shape_decode_past_256():
+    """The split decode attention inside the model's token graph at the 7B
+    head shape (32 / 8 heads of 128; positions from 256 on leave the fused
+    short-context launch): a 2-layer Mistral-7B-shaped Precision model takes
+    a 270-token prompt through the batched prefill, then decodes positions
+    270-273, each against the oracle's forward (logits within 1e-3)."""
+    from gsdlq import synth
+    import run_gpu_native_chat as chat
+    banner("7B-shaped 2-layer model: prefill 270, decode 270-273 (split attention)")
+    src = synth.SynthSource(synth.SynthSpec(n_layers=2, mode="precision"))
+    gpu = chat.GPUMistralV2Model(src, max_seq_len=512, verbose=False)
+    ref = O.OracleModel(src, kind="port", max_seq_len=512)
+    toks = np.random.default_rng(270).integers(0, gpu.vocab_size, 274).tolist()
+    got = gpu.prefill(toks[:270], 0)
+    want = None
+    for pos in range(270):
+        want = ref.forward_token(toks[pos], pos, return_logits=pos == 269)
+    e = rel_l2(got, want)
+    print(f"[model-parity] 7B-shaped prefill 270: rel L2 {e:.2e}", flush=True)
+    assert e < 1e-3
+    for pos in range(270, 274):
+        a, b = gpu.forward_token(toks[pos], pos), ref.forward_token(toks[pos], pos)
+        e = rel_l2(a, b)
+        print(f"[model-parity] 7B-shaped decode position {pos}: rel L2 {e:.2e}", flush=True)
+        assert e < 1e-3, pos
+    gpu.close()
+
+
 _LONG = {}
 
 
