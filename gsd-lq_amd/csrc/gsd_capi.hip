@@ -445,6 +445,9 @@ struct HexDev {
     uint16_t* U = nullptr;
     float* Sv = nullptr;
     uint16_t* Vt = nullptr;
+    // down only: the column slabs of the fused FFN launch (FfnArgs::dcodes)
+    unsigned char* dslab = nullptr;
+    uint32_t* dslab_sc = nullptr;
     void* block = nullptr;
     size_t bytes = 0;
 };
@@ -487,6 +490,11 @@ struct gsdh_model {
     unsigned long long* fa_words = nullptr;
     unsigned* fa_epoch = nullptr;
     bool fa_on = true;                   // GSD_FUSED_ATTN=0 turns it off (A/B)
+    // the fused FFN launch (gate/up + SwiGLU + down + residual): its partial
+    // words and the epoch the o launch advances before it
+    unsigned long long* ffn_words = nullptr;
+    unsigned* ffn_epoch = nullptr;
+    bool ffn_on = true;                  // GSD_FUSED_FFN=0 turns it off (A/B)
     int chunk = 64, max_splits = 1;
     StepState* st = nullptr;        // device
     StepState* st_host = nullptr;   // pinned
@@ -586,8 +594,48 @@ int issue_qkv_attention(gsdh_model* m, int l, bool* fused) {
     return 0;
 }
 
+// Whether layer l's gate/up + down run as one fused FFN launch: the model
+// shape within launch_ffn's grid, one codebook for the three tensors, and
+// rank 2 in each (Precision) or in none (Turbo).
+bool ffn_fused(gsdh_model* m, int l) {
+    if (!m->ffn_on) return false;
+    const HexDev& g = m->slot(l, GSDH_GATE);
+    const HexDev& u = m->slot(l, GSDH_UP);
+    const HexDev& d = m->slot(l, GSDH_DOWN);
+    if (!d.dslab || g.radius != u.radius || g.radius != d.radius) return false;
+    return (g.k == 0 && u.k == 0 && d.k == 0) || (g.k == 2 && u.k == 2 && d.k == 2);
+}
+
+int issue_ffn(gsdh_model* m, int l) {
+    const auto& c = m->c;
+    const HexDev& g = m->slot(l, GSDH_GATE);
+    const HexDev& u = m->slot(l, GSDH_UP);
+    const HexDev& d = m->slot(l, GSDH_DOWN);
+    FfnArgs a{};
+    a.gcodes = reinterpret_cast<const unsigned char*>(g.codes_t); a.gscales = g.scales_t;
+    a.ucodes = reinterpret_cast<const unsigned char*>(u.codes_t); a.uscales = u.scales_t;
+    a.dcodes = d.dslab; a.dscales = d.dslab_sc;
+    a.fields = m->fields[g.radius];
+    a.n_pts = 3 * g.radius * g.radius + 3 * g.radius + 1;
+    if (g.nk) { a.g_rp = g.row_ptr; a.g_kc = g.kcols; a.g_kd = g.kdel; }
+    if (u.nk) { a.u_rp = u.row_ptr; a.u_kc = u.kcols; a.u_kd = u.kdel; }
+    if (d.nk) { a.d_rp = d.row_ptr; a.d_kc = d.kcols; a.d_kd = d.kdel; }
+    if (g.k == 2) {
+        a.gU = g.U; a.uU = u.U; a.dU = d.U;
+        a.gS = g.Sv; a.uS = u.Sv; a.dS = d.Sv;
+        a.gVt = g.Vt; a.uVt = u.Vt; a.dVt = d.Vt;
+    }
+    a.x = m->x; a.norm_w = m->norm(l, 1); a.eps = c.rms_eps; a.h = m->h;
+    a.words = m->ffn_words; a.epoch = m->ffn_epoch; a.err = &m->st->err;
+    a.hidden = c.hidden; a.ffn = c.ffn;
+    HIPCHK(launch_ffn(a, m->stream));
+    return 0;
+}
+
 int issue_linear(gsdh_model* m, int l, int mask) {
     int rc = 0;
+    // gate/up and down together: one fused FFN launch where it covers the layer
+    const bool fffn = (mask & 12) == 12 && ffn_fused(m, l);
     if (mask & 1) {
         HexArgs a = qkv_args(m, l);
         if ((rc = prep_lowrank(m, a))) return rc;
@@ -600,8 +648,13 @@ int issue_linear(gsdh_model* m, int l, int mask) {
         fill_seg(a.seg[0], m->slot(l, GSDH_O), m, m->x);
         a.x = m->attn; a.cols = c.n_heads * c.head_dim; a.epilogue = kEpiResidual; a.resid = m->x;
         a.scale_t = 1;
+        a.bump = fffn ? m->ffn_epoch : nullptr;   // the epoch of the FFN launch below
         if ((rc = prep_lowrank(m, a))) return rc;
         HIPCHK(launch_hexmv4(a, m->stream));
+    }
+    if (fffn) {
+        if (!(mask & 2)) HIPCHK(launch_bump(m->ffn_epoch, m->stream));
+        return issue_ffn(m, l);
     }
     if (mask & 4) {   // gate + up with fused FFN RMSNorm and SwiGLU
         HexArgs a{};
@@ -929,6 +982,12 @@ int gsdh_model_create(const gsdh_model_config* cfg, gsdh_model** out) {
     {
         const char* fe = std::getenv("GSD_FUSED_ATTN");
         m->fa_on = !(fe && fe[0] == '0');
+        fe = std::getenv("GSD_FUSED_FFN");
+        m->ffn_on = !(fe && fe[0] == '0') && ffn_supported(c.hidden, c.ffn);
+    }
+    if (m->ffn_on) {
+        A((void**)&m->ffn_words, ffn_words(c.hidden, c.ffn) * 8);
+        A((void**)&m->ffn_epoch, 4);
     }
     A((void**)&m->st, sizeof(StepState));
     A((void**)&m->gen_tok, (size_t)c.max_seq_len * 4);
@@ -962,6 +1021,9 @@ int gsdh_model_create(const gsdh_model_config* cfg, gsdh_model** out) {
         if (e == hipSuccess) e = launch_fill_u32((unsigned*)m->pub, 0u, 2 * (size_t)m->pub_words, m->stream);
         if (e == hipSuccess) e = launch_fill_u32((unsigned*)m->fa_words, 0u, 2 * (qd + kvd), m->stream);
         if (e == hipSuccess) e = launch_fill_u32(m->fa_epoch, 0u, 1, m->stream);
+        if (e == hipSuccess && m->ffn_on)
+            e = launch_fill_u32((unsigned*)m->ffn_words, 0u, 2 * ffn_words(c.hidden, c.ffn), m->stream);
+        if (e == hipSuccess && m->ffn_on) e = launch_fill_u32(m->ffn_epoch, 0u, 1, m->stream);
         if (e == hipSuccess) e = launch_fill_u32((unsigned*)m->kc, 0u, kvn / 2, m->stream);
         if (e == hipSuccess) e = launch_fill_u32((unsigned*)m->vc, 0u, kvn / 2, m->stream);
         if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
@@ -1066,7 +1128,16 @@ int gsdh_model_set_hex(gsdh_model* m, int layer, int slot, int radius, int rows,
     const size_t o_codes = 0, o_sc = o_codes + al(nrb * nc * tbytes), o_rp = o_sc + al(nrb * nc * 64);
     const size_t o_kc = o_rp + al((size_t)(rows + 1) * 4), o_kd = o_kc + al((size_t)nk * 2);
     const size_t o_u = o_kd + al((size_t)nk * 4), o_s = o_u + al((size_t)rows * k_dim * 2);
-    const size_t o_vt = o_s + al((size_t)k_dim * 4), total = o_vt + al((size_t)k_dim * cols * 2);
+    const size_t o_vt = o_s + al((size_t)k_dim * 4), o_end = o_vt + al((size_t)k_dim * cols * 2);
+    // down of a model the fused FFN launch covers: also its column slabs
+    // (FfnArgs::dcodes): slab b = columns 64 b .. 64 b + 63, step sd = rows
+    // 32 sd .. 32 sd + 31, lane l: row 32 sd + (l & 15) in codes 0-7 and row
+    // 32 sd + 16 + (l & 15) in codes 8-15, pair 8 (l >> 4) + (j & 7) of the
+    // slab; the scale word: those two rows' scales of block b
+    const bool slabs = slot == GSDH_DOWN && m->ffn_on;
+    const size_t nslab = (size_t)cols / 64, nsd = ((size_t)rows + 31) / 32;
+    const size_t o_ds = o_end, o_dss = o_ds + (slabs ? al(nslab * nsd * tbytes) : 0);
+    const size_t total = o_dss + (slabs ? al(nslab * nsd * 64) : 0);
     void* blk = nullptr;
     HIPCHK(hipMalloc(&blk, total));
     char* b = static_cast<char*>(blk);
@@ -1074,6 +1145,17 @@ int gsdh_model_set_hex(gsdh_model* m, int layer, int slot, int radius, int rows,
     t.codes_t = (uint4*)(b + o_codes); t.scales_t = (uint32_t*)(b + o_sc); t.row_ptr = (uint32_t*)(b + o_rp);
     t.kcols = (uint16_t*)(b + o_kc); t.kdel = (float*)(b + o_kd); t.U = (uint16_t*)(b + o_u);
     t.Sv = (float*)(b + o_s); t.Vt = (uint16_t*)(b + o_vt);
+    // lane l's code j (value v) into a tile at dst
+    auto put_code = [b7](uint8_t* dst, int l, int j, unsigned v) {
+        uint8_t* ld = b7 ? dst + 28 * (l >> 1) + 14 * (l & 1) : dst + 16 * l;
+        if (!b7) {
+            ld[j] = (uint8_t)v;
+        } else {   // bits 7j .. 7j + 6 of the lane's field
+            const unsigned bit = 7u * (unsigned)j;
+            ld[bit >> 3] |= (uint8_t)(v << (bit & 7));
+            if ((bit & 7) > 1) ld[(bit >> 3) + 1] |= (uint8_t)(v >> (8 - (bit & 7)));
+        }
+    };
     {
         std::vector<uint8_t> ct(nrb * nc * tbytes, 0);
         std::vector<uint32_t> stl(nrb * nc * 16, 0);
@@ -1084,17 +1166,9 @@ int gsdh_model_set_hex(gsdh_model* m, int layer, int slot, int radius, int rows,
                     const size_t row = rb * 16 + (size_t)(l & 15);
                     if (row >= (size_t)rows) continue;
                     const uint8_t* src = codes + row * half;
-                    uint8_t* ld = b7 ? dst + 28 * (l >> 1) + 14 * (l & 1) : dst + 16 * l;
                     for (int j = 0; j < 16; j++) {
                         const size_t p = 64 * c + (j < 8 ? 8 * (size_t)(l >> 4) + j : 32 + 8 * (size_t)(l >> 4) + (j - 8));
-                        const unsigned v = p < half ? src[p] : 0u;
-                        if (!b7) {
-                            ld[j] = (uint8_t)v;
-                        } else {   // bits 7j .. 7j + 6 of the lane's field
-                            const unsigned bit = 7u * (unsigned)j;
-                            ld[bit >> 3] |= (uint8_t)(v << (bit & 7));
-                            if ((bit & 7) > 1) ld[(bit >> 3) + 1] |= (uint8_t)(v >> (8 - (bit & 7)));
-                        }
+                        put_code(dst, l, j, p < half ? src[p] : 0u);
                     }
                 }
                 for (int n = 0; n < 16; n++) {
@@ -1107,6 +1181,31 @@ int gsdh_model_set_hex(gsdh_model* m, int layer, int slot, int radius, int rows,
             }
         HIPCHK(hipMemcpy(t.codes_t, ct.data(), ct.size(), hipMemcpyHostToDevice));
         HIPCHK(hipMemcpy(t.scales_t, stl.data(), stl.size() * 4, hipMemcpyHostToDevice));
+    }
+    if (slabs) {
+        t.dslab = (unsigned char*)(b + o_ds);
+        t.dslab_sc = (uint32_t*)(b + o_dss);
+        std::vector<uint8_t> ct(nslab * nsd * tbytes, 0);
+        std::vector<uint32_t> stl(nslab * nsd * 16, 0);
+        for (size_t sb = 0; sb < nslab; sb++)
+            for (size_t sd = 0; sd < nsd; sd++) {
+                const size_t ti = sb * nsd + sd;
+                uint8_t* dst = ct.data() + ti * tbytes;
+                for (int l = 0; l < 64; l++)
+                    for (int j = 0; j < 16; j++) {
+                        const size_t row = 32 * sd + 16 * (size_t)(j >> 3) + (size_t)(l & 15);
+                        if (row >= (size_t)rows) continue;
+                        put_code(dst, l, j, codes[row * half + 32 * sb + 8 * (size_t)(l >> 4) + (size_t)(j & 7)]);
+                    }
+                for (int n = 0; n < 16; n++) {
+                    const size_t r0 = 32 * sd + (size_t)n, r1 = r0 + 16;
+                    const uint32_t s0 = r0 < (size_t)rows ? scales[r0 * nsb + sb] : 0u;
+                    const uint32_t s1 = r1 < (size_t)rows ? scales[r1 * nsb + sb] : 0u;
+                    stl[ti * 16 + n] = s0 | (s1 << 16);
+                }
+            }
+        HIPCHK(hipMemcpy(t.dslab, ct.data(), ct.size(), hipMemcpyHostToDevice));
+        HIPCHK(hipMemcpy(t.dslab_sc, stl.data(), stl.size() * 4, hipMemcpyHostToDevice));
     }
     HIPCHK(hipMemcpy(t.row_ptr, row_ptr, (size_t)(rows + 1) * 4, hipMemcpyHostToDevice));
     if (nk > 0) {
@@ -1227,6 +1326,12 @@ int gsdh_model_prefill(gsdh_model* m, const int* tokens, int n, int start_pos, i
     (void)hipStreamSynchronize(m->stream);
     (void)hipHostFree(ring);
     return rc;
+}
+
+int gsdh_model_fused_ffn(gsdh_model* m, int layer) {
+    if (!m) return fail(-1, "fused_ffn: null model");
+    if (layer < 0 || layer >= m->c.n_layers) return fail(-1, "fused_ffn: layer %d", layer);
+    return ffn_fused(m, layer) ? 1 : 0;
 }
 
 int gsdh_model_set_prefill(gsdh_model* m, int batched) {

@@ -79,6 +79,9 @@ struct HexArgs {
     // be zero when the launch starts (each launch of a sequence has its own).
     unsigned long long* pub;
     unsigned* err;             // set to 1 when the wait exceeds its bound
+    // non-null: one thread of block 0 adds one to *bump (the epoch of the
+    // fused FFN launch that follows on the stream)
+    unsigned* bump;
     // Decode attention in the q/k/v launch (kEpiRopeKV, positions < 256):
     // the last nkv blocks of the grid are attention blocks, one per KV head.
     // The q/k/v epilogue publishes its outputs as 64-bit words, tag << 32 |
@@ -113,6 +116,79 @@ struct HexArgs {
 };
 
 constexpr int kLeadMax = kMaxSeg * kMaxRank;   // publishing blocks per launch
+
+// The feed-forward block of one decode token in one launch
+// (gsd_lq_cpu_runtime.py:380-404: x += W_down (silu(W_gate x') * (W_up x')),
+// x' = rmsnorm(x) * ffn_norm).  Block b < nb owns FFN rows 64 b .. 64 b + 63:
+// it forms those rows of gate and up (four 16-row units of each), their
+// SwiGLU values h, then the down product of its own h over every output row,
+// W_down[:, 64 b .. 64 b + 63] h[64 b ..], as partial sums (split-K): no
+// block waits for another's h.  The partials go out as 64-bit words tag << 32
+// | float bits (relaxed device-scope stores); block s < nslices then sums
+// rows 16 s .. 16 s + 15 over every block's words in block order
+// (deterministic), adds the rank-k and kink terms and the residual, and
+// writes x.  Every block of the grid is resident at once (grid <= CU count,
+// one block per CU), so the wait for the words ends (bounded: a timeout sets
+// *err).  tag = *epoch, which an earlier launch on the stream advances once
+// per FFN launch (the o launch: HexArgs::bump), so words of other launches
+// never match and nothing is cleared.
+struct FfnArgs {
+    // gate / up in the tiled matvec layout (HexSeg::codes_t / scales_t)
+    const unsigned char* gcodes;
+    const uint32_t* gscales;
+    const unsigned char* ucodes;
+    const uint32_t* uscales;
+    // down as column slabs: slab b = columns 64 b .. 64 b + 63, its step sd =
+    // rows 32 sd .. 32 sd + 31 as one tile of 64 lanes x 16 codes; lane l
+    // holds row 32 sd + (l & 15) (codes j < 8) and row 32 sd + 16 + (l & 15)
+    // (j >= 8), pair 8 (l >> 4) + (j & 7) of the slab; the scale word holds
+    // the fp16 scales of those two rows' 64-weight block
+    const unsigned char* dcodes;
+    const uint32_t* dscales;
+    const uint32_t* fields;   // (r0, r1) fp16 pairs, padded to 256 entries
+    int n_pts;
+    // CSR kinks (row_ptr null: none) and rank-2 factors (R2 kernels)
+    const uint32_t* g_rp;
+    const uint16_t* g_kc;
+    const float* g_kd;
+    const uint32_t* u_rp;
+    const uint16_t* u_kc;
+    const float* u_kd;
+    const uint32_t* d_rp;
+    const uint16_t* d_kc;
+    const float* d_kd;
+    const uint16_t* gU;
+    const uint16_t* uU;
+    const uint16_t* dU;
+    const float* gS;
+    const float* uS;
+    const float* dS;
+    const uint16_t* gVt;
+    const uint16_t* uVt;
+    const uint16_t* dVt;
+    float* x;                    // residual stream: read, then x += W_down h
+    const float* norm_w;         // ffn_norm
+    float eps;
+    float* h;                    // the SwiGLU values (written for inspection)
+    unsigned long long* words;   // [nb][hpad] partials, [nb][2] rank words, [ffn] h words
+    const unsigned* epoch;
+    unsigned* err;
+    int hidden, ffn;
+    int nb;          // working blocks: ffn / 64
+    int nslices;     // reducing blocks: hidden / 16
+    int hpad;        // row stride of the partial words (nslices * 16)
+    int nc;          // 128-column chunks of x (hidden / 128)
+    int nrb;         // 16-row blocks of gate / up
+    int ns2;         // 32-row steps of a down slab
+    int spin_limit;  // polling rounds before a wait counts as timed out
+};
+hipError_t launch_ffn(const FfnArgs& a, hipStream_t stream);
+// *p += 1 on the device (the FFN epoch where no o launch advances it)
+hipError_t launch_bump(unsigned* p, hipStream_t stream);
+// words an FfnArgs::words buffer needs for a model shape
+size_t ffn_words(int hidden, int ffn);
+// whether launch_ffn covers the shape (grid within the CU count, chunking)
+bool ffn_supported(int hidden, int ffn);
 
 // Launches (all asynchronous on `stream`).
 hipError_t launch_hexmv(const HexArgs& a, hipStream_t stream);

@@ -71,6 +71,7 @@ SIGNATURES = {
 }
 RESTYPES = {"gsdh_model_device_bytes": (u64, [vp]), "gsdh_model_stream": (vp, [vp]),
             "gsdh_attention_workspace_bytes": (u64, [i32, i32, i32, i32]),
+            "gsdh_model_fused_ffn": (i32, [vp, i32]),
             "gsdh_last_error": (ctypes.c_char_p, [])}
 
 

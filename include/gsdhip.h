@@ -313,6 +313,15 @@ int gsdh_model_read_codes(gsdh_model* m, int layer, int slot, uint8_t* codes_out
  * full-shape parity tests of each launch. */
 int gsdh_model_run_linear(gsdh_model* m, int layer, int mask);
 
+/* 1 when gate/up + down of `layer` run as one fused FFN launch (mask 4 | 8 of
+ * gsdh_model_run_linear and every decode token): h of each block's 64 FFN
+ * rows, then that block's 64 columns of W_down as partial sums that the
+ * launch reduces in block order (gsd_lq_cpu_runtime.py:384-404; no
+ * counterpart entry point).  0 where the two launches run (GSD_FUSED_FFN=0,
+ * shapes beyond the launch's grid, tensors of different radii or of ranks
+ * other than all 0 / all 2), negative on a bad argument. */
+int gsdh_model_fused_ffn(gsdh_model* m, int layer);
+
 /* Activation vectors of the model context (f32): x [hidden], q [n_heads*hd],
  * k / v [n_kv*hd], attn [n_heads*hd], h [ffn], logits [vocab].  write = 1
  * copies host -> device, 0 device -> host; nbytes must be the vector's size.

@@ -184,6 +184,89 @@ def test_down_launch_full_shape(layer7b):
     _check(f"{mode} down + residual", got, x + y)
 
 
+def _ffn_ref(ref, x, layer=0):
+    """x + W_down (silu(W_gate x') * (W_up x')), x' = rmsnorm(x) * ffn_norm,
+    through the oracle's engine functions (gsd_lq_cpu_runtime.py:380-404);
+    returns (h, y, x + y)."""
+    ly = ref.layers[layer]
+    xb = _rmsnorm(ref, x, ly["ffn_norm"])
+    n = ref.ffn_size
+    g = np.empty(n, np.float32)
+    u = np.empty(n, np.float32)
+    ref.matvec(xb, ly["gate"], g)
+    ref.matvec(xb, ly["up"], u)
+    ref.lib.gsd_cpu_swiglu(O.P(g), O.P(u), O.P(g), n)
+    y = np.empty(x.size, np.float32)
+    ref.matvec(g, ly["down"], y)
+    return g, y, x + y
+
+
+def test_ffn_launch_full_shape(layer7b):
+    """The fused FFN launch (gate/up + SwiGLU + split down + residual in one
+    launch, the decode's and the benchmark's): h, the down product and the
+    new x against the oracle at the 7B shape."""
+    mode, gpu, ref = layer7b
+    assert gpu.cl.lib.gsdh_model_fused_ffn(gpu._m, 0) == 1
+    rng = np.random.default_rng(108)
+    x = rng.standard_normal(gpu.hidden).astype(np.float32)
+    _put(gpu, "x", x)
+    gpu.cl.lib.gsdh_model_run_linear(gpu._m, 0, 12)
+    got = _get(gpu, "x", gpu.hidden)
+    h = _get(gpu, "h", gpu.ffn_size)
+    hr, y, want = _ffn_ref(ref, x)
+    _check(f"{mode} FFN launch: h (2x14336x4096 + SwiGLU)", h, hr)
+    _check(f"{mode} FFN launch: down (4096x14336) without residual", got - x, y)
+    _check(f"{mode} FFN launch: x + down", got, want)
+
+
+def test_ffn_launch_repeat_bit_identical(layer7b):
+    """The fused FFN's cross-block sums run in a fixed block order: two runs
+    on the same x give the same bits (each with a new epoch)."""
+    mode, gpu, _ = layer7b
+    x = np.random.default_rng(109).standard_normal(gpu.hidden).astype(np.float32)
+    outs = []
+    for _ in range(3):
+        _put(gpu, "x", x)
+        gpu.cl.lib.gsdh_model_run_linear(gpu._m, 0, 12)
+        outs.append(_get(gpu, "x", gpu.hidden))
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+
+
+@pytest.mark.parametrize("mode", ["turbo", "precision"])
+def test_ffn_launch_ragged_kinks(mode):
+    """The fused FFN at hidden 2048 / ffn 5056 (79 row blocks of 64, 128
+    reducing slices, one chunk of x per wave) with kink terms in gate, up and
+    down (down's read h of other blocks through the tagged h words), after an
+    o launch (which advances the FFN epoch) and alone."""
+    from gsdlq import synth
+    import run_gpu_native_chat as chat
+    banner(f"fused FFN 2048 / 5056 {mode}, kinks")
+    spec = synth.SynthSpec(n_layers=1, hidden=2048, ffn=5056, n_heads=16, n_kv_heads=4, head_dim=128, vocab=512,
+                           mode=mode, kinks_per_row=2)
+    src = synth.SynthSource(spec)
+    gpu = chat.GPUMistralV2Model(src, max_seq_len=16, verbose=False)
+    ref = O.OracleModel(src, kind="port", max_seq_len=16)
+    try:
+        assert gpu.cl.lib.gsdh_model_fused_ffn(gpu._m, 0) == 1
+        rng = np.random.default_rng(110)
+        for mask in (12, 14):
+            x = rng.standard_normal(gpu.hidden).astype(np.float32)
+            att = rng.standard_normal(gpu.n_heads * gpu.head_dim).astype(np.float32)
+            _put(gpu, "x", x)
+            _put(gpu, "attn", att)
+            gpu.cl.lib.gsdh_model_run_linear(gpu._m, 0, mask)
+            got = _get(gpu, "x", gpu.hidden)
+            if mask & 2:
+                yo = np.empty(gpu.hidden, np.float32)
+                ref.matvec(att, ref.layers[0]["o"], yo)
+                x = x + yo
+            hr, y, want = _ffn_ref(ref, x)
+            _check(f"{mode} FFN 2048/5056 mask {mask}: h", _get(gpu, "h", gpu.ffn_size), hr)
+            _check(f"{mode} FFN 2048/5056 mask {mask}: x + down", got, want)
+    finally:
+        gpu.close()
+
+
 def test_head_launch_full_shape(layer7b):
     mode, gpu, ref = layer7b
     rng = np.random.default_rng(105)

@@ -234,6 +234,47 @@ def test_fused_attention_matches_two_launches(mode, shape, monkeypatch):
         m.close()
 
 
+@pytest.mark.parametrize("mode,shape", [
+    ("precision", dict(kinks_per_row=2)),                                     # 2 chunks of x, 8 FFN blocks
+    ("turbo", dict(n_layers=3, hidden=512, ffn=1344, n_heads=8, n_kv_heads=2, head_dim=128, vocab=1000,
+                   kinks_per_row=1)),                                         # 21 FFN blocks, 32 slices
+    ("precision", dict(codebook_radius=5, kinks_per_row=1)),                  # 91-point codebook, 7-bit tiles
+])
+def test_fused_ffn_matches_two_launches(mode, shape, monkeypatch):
+    """Every decode token runs gate/up + down as one fused FFN launch where it
+    covers the model; with GSD_FUSED_FFN=0 the model issues the gate/up and
+    the down launches instead.  Both match the oracle at every checked
+    position, and each other closely; greedy tokens are equal."""
+    banner(f"fused FFN vs two launches {mode} {shape}")
+    from gsdlq import synth
+    import run_gpu_native_chat as chat
+    src = synth.SynthSource(_spec(mode=mode, **shape))
+    models = []
+    for ff in ("1", "0"):
+        monkeypatch.setenv("GSD_FUSED_FFN", ff)
+        models.append(chat.GPUMistralV2Model(src, max_seq_len=128, verbose=False))
+    fused, plain = models
+    assert fused.cl.lib.gsdh_model_fused_ffn(fused._m, 0) == 1
+    assert plain.cl.lib.gsdh_model_fused_ffn(plain._m, 0) == 0
+    ref = O.OracleModel(src, kind="port", max_seq_len=128)
+    toks = np.random.default_rng(8).integers(0, fused.vocab_size, 40).tolist()
+    for pos, t in enumerate(toks):
+        want = pos % 5 == 0 or pos == len(toks) - 1
+        a = fused.forward_token(t, pos, return_logits=want)
+        b = plain.forward_token(t, pos, return_logits=want)
+        r = ref.forward_token(t, pos, return_logits=want)
+        if want:
+            assert rel_l2(a, r) < 1e-3, pos
+            assert rel_l2(b, r) < 1e-3, pos
+            assert rel_l2(a, b) < 1e-4, pos
+    ta, _ = fused.generate_greedy(toks[:5], 12)
+    tb, _ = plain.generate_greedy(toks[:5], 12)
+    tr, _ = ref.generate_greedy(toks[:5], 12)
+    assert ta == tr and tb == tr
+    for m in models:
+        m.close()
+
+
 def test_model_rejects_invalid_codes():
     from gsdlq import synth
     import run_gpu_native_chat as chat
