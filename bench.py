@@ -4,8 +4,9 @@ Workload (the metric's configuration): the full Mistral-7B linear set of one
 layer -- q 4096x4096, k/v 1024x4096, o 4096x4096, gate/up 14336x4096,
 down 4096x14336 -- packed in Turbo mode (radius 8, ~4.26 bpw), batch 1, fp32
 activations.  A step is one pass of the layer's fused unpack-matvec launches
-(qkv with fused RMSNorm, o + residual, gate/up with fused RMSNorm + SwiGLU,
-down + residual).  Steps rotate over `--layers` distinct packed layers
+(qkv with fused RMSNorm, o + residual, and one FFN launch: RMSNorm, gate/up,
+SwiGLU, down split over the FFN rows, residual).  Steps rotate over
+`--layers` distinct packed layers
 (> 256 MB) so the Infinity Cache cannot serve the weights, and are timed with
 HIP events around a captured HIP graph on the engine's stream.
 
@@ -15,8 +16,8 @@ byte each for radius 8, seven bits for radius <= 6) + fp16 scales + row_ptr +
 6 B per kink + low-rank factors + x (4 B/col) + y (4 B/row).
 
 Also reported: the same for Precision mode (radius 6: 7-bit codes, rank 2),
-the dominant kernel's roofline (the fused gate/up launch, 2 x
-14336x4096), decode attention with RoPE + K/V append at contexts 512 / 2048 /
+the dominant kernel's roofline (the fused FFN launch: 2 x 14336x4096 +
+4096x14336 of weights, x in and out), decode attention with RoPE + K/V append at contexts 512 / 2048 /
 8192 (GB/s of K/V cache read), end-to-end greedy decode tok/s of a 32-layer
 7B-shaped model, and the reference CPU engine timed on this host's cores on a
 bounded sample.
@@ -55,13 +56,26 @@ def code_bytes(f):
     return (7 * n + 7) // 8 if f["radius"] <= 6 else n
 
 
-def alg_bytes(f):
-    """Algorithmic bytes of one fused matvec over packed tensor f."""
+def weight_bytes(f):
+    """Bytes of packed tensor f a matvec streams: codes in the device format,
+    scales, row_ptr, kinks, low-rank factors."""
     rows, cols, k = f["rows"], f["cols"], f["k_dim"]
     b = code_bytes(f) + f["scales"].nbytes + f["row_ptr"].nbytes + 6 * f["nk"]
     if k:
         b += 2 * rows * k + 2 * k * cols + 4 * k
-    return b + 4 * cols + 4 * rows
+    return b
+
+
+def alg_bytes(f):
+    """Algorithmic bytes of one fused matvec over packed tensor f (weights +
+    x read + y written)."""
+    return weight_bytes(f) + 4 * f["cols"] + 4 * f["rows"]
+
+
+def ffn_bytes(bank, l):
+    """Algorithmic bytes of the fused FFN launch of layer l: the gate, up and
+    down weights, x read once and x written (h stays inside the launch)."""
+    return sum(weight_bytes(bank.packed[(l, t)]) for t in ("ffn_gate", "ffn_up", "ffn_down")) + 8 * H
 
 
 class LayerBank:
@@ -145,20 +159,22 @@ def bench_linear(bank, steps, warmup):
     ms = time_graph(model, ge, 1)
     ms_step = ms / steps
     gbs = sum(bank.layer_bytes[i % L] for i in range(steps)) / (ms * 1e-3) / 1e9
-    # dominant kernel: fused gate+up (2 x 14336 x 4096), timed alone over
-    # 128 launches rotating the distinct layers
+    # dominant kernel: the fused FFN launch (RMSNorm, gate/up 2 x 14336 x
+    # 4096, SwiGLU, down 4096 x 14336, residual), timed alone over 128
+    # launches rotating the distinct layers
     ng = 128
-    gu = capture(model, lambda: [lib.gsdh_model_run_linear(model._m, i % L, 4) for i in range(ng)])
+    assert lib.gsdh_model_fused_ffn(model._m, 0) == 1, "the fused FFN launch does not cover this model"
+    gu = capture(model, lambda: [lib.gsdh_model_run_linear(model._m, i % L, 12) for i in range(ng)])
     time_graph(model, gu, 1)
     gms = time_graph(model, gu, 1)
     per_launch_ms = gms / ng
-    gu_bytes = sum(alg_bytes(bank.packed[(l, t)]) for l in range(L) for t in ("ffn_gate", "ffn_up")) / L
-    gu_bytes -= 4 * H   # gate and up read the same x once
-    ach = gu_bytes / (per_launch_ms * 1e-3) / 1e9
-    roof = {"kernel": "hexmv4_kernel (MFMA fused RMSNorm + gate/up matvec + SwiGLU, 2x14336x4096)",
+    fb = sum(ffn_bytes(bank, i % L) for i in range(ng)) / ng
+    ach = fb / (per_launch_ms * 1e-3) / 1e9
+    roof = {"kernel": "ffn_kernel (MFMA fused RMSNorm + gate/up + SwiGLU + split-K down + residual, "
+                      "2x14336x4096 + 4096x14336)",
             "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(),
-            "launch_us": round(per_launch_ms * 1e3, 2), "alg_bytes_per_launch": int(gu_bytes),
+            "launch_us": round(per_launch_ms * 1e3, 2), "alg_bytes_per_launch": int(fb),
             "launches_timed": ng}
     for g in (ge, gu):
         lib.gsdh_graph_destroy(g)
@@ -413,6 +429,8 @@ def cpu_decode(bank, n_prompt=2, n_new=6):
 def probe(kind: str, n: int, ctx: int = 8192, m: int = 128):
     """Launch one kernel repeatedly for counter collection under rocprofv3:
     'gateup' = the fused gate/up matvec over 8 rotated Turbo layers,
+    'ffn' = the fused FFN launch (gate/up + SwiGLU + down + residual) over 8
+    rotated Turbo layers,
     'copy' = a 256 MiB device copy (the calibration of FETCH/WRITE_SIZE),
     'attn' = RoPE + K/V append and decode attention at context `ctx`,
     'prefill' = the batched projection of 8 Turbo layer sets for `m` tokens,
@@ -466,11 +484,15 @@ def probe(kind: str, n: int, ctx: int = 8192, m: int = 128):
     bank = LayerBank("turbo", 8)
     model = build_model(bank, bank.n)
     model.forward_token(1, 0)
+    mask = 12 if kind == "ffn" else 4
     for i in range(n):
-        lib.gsdh_model_run_linear(model._m, i % bank.n, 4)
+        lib.gsdh_model_run_linear(model._m, i % bank.n, mask)
     lib.gsdh_stream_sync(lib.gsdh_model_stream(model._m))
-    gu = sum(alg_bytes(bank.packed[(0, t)]) for t in ("ffn_gate", "ffn_up")) - 4 * H
-    print(f"[probe] gate/up launches {n}, algorithmic bytes per launch {gu}", flush=True)
+    if kind == "ffn":
+        print(f"[probe] FFN launches {n}, algorithmic bytes per launch {ffn_bytes(bank, 0)}", flush=True)
+    else:
+        gu = sum(alg_bytes(bank.packed[(0, t)]) for t in ("ffn_gate", "ffn_up")) - 4 * H
+        print(f"[probe] gate/up launches {n}, algorithmic bytes per launch {gu}", flush=True)
     model.close()
 
 
@@ -551,10 +573,10 @@ def bench_attention(ctxs=(512, 2048, 8192), reps=20):
 
 
 def traffic_from_profile():
-    """HBM bytes per gate/up launch from the committed counter summary
-    (profiles/hexmv_gateup_traffic.txt: FETCH_SIZE and WRITE_SIZE per
-    dispatch of the kernel and of a 256 MiB copy), or None."""
-    path = os.path.join(ROOT, "profiles", "hexmv_gateup_traffic.txt")
+    """HBM bytes per fused FFN launch from the committed counter summary
+    (profiles/ffn_kernel_traffic.txt: FETCH_SIZE and WRITE_SIZE per dispatch
+    of the kernel and of a 256 MiB copy), or None."""
+    path = os.path.join(ROOT, "profiles", "ffn_kernel_traffic.txt")
     if not os.path.exists(path):
         return None
     kv = {}
@@ -566,7 +588,7 @@ def traffic_from_profile():
         copy_bytes = float(kv["copy_bytes"])
         f_scale = copy_bytes / float(kv["copy_fetch_kib"])
         w_scale = copy_bytes / float(kv["copy_write_kib"])
-        return int(float(kv["gateup_fetch_kib"]) * f_scale + float(kv["gateup_write_kib"]) * w_scale)
+        return int(float(kv["ffn_fetch_kib"]) * f_scale + float(kv["ffn_write_kib"]) * w_scale)
     except (KeyError, ValueError, ZeroDivisionError):
         return None
 
@@ -583,7 +605,7 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-attention", action="store_true")
     ap.add_argument("--no-c1", action="store_true")
-    ap.add_argument("--probe", choices=["gateup", "copy", "attn", "prefill", "prompt", "decode"],
+    ap.add_argument("--probe", choices=["gateup", "ffn", "copy", "attn", "prefill", "prompt", "decode"],
                     help="run one kernel for rocprofv3 counters")
     ap.add_argument("--ctx", type=int, default=8192, help="--probe attn: context length")
     ap.add_argument("--m", type=int, default=128, help="--probe prefill / prompt: tokens")
@@ -601,7 +623,7 @@ def main():
 
     turbo = LayerBank("turbo", a.layers)
     gbs, ms_step, roof = bench_linear(turbo, a.steps, a.warmup)
-    log(f"turbo layer set: {gbs:.1f} GB/s, {ms_step * 1e3:.1f} us/step; gate/up {roof['achieved']} GB/s")
+    log(f"turbo layer set: {gbs:.1f} GB/s, {ms_step * 1e3:.1f} us/step; FFN launch {roof['achieved']} GB/s")
     extra = {}
     if not a.no_prefill:
         extra["prefill_turbo"] = dict(bench_prefill(turbo), workload="Turbo 7B layer set (7 tensors), X bf16 "
@@ -617,7 +639,8 @@ def main():
         pg, pms, proof = bench_linear(prec, a.steps, a.warmup)
         extra["precision"] = {"value": round(pg, 1), "unit": "GB/s", "us_per_step": round(pms * 1e3, 2),
                               "frac_hbm": round(pg / HBM_PEAK_GBS, 4), "codes": "7-bit device tiles (radius 6)",
-                              "gate_up_GBs": proof["achieved"], "bytes_per_step": prec.layer_bytes[0]}
+                              "ffn_GBs": proof["achieved"], "ffn_us": proof["launch_us"],
+                              "bytes_per_step": prec.layer_bytes[0]}
         log(f"precision layer set: {pg:.1f} GB/s")
         if not a.no_decode:
             extra["decode_7b_precision"] = bench_decode(prec)

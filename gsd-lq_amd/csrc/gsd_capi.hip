@@ -491,9 +491,9 @@ struct gsdh_model {
     unsigned* fa_epoch = nullptr;
     bool fa_on = true;                   // GSD_FUSED_ATTN=0 turns it off (A/B)
     // the fused FFN launch (gate/up + SwiGLU + down + residual): its partial
-    // words and the epoch the o launch advances before it
+    // words and per-block launch counters
     unsigned long long* ffn_words = nullptr;
-    unsigned* ffn_epoch = nullptr;
+    unsigned* ffn_ctr = nullptr;
     bool ffn_on = true;                  // GSD_FUSED_FFN=0 turns it off (A/B)
     int chunk = 64, max_splits = 1;
     StepState* st = nullptr;        // device
@@ -626,7 +626,7 @@ int issue_ffn(gsdh_model* m, int l) {
         a.gVt = g.Vt; a.uVt = u.Vt; a.dVt = d.Vt;
     }
     a.x = m->x; a.norm_w = m->norm(l, 1); a.eps = c.rms_eps; a.h = m->h;
-    a.words = m->ffn_words; a.epoch = m->ffn_epoch; a.err = &m->st->err;
+    a.words = m->ffn_words; a.ctr = m->ffn_ctr; a.err = &m->st->err;
     a.hidden = c.hidden; a.ffn = c.ffn;
     HIPCHK(launch_ffn(a, m->stream));
     return 0;
@@ -648,14 +648,10 @@ int issue_linear(gsdh_model* m, int l, int mask) {
         fill_seg(a.seg[0], m->slot(l, GSDH_O), m, m->x);
         a.x = m->attn; a.cols = c.n_heads * c.head_dim; a.epilogue = kEpiResidual; a.resid = m->x;
         a.scale_t = 1;
-        a.bump = fffn ? m->ffn_epoch : nullptr;   // the epoch of the FFN launch below
         if ((rc = prep_lowrank(m, a))) return rc;
         HIPCHK(launch_hexmv4(a, m->stream));
     }
-    if (fffn) {
-        if (!(mask & 2)) HIPCHK(launch_bump(m->ffn_epoch, m->stream));
-        return issue_ffn(m, l);
-    }
+    if (fffn) return issue_ffn(m, l);
     if (mask & 4) {   // gate + up with fused FFN RMSNorm and SwiGLU
         HexArgs a{};
         a.nseg = 2;
@@ -987,7 +983,7 @@ int gsdh_model_create(const gsdh_model_config* cfg, gsdh_model** out) {
     }
     if (m->ffn_on) {
         A((void**)&m->ffn_words, ffn_words(c.hidden, c.ffn) * 8);
-        A((void**)&m->ffn_epoch, 4);
+        A((void**)&m->ffn_ctr, kFfnMaxGrid * 4);
     }
     A((void**)&m->st, sizeof(StepState));
     A((void**)&m->gen_tok, (size_t)c.max_seq_len * 4);
@@ -1023,7 +1019,7 @@ int gsdh_model_create(const gsdh_model_config* cfg, gsdh_model** out) {
         if (e == hipSuccess) e = launch_fill_u32(m->fa_epoch, 0u, 1, m->stream);
         if (e == hipSuccess && m->ffn_on)
             e = launch_fill_u32((unsigned*)m->ffn_words, 0u, 2 * ffn_words(c.hidden, c.ffn), m->stream);
-        if (e == hipSuccess && m->ffn_on) e = launch_fill_u32(m->ffn_epoch, 0u, 1, m->stream);
+        if (e == hipSuccess && m->ffn_on) e = launch_fill_u32(m->ffn_ctr, 0u, kFfnMaxGrid, m->stream);
         if (e == hipSuccess) e = launch_fill_u32((unsigned*)m->kc, 0u, kvn / 2, m->stream);
         if (e == hipSuccess) e = launch_fill_u32((unsigned*)m->vc, 0u, kvn / 2, m->stream);
         if (e == hipSuccess) e = hipStreamSynchronize(m->stream);

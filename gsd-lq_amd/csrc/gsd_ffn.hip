@@ -101,7 +101,10 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int b = blockIdx.x;
-    const unsigned tag = *(KU32*)a.epoch;
+    // this launch's tag: the block's launch count + 1 (every block's count
+    // is the same; the block's own word, read by no other block)
+    const unsigned tag = *(KU32*)(a.ctr + b) + 1u;
+    if (tid == 0) a.ctr[b] = tag;
     const int lim = a.spin_limit;
     const int hidden = a.hidden, ffn = a.ffn, nb = a.nb, hpad = a.hpad;
     const bool reduces = b < a.nslices;
@@ -531,18 +534,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     }
 }
 
-// the epoch of the fused FFN launch that follows, where no o launch precedes
-// it on the stream (a launch of the FFN alone)
-__global__ void bump_kernel(unsigned* p) {
-    __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 }  // namespace
-
-hipError_t launch_bump(unsigned* p, hipStream_t st) {
-    hipLaunchKernelGGL(bump_kernel, dim3(1), dim3(1), 0, st, p);
-    return hipGetLastError();
-}
 
 size_t ffn_words(int hidden, int ffn) {
     const int nb = ffn / 64, hpad = (hidden + 15) / 16 * 16;
@@ -560,7 +552,7 @@ bool ffn_supported(int hidden, int ffn) {
 hipError_t launch_ffn(const FfnArgs& a0, hipStream_t st) {
     if (!ffn_supported(a0.hidden, a0.ffn)) return hipErrorNotSupported;
     if (!a0.gcodes || !a0.ucodes || !a0.dcodes || !a0.fields || !a0.x || !a0.norm_w || !a0.h || !a0.words ||
-        !a0.epoch || a0.n_pts < 1 || a0.n_pts > kTableSlots)
+        !a0.ctr || a0.n_pts < 1 || a0.n_pts > kTableSlots)
         return hipErrorInvalidValue;
     const bool r2 = a0.gU != nullptr;
     if (r2 && (!a0.uU || !a0.dU || !a0.gS || !a0.uS || !a0.dS || !a0.gVt || !a0.uVt || !a0.dVt))
@@ -574,6 +566,7 @@ hipError_t launch_ffn(const FfnArgs& a0, hipStream_t st) {
     a.ns2 = (a.hidden + 31) / 32;
     if (a.spin_limit <= 0) a.spin_limit = kFfnSpinLimit;
     const int grid = std::max(a.nb, a.nslices);
+    if (grid > kFfnMaxGrid) return hipErrorNotSupported;
     const int p1 = a.nc <= kFfnWaves ? 1 : a.nc / kFfnWaves;
     const bool b7 = a.n_pts <= 128;
 #define GSD_FFN(P, B, R) \

@@ -79,9 +79,6 @@ struct HexArgs {
     // be zero when the launch starts (each launch of a sequence has its own).
     unsigned long long* pub;
     unsigned* err;             // set to 1 when the wait exceeds its bound
-    // non-null: one thread of block 0 adds one to *bump (the epoch of the
-    // fused FFN launch that follows on the stream)
-    unsigned* bump;
     // Decode attention in the q/k/v launch (kEpiRopeKV, positions < 256):
     // the last nkv blocks of the grid are attention blocks, one per KV head.
     // The q/k/v epilogue publishes its outputs as 64-bit words, tag << 32 |
@@ -129,9 +126,11 @@ constexpr int kLeadMax = kMaxSeg * kMaxRank;   // publishing blocks per launch
 // (deterministic), adds the rank-k and kink terms and the residual, and
 // writes x.  Every block of the grid is resident at once (grid <= CU count,
 // one block per CU), so the wait for the words ends (bounded: a timeout sets
-// *err).  tag = *epoch, which an earlier launch on the stream advances once
-// per FFN launch (the o launch: HexArgs::bump), so words of other launches
-// never match and nothing is cleared.
+// *err).  The tag is the launch count + 1: block b reads its own counter
+// ctr[b] and stores it plus one (no other block reads ctr[b], and every block
+// of every launch advances its own once, so all counters agree), so words of
+// other launches never match and nothing is cleared (the counters wrap after
+// 2^32 launches of one model).  Zero ctr and words at allocation.
 struct FfnArgs {
     // gate / up in the tiled matvec layout (HexSeg::codes_t / scales_t)
     const unsigned char* gcodes;
@@ -171,7 +170,7 @@ struct FfnArgs {
     float eps;
     float* h;                    // the SwiGLU values (written for inspection)
     unsigned long long* words;   // [nb][hpad] partials, [nb][2] rank words, [ffn] h words
-    const unsigned* epoch;
+    unsigned* ctr;               // [grid] launch counters, one per block
     unsigned* err;
     int hidden, ffn;
     int nb;          // working blocks: ffn / 64
@@ -183,10 +182,9 @@ struct FfnArgs {
     int spin_limit;  // polling rounds before a wait counts as timed out
 };
 hipError_t launch_ffn(const FfnArgs& a, hipStream_t stream);
-// *p += 1 on the device (the FFN epoch where no o launch advances it)
-hipError_t launch_bump(unsigned* p, hipStream_t stream);
-// words an FfnArgs::words buffer needs for a model shape
+// words an FfnArgs::words buffer needs for a model shape, and the counters
 size_t ffn_words(int hidden, int ffn);
+constexpr int kFfnMaxGrid = 1024;
 // whether launch_ffn covers the shape (grid within the CU count, chunking)
 bool ffn_supported(int hidden, int ffn);
 

@@ -1976,9 +1976,6 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
         __asm__ volatile("" ::"s"(t0), "s"(t1), "s"(t2), "s"(t3), "s"(t4), "s"(t5), "s"(t6), "s"(t7), "s"(t8), "s"(t9)
                          : "memory");
     }
-    // the epoch of the fused FFN launch that follows (no return value: no wait)
-    if (blockIdx.x == 0 && threadIdx.x == 0 && a.bump)
-        __hip_atomic_fetch_add(a.bump, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // (argument values used right away pass through an asm placed after the
     // batch, so nothing waits for them before the batch is out)
     unsigned bdim = blockDim.x;

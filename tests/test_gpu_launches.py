@@ -220,8 +220,8 @@ def test_ffn_launch_full_shape(layer7b):
 
 
 def test_ffn_launch_repeat_bit_identical(layer7b):
-    """The fused FFN's cross-block sums run in a fixed block order: two runs
-    on the same x give the same bits (each with a new epoch)."""
+    """The fused FFN's cross-block sums run in a fixed block order: runs on
+    the same x give the same bits (each launch with a new tag)."""
     mode, gpu, _ = layer7b
     x = np.random.default_rng(109).standard_normal(gpu.hidden).astype(np.float32)
     outs = []
@@ -236,8 +236,8 @@ def test_ffn_launch_repeat_bit_identical(layer7b):
 def test_ffn_launch_ragged_kinks(mode):
     """The fused FFN at hidden 2048 / ffn 5056 (79 row blocks of 64, 128
     reducing slices, one chunk of x per wave) with kink terms in gate, up and
-    down (down's read h of other blocks through the tagged h words), after an
-    o launch (which advances the FFN epoch) and alone."""
+    down (down's read h of other blocks through the tagged h words), alone
+    and after an o launch."""
     from gsdlq import synth
     import run_gpu_native_chat as chat
     banner(f"fused FFN 2048 / 5056 {mode}, kinks")
