@@ -495,6 +495,7 @@ struct gsdh_model {
     unsigned long long* ffn_words = nullptr;
     unsigned* ffn_ctr = nullptr;
     bool ffn_on = true;                  // GSD_FUSED_FFN=0 turns it off (A/B)
+    bool offn_on = true;                 // the o projection in the same launch (GSD_FUSED_OFFN=0: off)
     int chunk = 64, max_splits = 1;
     StepState* st = nullptr;        // device
     StepState* st_host = nullptr;   // pinned
@@ -606,7 +607,17 @@ bool ffn_fused(gsdh_model* m, int l) {
     return (g.k == 0 && u.k == 0 && d.k == 0) || (g.k == 2 && u.k == 2 && d.k == 2);
 }
 
-int issue_ffn(gsdh_model* m, int l) {
+// Whether layer l's o projection runs in the same launch as its FFN: the FFN
+// fused, o of the FFN's radius and rank, o square (n_heads * head_dim ==
+// hidden: its input chunks are the FFN's).
+bool offn_fused(gsdh_model* m, int l) {
+    if (!m->offn_on || !ffn_fused(m, l)) return false;
+    const HexDev& o = m->slot(l, GSDH_O);
+    const HexDev& g = m->slot(l, GSDH_GATE);
+    return o.radius == g.radius && o.k == g.k && o.cols == o.rows;
+}
+
+int issue_ffn(gsdh_model* m, int l, bool with_o) {
     const auto& c = m->c;
     const HexDev& g = m->slot(l, GSDH_GATE);
     const HexDev& u = m->slot(l, GSDH_UP);
@@ -625,6 +636,14 @@ int issue_ffn(gsdh_model* m, int l) {
         a.gS = g.Sv; a.uS = u.Sv; a.dS = d.Sv;
         a.gVt = g.Vt; a.uVt = u.Vt; a.dVt = d.Vt;
     }
+    if (with_o) {
+        const HexDev& o = m->slot(l, GSDH_O);
+        a.ocodes = reinterpret_cast<const unsigned char*>(o.codes_t); a.oscales = o.scales_t;
+        if (o.nk) { a.o_rp = o.row_ptr; a.o_kc = o.kcols; a.o_kd = o.kdel; }
+        if (o.k == 2) { a.oU = o.U; a.oS = o.Sv; a.oVt = o.Vt; }
+        a.attn = m->attn;
+        a.qd = o.cols;
+    }
     a.x = m->x; a.norm_w = m->norm(l, 1); a.eps = c.rms_eps; a.h = m->h;
     a.words = m->ffn_words; a.ctr = m->ffn_ctr; a.err = &m->st->err;
     a.hidden = c.hidden; a.ffn = c.ffn;
@@ -634,15 +653,17 @@ int issue_ffn(gsdh_model* m, int l) {
 
 int issue_linear(gsdh_model* m, int l, int mask) {
     int rc = 0;
-    // gate/up and down together: one fused FFN launch where it covers the layer
+    // gate/up and down together: one fused FFN launch where it covers the
+    // layer, with o in it too where o is issued with them
     const bool fffn = (mask & 12) == 12 && ffn_fused(m, l);
+    const bool fo = fffn && (mask & 2) && offn_fused(m, l);
     if (mask & 1) {
         HexArgs a = qkv_args(m, l);
         if ((rc = prep_lowrank(m, a))) return rc;
         HIPCHK(launch_hexmv4(a, m->stream));
     }
     const auto& c = m->c;
-    if (mask & 2) {   // o projection + residual
+    if ((mask & 2) && !fo) {   // o projection + residual
         HexArgs a{};
         a.nseg = 1;
         fill_seg(a.seg[0], m->slot(l, GSDH_O), m, m->x);
@@ -651,7 +672,7 @@ int issue_linear(gsdh_model* m, int l, int mask) {
         if ((rc = prep_lowrank(m, a))) return rc;
         HIPCHK(launch_hexmv4(a, m->stream));
     }
-    if (fffn) return issue_ffn(m, l);
+    if (fffn) return issue_ffn(m, l, fo);
     if (mask & 4) {   // gate + up with fused FFN RMSNorm and SwiGLU
         HexArgs a{};
         a.nseg = 2;
@@ -980,6 +1001,8 @@ int gsdh_model_create(const gsdh_model_config* cfg, gsdh_model** out) {
         m->fa_on = !(fe && fe[0] == '0');
         fe = std::getenv("GSD_FUSED_FFN");
         m->ffn_on = !(fe && fe[0] == '0') && ffn_supported(c.hidden, c.ffn);
+        fe = std::getenv("GSD_FUSED_OFFN");
+        m->offn_on = m->ffn_on && !(fe && fe[0] == '0') && c.n_heads * c.head_dim == c.hidden;
     }
     if (m->ffn_on) {
         A((void**)&m->ffn_words, ffn_words(c.hidden, c.ffn) * 8);
@@ -1327,7 +1350,7 @@ int gsdh_model_prefill(gsdh_model* m, const int* tokens, int n, int start_pos, i
 int gsdh_model_fused_ffn(gsdh_model* m, int layer) {
     if (!m) return fail(-1, "fused_ffn: null model");
     if (layer < 0 || layer >= m->c.n_layers) return fail(-1, "fused_ffn: layer %d", layer);
-    return ffn_fused(m, layer) ? 1 : 0;
+    return ffn_fused(m, layer) ? (offn_fused(m, layer) ? 2 : 1) : 0;
 }
 
 int gsdh_model_set_prefill(gsdh_model* m, int batched) {

@@ -81,16 +81,27 @@ __device__ __forceinline__ int pair_dword(int q) {
 
 // P1: 128-column chunks of x per wave (waves at or past the chunk count have
 // none); B7: 7-bit code tiles (codebooks of <= 128 points); R2: every tensor
-// carries a rank-2 term
-template <int P1, bool B7, bool R2>
+// carries a rank-2 term; OF: the o projection and its residual add first
+// (x = x + W_o attn, formed 16 rows per block and handed over as tagged
+// words), so a layer's o and FFN are one launch
+template <int P1, bool B7, bool R2, bool OF>
 __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) ffn_kernel(const FfnArgs a) {
+    // arguments used outside the main loops are read where they are used,
+    // through the argument segment (the asm keeps the compiler from holding
+    // them all in scalar registers across the loops, where they spilled)
+    using KA = const __attribute__((address_space(4))) FfnArgs;
+    KA* ka = (KA*)__builtin_amdgcn_kernarg_segment_ptr();
+    __asm__ volatile("" : "+s"(ka));
     constexpr int NW = kFfnWaves, TBY = B7 ? kTile7 : kTileU8, D = kFfnDepth;
     __shared__ __attribute__((aligned(16))) uint32_t stab[kTableSlots * 64];   // lane copies of the codebook
     __shared__ __attribute__((aligned(16))) uint32_t xop[NW][P1 * 128];       // each wave's x operands
     __shared__ __attribute__((aligned(16))) uint32_t hop[64];                 // the block's h operands
     __shared__ float red[NW][8][16];
+    __shared__ float rsum[NW][16];         // slice sums of each wave
     __shared__ float ssq[NW];
     __shared__ float vtp[NW][4];
+    __shared__ float ovtp[NW][2];          // OF: each wave's attn . Vt_o[j]
+    __shared__ float sS[8];                // OF, R2: S_o[j] at 6 + j
     __shared__ uint32_t hu[3][64];         // R2, lane l: U of gate / up row 64 b + l, down Vt column 64 b + l
     __shared__ float hsc;                  // descale of the h operands
     __shared__ float tk[2];                // down's rank values S[j] * (Vt[j] . h)
@@ -115,46 +126,89 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     uint32_t xres = 0u, dur = 0u;
     if (reduces && wid == 0) {
         const int r = min(srow, hidden - 1);
-        xres = __float_as_uint(a.x[r]);
-        if constexpr (R2) dur = reinterpret_cast<const uint32_t*>(a.dU)[r];
+        xres = __float_as_uint(ka->x[r]);
+        if constexpr (R2) dur = reinterpret_cast<const uint32_t*>(ka->dU)[r];
     }
 
-    if (b < nb) {
+    // OF: block s < nslices first forms rows 16 s .. 16 s + 15 of x + W_o attn
+    // (the o projection of the token, gsd_lq_cpu_runtime.py:376-378), the
+    // rows every block's gate / up input needs, and publishes them as tagged
+    // words (xw)
+    const bool work = b < nb, doO = OF && reduces;
+    unsigned long long* xw = a.words + (size_t)nb * hpad + 2 * nb + ffn;
+    if (work || doO) {
         const int nc = a.nc;
-        const int p1 = wid < nc ? P1 : 0;   // chunks of this wave: wid + NW p, p < p1
+        const int p1 = work && wid < nc ? P1 : 0;   // chunks of this wave: wid + NW p, p < p1
+        const int po = doO && wid < nc ? P1 : 0;    // (o: as many input chunks as gate / up)
         const int n1 = 8 * p1;
-        const int n2 = wid < a.ns2 ? (a.ns2 - 1 - wid) / NW + 1 : 0;
+        const int n2 = work && wid < a.ns2 ? (a.ns2 - 1 - wid) / NW + 1 : 0;
         const int nsteps = n1 + n2;
         const uint32_t lto = tile_lane_off(B7, lane), lso = (uint32_t)(lane & 15);
         const int nrb = a.nrb;
 
-        // ---- prologue: x, the norm weights and the rank-2 rows of the
-        // wave's chunks, then the epilogue inputs, then the first code steps
+        // ---- prologue.  OF: the wave's chunks of attn and of o's rank-2
+        // rows, o's code steps of the block's unit, o's epilogue inputs.
+        // Otherwise: x, the norm weights and the rank-2 rows of the wave's
+        // chunks.  Then the FFN's epilogue inputs and first code steps.
+        float2 av[P1];
+        uint32_t avt[P1][2];
+        uint4 ocw[P1];
+        uint32_t osw[P1];
+        uint32_t oug = 0u;
+        float osv = 0.f;
+        if constexpr (OF) {
+            if (po) {
+#pragma unroll
+                for (int p = 0; p < P1; p++) {
+                    const int c0 = (wid + NW * p) * 128 + 2 * lane;
+                    av[p] = *reinterpret_cast<const float2*>(ka->attn + c0);
+                    if constexpr (R2) {
+                        avt[p][0] = *reinterpret_cast<const uint32_t*>(ka->oVt + c0);
+                        avt[p][1] = *reinterpret_cast<const uint32_t*>(ka->oVt + hidden + c0);
+                    }
+                }
+#pragma unroll
+                for (int p = 0; p < P1; p++) {
+                    const size_t t = (size_t)b * nc + wid + NW * p;
+                    ocw[p] = tile_load(ka->ocodes + t * TBY + lto);
+                    osw[p] = ka->oscales[t * 16 + lso];
+                }
+            }
+            if (R2 && doO && wid == 0) {
+                oug = reinterpret_cast<const uint32_t*>(ka->oU)[min(srow, hidden - 1)];
+                osv = ka->oS[lane & 1];
+            }
+        }
         float2 xv[P1], wv[P1];
         uint32_t vt[P1][4];
-        if (p1) {
+        auto load_x_aux = [&]() {   // the norm weights and rank-2 rows of the wave's chunks
 #pragma unroll
             for (int p = 0; p < P1; p++) {
                 const int c0 = (wid + NW * p) * 128 + 2 * lane;
-                xv[p] = *reinterpret_cast<const float2*>(a.x + c0);
-                wv[p] = *reinterpret_cast<const float2*>(a.norm_w + c0);
+                wv[p] = *reinterpret_cast<const float2*>(ka->norm_w + c0);
                 if constexpr (R2) {
-                    vt[p][0] = *reinterpret_cast<const uint32_t*>(a.gVt + c0);
-                    vt[p][1] = *reinterpret_cast<const uint32_t*>(a.gVt + hidden + c0);
-                    vt[p][2] = *reinterpret_cast<const uint32_t*>(a.uVt + c0);
-                    vt[p][3] = *reinterpret_cast<const uint32_t*>(a.uVt + hidden + c0);
+                    vt[p][0] = *reinterpret_cast<const uint32_t*>(ka->gVt + c0);
+                    vt[p][1] = *reinterpret_cast<const uint32_t*>(ka->gVt + hidden + c0);
+                    vt[p][2] = *reinterpret_cast<const uint32_t*>(ka->uVt + c0);
+                    vt[p][3] = *reinterpret_cast<const uint32_t*>(ka->uVt + hidden + c0);
                 }
             }
+        };
+        if (!OF && p1) {
+#pragma unroll
+            for (int p = 0; p < P1; p++)
+                xv[p] = *reinterpret_cast<const float2*>(ka->x + (wid + NW * p) * 128 + 2 * lane);
+            load_x_aux();
         }
         // wave 0: U rows of the block's gate and up rows, down's Vt columns
         // of the block's slab (lane l: FFN row / column 64 b + l)
         const int frow = 64 * b + lane, fr = min(frow, ffn - 1);
         uint32_t gur = 0u, uur = 0u, dv0 = 0u, dv1 = 0u;
-        if (R2 && wid == 0) {
-            gur = reinterpret_cast<const uint32_t*>(a.gU)[fr];
-            uur = reinterpret_cast<const uint32_t*>(a.uU)[fr];
-            dv0 = a.dVt[fr];
-            dv1 = a.dVt[ffn + fr];
+        if (R2 && work && wid == 0) {
+            gur = reinterpret_cast<const uint32_t*>(ka->gU)[fr];
+            uur = reinterpret_cast<const uint32_t*>(ka->uU)[fr];
+            dv0 = ka->dVt[fr];
+            dv1 = ka->dVt[ffn + fr];
         }
 
         auto step_ptr = [&](int s, const unsigned char*& cp, const uint32_t*& sp) {
@@ -187,8 +241,8 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
 
         // codebook: entry e of lane l at byte e * 256 + l * 4; wave w
         // writes entries 16 w .. 16 w + 15 (one 64-byte scalar read)
-        if (wid * 16 < a.n_pts) {
-            KU32* fp = (KU32*)a.fields + wid * 16;
+        if (wid * 16 < ka->n_pts) {
+            KU32* fp = (KU32*)ka->fields + wid * 16;
             uint32_t fv[16];
 #pragma unroll
             for (int j = 0; j < 16; j++) fv[j] = fp[j];
@@ -196,75 +250,226 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
             for (int j = 0; j < 16; j++) stab[(wid * 16 + j) * 64 + lane] = fv[j];
         }
 
+        // OF: attn operands as the x operands below (no norm weights), with
+        // the wave's o rank-2 partials attn . Vt_o[j]
+        float odk0 = 0.f, odk1 = 0.f, dno = 0.f;
+        if constexpr (OF) {
+            float omx = 0.f;
+            if (po) {
+#pragma unroll
+                for (int p = 0; p < P1; p++) {
+                    const float xa = av[p].x, xb = av[p].y;
+                    if constexpr (R2) {
+                        odk0 = fmaf(xa, h2f((uint16_t)(avt[p][0] & 0xFFFFu)), odk0);
+                        odk0 = fmaf(xb, h2f((uint16_t)(avt[p][0] >> 16)), odk0);
+                        odk1 = fmaf(xa, h2f((uint16_t)(avt[p][1] & 0xFFFFu)), odk1);
+                        odk1 = fmaf(xb, h2f((uint16_t)(avt[p][1] >> 16)), odk1);
+                    }
+                    const float u = xa, v = fmaf(kS32f, xb, 0.5f * xa);
+                    omx = fmaxf(omx, fmaxf(fabsf(u), fabsf(v)));
+                    xop[wid][p * 128 + pair_dword(lane)] = __float_as_uint(u);
+                    xop[wid][p * 128 + pair_dword(lane) + 4] = __float_as_uint(v);
+                }
+            }
+            omx = wave_max_nonneg(omx);
+            if constexpr (R2) {
+                odk0 = wave_sum_valu(odk0);
+                odk1 = wave_sum_valu(odk1);
+            }
+            int ex = 0;
+            if (omx > 0.f && omx < INFINITY) (void)frexpf(omx, &ex);
+            const float up0 = ldexpf(1.f, 14 - ex);
+            dno = ldexpf(1.f, ex - 14);
+            if (po) {
+#pragma unroll
+                for (int p = 0; p < P1; p++) {
+                    const int o = p * 128 + pair_dword(lane);
+                    uint32_t hi, lo;
+                    hilo(__uint_as_float(xop[wid][o]), __uint_as_float(xop[wid][o + 4]), up0, hi, lo);
+                    xop[wid][o] = hi;
+                    xop[wid][o + 4] = lo;
+                }
+            }
+            if (lane == 0) {
+                ovtp[wid][0] = odk0;
+                ovtp[wid][1] = odk1;
+            }
+            if (R2 && doO && wid == 0) {
+                hu[2][lane] = oug;   // (lanes 0-15: U_o of the slice rows)
+                if (lane < 2) sS[6 + lane] = osv;
+            }
+        }
+
         // x operands: pair `lane` of chunk p -> (u, v) of x' = x * w (the
         // RMSNorm factor goes on the finished sums), sum of x^2, the rank-2
         // partials x' . Vt[j] over the wave's columns
-        float ss = 0.f, mx = 0.f, dk[4] = {0.f, 0.f, 0.f, 0.f};
-        if (p1) {
+        float dn1 = 1.f;
+        auto stage_x = [&]() {
+            float ss = 0.f, mx = 0.f, dk[4] = {0.f, 0.f, 0.f, 0.f};
+            if (p1) {
 #pragma unroll
-            for (int p = 0; p < P1; p++) {
-                ss = fmaf(xv[p].x, xv[p].x, ss);
-                ss = fmaf(xv[p].y, xv[p].y, ss);
-                const float xa = xv[p].x * wv[p].x, xb = xv[p].y * wv[p].y;
-                if constexpr (R2) {
+                for (int p = 0; p < P1; p++) {
+                    ss = fmaf(xv[p].x, xv[p].x, ss);
+                    ss = fmaf(xv[p].y, xv[p].y, ss);
+                    const float xa = xv[p].x * wv[p].x, xb = xv[p].y * wv[p].y;
+                    if constexpr (R2) {
 #pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        dk[r] = fmaf(xa, h2f((uint16_t)(vt[p][r] & 0xFFFFu)), dk[r]);
-                        dk[r] = fmaf(xb, h2f((uint16_t)(vt[p][r] >> 16)), dk[r]);
+                        for (int r = 0; r < 4; r++) {
+                            dk[r] = fmaf(xa, h2f((uint16_t)(vt[p][r] & 0xFFFFu)), dk[r]);
+                            dk[r] = fmaf(xb, h2f((uint16_t)(vt[p][r] >> 16)), dk[r]);
+                        }
                     }
+                    const float u = xa, v = fmaf(kS32f, xb, 0.5f * xa);
+                    mx = fmaxf(mx, fmaxf(fabsf(u), fabsf(v)));
+                    xop[wid][p * 128 + pair_dword(lane)] = __float_as_uint(u);
+                    xop[wid][p * 128 + pair_dword(lane) + 4] = __float_as_uint(v);
                 }
-                const float u = xa, v = fmaf(kS32f, xb, 0.5f * xa);
-                mx = fmaxf(mx, fmaxf(fabsf(u), fabsf(v)));
-                xop[wid][p * 128 + pair_dword(lane)] = __float_as_uint(u);
-                xop[wid][p * 128 + pair_dword(lane) + 4] = __float_as_uint(v);
             }
-        }
-        ss = wave_sum_valu(ss);
-        mx = wave_max_nonneg(mx);
-        if constexpr (R2) {
+            ss = wave_sum_valu(ss);
+            mx = wave_max_nonneg(mx);
+            if constexpr (R2) {
 #pragma unroll
-            for (int r = 0; r < 4; r++) dk[r] = wave_sum_valu(dk[r]);
-        }
-        if (lane == 0) {
-            ssq[wid] = ss;
-            vtp[wid][0] = dk[0];
-            vtp[wid][1] = dk[1];
-            vtp[wid][2] = dk[2];
-            vtp[wid][3] = dk[3];
-        }
+                for (int r = 0; r < 4; r++) dk[r] = wave_sum_valu(dk[r]);
+            }
+            if (lane == 0) {
+                ssq[wid] = ss;
+                vtp[wid][0] = dk[0];
+                vtp[wid][1] = dk[1];
+                vtp[wid][2] = dk[2];
+                vtp[wid][3] = dk[3];
+            }
+            // power-of-two scale putting the wave's largest |u|, |v| in [2^13, 2^14)
+            int ex = 0;
+            if (mx > 0.f && mx < INFINITY) (void)frexpf(mx, &ex);
+            const float up1 = ldexpf(1.f, 14 - ex);
+            dn1 = ldexpf(1.f, ex - 14);
+            if (p1) {
+#pragma unroll
+                for (int p = 0; p < P1; p++) {
+                    const int o = p * 128 + pair_dword(lane);
+                    uint32_t hi, lo;
+                    hilo(__uint_as_float(xop[wid][o]), __uint_as_float(xop[wid][o + 4]), up1, hi, lo);
+                    xop[wid][o] = hi;
+                    xop[wid][o + 4] = lo;
+                }
+            }
+        };
+        if (!OF) stage_x();
         // (every loaded register is stored before the loops: a register
         // whose load is still pending at a use after them would make the
         // compiler drain the code loads in flight there)
-        if (R2 && wid == 0) {
+        if (R2 && work && wid == 0) {
             hu[0][lane] = gur;
             hu[1][lane] = uur;
-            hu[2][lane] = frow < ffn ? (dv0 | (dv1 << 16)) : 0u;
+            if (!OF) hu[2][lane] = frow < ffn ? (dv0 | (dv1 << 16)) : 0u;
         }
-        if (reduces && wid == 0 && lane < 16) {
+        if (!OF && reduces && wid == 0 && lane < 16) {
             pres[0][lane] = xres;
             pres[1][lane] = dur;
         }
-        // power-of-two scale putting the wave's largest |u|, |v| in [2^13, 2^14)
-        int ex = 0;
-        if (mx > 0.f && mx < INFINITY) (void)frexpf(mx, &ex);
-        const float up1 = ldexpf(1.f, 14 - ex), dn1 = ldexpf(1.f, ex - 14);
-        if (p1) {
-#pragma unroll
-            for (int p = 0; p < P1; p++) {
-                const int o = p * 128 + pair_dword(lane);
-                uint32_t hi, lo;
-                hilo(__uint_as_float(xop[wid][o]), __uint_as_float(xop[wid][o + 4]), up1, hi, lo);
-                xop[wid][o] = hi;
-                xop[wid][o + 4] = lo;
-            }
-        }
-        // the codebook (and every wave's own x operands) in LDS
+        // the codebook and every wave's own operands in LDS
         lds_barrier();
 
         const uint32_t lane_off = (uint32_t)lane * 4u;
         const uint32_t sh7 = (uint32_t)(lane & 1) * 16u;
         const int m = lane & 15, lg = lane >> 4;
         const uint4* Xw = reinterpret_cast<const uint4*>(xop[wid]);
+
+        if constexpr (OF) {
+            // ---- o: the block's 16 rows over the wave's chunks of attn
+            if (doO) {
+                float acc = 0.f;
+                for (int p = 0; p < po; p++) {
+                    u32x4v A[2][2];
+#pragma unroll
+                    for (int h = 0; h < 2; h++)
+#pragma unroll
+                        for (int t = 0; t < 2; t++) {
+                            const uint4 v = Xw[(((p * 2 + h) * 2 + t) * 4 + lg) * 2 + (m & 1)];
+                            A[h][t][0] = v.x; A[h][t][1] = v.y; A[h][t][2] = v.z; A[h][t][3] = v.w;
+                        }
+                    float r0, r1;
+                    tile_dots<B7>(ocw[p], stab, lane_off, sh7, A[0], A[1], r0, r1);
+                    acc = fmaf(r0, h2f((uint16_t)(osw[p] & 0xFFFFu)), acc);
+                    acc = fmaf(r1, h2f((uint16_t)(osw[p] >> 16)), acc);
+                }
+                if (lane < 16) red[wid][0][lane] = acc * dno;
+                lds_barrier();
+                if (wid == 0) {
+                    // x + (W_o attn + kinks + U_o S_o (Vt_o attn)), gsd_lq_cpu_engine.c:129-183
+                    float y = 0.f, d0 = 0.f, d1 = 0.f;
+                    for (int w = 0; w < NW; w++) {
+                        y += red[w][0][lane & 15];
+                        d0 += ovtp[w][0];
+                        d1 += ovtp[w][1];
+                    }
+                    if (ka->o_rp && srow < hidden) {
+                        const uint32_t e = ka->o_rp[srow + 1];
+                        for (uint32_t i = ka->o_rp[srow]; i < e; i++) y += ka->o_kd[i] * ka->attn[ka->o_kc[i]];
+                    }
+                    if constexpr (R2) {
+                        const uint32_t uw = hu[2][lane & 15];
+                        y += h2f((uint16_t)(uw & 0xFFFFu)) * (sS[6] * d0);
+                        y += h2f((uint16_t)(uw >> 16)) * (sS[7] * d1);
+                    }
+                    const float xn = __uint_as_float(xres) + y;
+                    if (lane < 16) {
+                        pres[0][lane] = __float_as_uint(xn);
+                        pres[1][lane] = dur;
+                        if (srow < hidden)
+                            __hip_atomic_store(xw + srow, ((unsigned long long)tag << 32) | __float_as_uint(xn),
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                }
+            }
+            if (work) {
+                // ---- x = x + W_o attn of every row the wave's chunks cover,
+                // from the blocks that formed them (bounded wait); with it
+                // the norm weights and rank-2 rows
+                if (p1) load_x_aux();
+                if (p1) {
+                    const __amdgpu_buffer_rsrc_t rx =
+                        __builtin_amdgcn_make_buffer_rsrc(xw, (short)0, hidden * 8, 0x00020000);
+                    for (int spins = 0;; spins++) {
+                        bool done = true;
+#pragma unroll
+                        for (int p = 0; p < P1; p++) {
+                            const auto q = __builtin_amdgcn_raw_buffer_load_b128(
+                                rx, ((wid + NW * p) * 128 + 2 * lane) * 8, 0, 16 /* sc1 */);
+                            done = done && q[1] == tag && q[3] == tag;
+                            xv[p] = make_float2(__uint_as_float(q[0]), __uint_as_float(q[2]));
+                        }
+                        if (done) break;
+                        if (spins >= lim) {
+                            if (ka->err) *ka->err = 1u;
+                            break;
+                        }
+                        __builtin_amdgcn_s_sleep(2);
+                    }
+                }
+                stage_x();
+                if (R2 && wid == 0) hu[2][lane] = frow < ffn ? (dv0 | (dv1 << 16)) : 0u;
+                lds_barrier();   // (also: every wave's o operands read before the x operands replace them)
+            }
+        }
+        if (work) {
+        const uint32_t lane_off = (uint32_t)lane * 4u;
+        const uint32_t sh7 = (uint32_t)(lane & 1) * 16u;
+        const int m = lane & 15, lg = lane >> 4;
+        const uint4* Xw = reinterpret_cast<const uint4*>(xop[wid]);
+
+        // x[c] of the FFN input (OF: x + W_o attn, from the tagged words)
+        auto xin = [&](int c) -> float {
+            if constexpr (!OF) return ka->x[c];
+            unsigned long long v;
+            int spins = 0;
+            while ((unsigned)((v = __hip_atomic_load(xw + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) >> 32) != tag &&
+                   spins < lim) {
+                if (++spins == lim && ka->err) *ka->err = 1u;
+                __builtin_amdgcn_s_sleep(2);
+            }
+            return __uint_as_float((unsigned)v);
+        };
 
         // ---- gate / up: 8 row groups (gate units 0-3, up units 0-3) per chunk
         float acc[8];
@@ -304,7 +509,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
         if (wid == 0) {
             float sx = 0.f;
             for (int w = 0; w < NW; w++) sx += ssq[w];
-            const float inv = 1.0f / sqrtf(sx / (float)hidden + a.eps);
+            const float inv = 1.0f / sqrtf(sx / (float)hidden + ka->eps);
             const int k = lane >> 4, r = lane & 15;
             float g = 0.f, u = 0.f;
             for (int w = 0; w < NW; w++) {
@@ -314,18 +519,18 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
             g *= inv;
             u *= inv;
             if (frow < ffn) {
-                if (a.g_rp) {
-                    const uint32_t e = a.g_rp[frow + 1];
-                    for (uint32_t i = a.g_rp[frow]; i < e; i++) {
-                        const int c = a.g_kc[i];
-                        g += a.g_kd[i] * ((a.x[c] * inv) * a.norm_w[c]);
+                if (ka->g_rp) {
+                    const uint32_t e = ka->g_rp[frow + 1];
+                    for (uint32_t i = ka->g_rp[frow]; i < e; i++) {
+                        const int c = ka->g_kc[i];
+                        g += ka->g_kd[i] * ((xin(c) * inv) * ka->norm_w[c]);
                     }
                 }
-                if (a.u_rp) {
-                    const uint32_t e = a.u_rp[frow + 1];
-                    for (uint32_t i = a.u_rp[frow]; i < e; i++) {
-                        const int c = a.u_kc[i];
-                        u += a.u_kd[i] * ((a.x[c] * inv) * a.norm_w[c]);
+                if (ka->u_rp) {
+                    const uint32_t e = ka->u_rp[frow + 1];
+                    for (uint32_t i = ka->u_rp[frow]; i < e; i++) {
+                        const int c = ka->u_kc[i];
+                        u += ka->u_kd[i] * ((xin(c) * inv) * ka->norm_w[c]);
                     }
                 }
                 if constexpr (R2) {
@@ -337,8 +542,8 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                         e1 += vtp[w][3];
                     }
                     // tmp_k[j] = S[j] * (x' . Vt[j]) (gsd_lq_cpu_engine.c:110-127)
-                    const float tg0 = ((KF32*)a.gS)[0] * (d0 * inv), tg1 = ((KF32*)a.gS)[1] * (d1 * inv);
-                    const float tu0 = ((KF32*)a.uS)[0] * (e0 * inv), tu1 = ((KF32*)a.uS)[1] * (e1 * inv);
+                    const float tg0 = ((KF32*)ka->gS)[0] * (d0 * inv), tg1 = ((KF32*)ka->gS)[1] * (d1 * inv);
+                    const float tu0 = ((KF32*)ka->uS)[0] * (e0 * inv), tu1 = ((KF32*)ka->uS)[1] * (e1 * inv);
                     const uint32_t gw = hu[0][lane], uw = hu[1][lane];
                     g += h2f((uint16_t)(gw & 0xFFFFu)) * tg0;
                     g += h2f((uint16_t)(gw >> 16)) * tg1;
@@ -349,8 +554,8 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
             // SwiGLU (gsd_lq_cpu_engine.c:96-108); rows past ffn are 0
             const float hv = frow < ffn ? (g / (1.0f + expf(-g))) * u : 0.f;
             if (frow < ffn) {
-                a.h[frow] = hv;
-                if (a.d_rp)   // (down's kinks read h of any block)
+                ka->h[frow] = hv;
+                if (ka->d_rp)   // (down's kinks read h of any block)
                     __hip_atomic_store(a.words + (size_t)nb * hpad + 2 * nb + frow,
                                        ((unsigned long long)tag << 32) | __float_as_uint(hv), __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
@@ -414,6 +619,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
 #pragma unroll
         for (int k = 0; k < D - 1; k++)
             if (i2 + k < n2) down_step(i2 + k, k);
+        }
     } else if (reduces && wid == 0 && lane < 16) {
         pres[0][lane] = xres;
         pres[1][lane] = dur;
@@ -450,7 +656,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
             for (int i = 0; i < NI; i++) done = done && (!use[i] || (unsigned)(wv[i] >> 32) == tag);
             if (done) break;
             if (spins >= lim) {
-                if (a.err) *a.err = 1u;
+                if (ka->err) *ka->err = 1u;
                 break;
             }
             __builtin_amdgcn_s_sleep(2);
@@ -460,7 +666,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
         for (int i = 0; i < NI; i++) v += use[i] ? __uint_as_float((unsigned)wv[i]) : 0.f;
         v = swap_add16(v, v);        // + the lane 16 apart (another block, same row)
         v = swap_add32(v, v, false);  // + the lanes 32 apart
-        if (lane < 16) red[wid][0][lane] = v;
+        if (lane < 16) rsum[wid][lane] = v;
         if (R2 && wid == 1) {
             // rank words: lane l, blocks l + 64 i, both j in one 16-byte load
             int ro[NI];
@@ -485,7 +691,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                     done = done && (!rok[i] || ((unsigned)(w0[i] >> 32) == tag && (unsigned)(w1[i] >> 32) == tag));
                 if (done) break;
                 if (spins >= lim) {
-                    if (a.err) *a.err = 1u;
+                    if (ka->err) *ka->err = 1u;
                     break;
                 }
                 __builtin_amdgcn_s_sleep(2);
@@ -499,30 +705,30 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
             d0 = wave_sum_valu(d0);
             d1 = wave_sum_valu(d1);
             if (lane == 0) {
-                tk[0] = ((KF32*)a.dS)[0] * d0;
-                tk[1] = ((KF32*)a.dS)[1] * d1;
+                tk[0] = ((KF32*)ka->dS)[0] * d0;
+                tk[1] = ((KF32*)ka->dS)[1] * d1;
             }
         }
     }
     lds_barrier();
     if (wid == 0 && lane < 16 && srow < hidden) {
         float y = 0.f;
-        for (int w = 0; w < NW; w++) y += red[w][0][lane];
-        if (a.d_rp) {
+        for (int w = 0; w < NW; w++) y += rsum[w][lane];
+        if (ka->d_rp) {
             // kink terms of down read h of any block (tagged words)
             const unsigned long long* hw = a.words + (size_t)nb * hpad + 2 * nb;
-            const uint32_t e = a.d_rp[srow + 1];
-            for (uint32_t i = a.d_rp[srow]; i < e; i++) {
-                const int c = a.d_kc[i];
+            const uint32_t e = ka->d_rp[srow + 1];
+            for (uint32_t i = ka->d_rp[srow]; i < e; i++) {
+                const int c = ka->d_kc[i];
                 unsigned long long v;
                 int spins = 0;
                 while ((unsigned)((v = __hip_atomic_load(hw + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) >> 32) !=
                            tag &&
                        spins < lim) {
-                    if (++spins == lim && a.err) *a.err = 1u;
+                    if (++spins == lim && ka->err) *ka->err = 1u;
                     __builtin_amdgcn_s_sleep(2);
                 }
-                y += a.d_kd[i] * __uint_as_float((unsigned)v);
+                y += ka->d_kd[i] * __uint_as_float((unsigned)v);
             }
         }
         if constexpr (R2) {
@@ -530,7 +736,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
             y += h2f((uint16_t)(uw & 0xFFFFu)) * tk[0];
             y += h2f((uint16_t)(uw >> 16)) * tk[1];
         }
-        a.x[srow] = __uint_as_float(pres[0][lane]) + y;
+        ka->x[srow] = __uint_as_float(pres[0][lane]) + y;
     }
 }
 
@@ -538,7 +744,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
 
 size_t ffn_words(int hidden, int ffn) {
     const int nb = ffn / 64, hpad = (hidden + 15) / 16 * 16;
-    return (size_t)nb * hpad + 2 * (size_t)nb + (size_t)ffn;
+    return (size_t)nb * hpad + 2 * (size_t)nb + (size_t)ffn + (size_t)hidden;
 }
 
 bool ffn_supported(int hidden, int ffn) {
@@ -554,8 +760,10 @@ hipError_t launch_ffn(const FfnArgs& a0, hipStream_t st) {
     if (!a0.gcodes || !a0.ucodes || !a0.dcodes || !a0.fields || !a0.x || !a0.norm_w || !a0.h || !a0.words ||
         !a0.ctr || a0.n_pts < 1 || a0.n_pts > kTableSlots)
         return hipErrorInvalidValue;
-    const bool r2 = a0.gU != nullptr;
+    const bool r2 = a0.gU != nullptr, of = a0.ocodes != nullptr;
     if (r2 && (!a0.uU || !a0.dU || !a0.gS || !a0.uS || !a0.dS || !a0.gVt || !a0.uVt || !a0.dVt))
+        return hipErrorInvalidValue;
+    if (of && (!a0.oscales || !a0.attn || a0.qd != a0.hidden || (r2 && (!a0.oU || !a0.oS || !a0.oVt))))
         return hipErrorInvalidValue;
     FfnArgs a = a0;
     a.nb = a.ffn / 64;
@@ -569,20 +777,18 @@ hipError_t launch_ffn(const FfnArgs& a0, hipStream_t st) {
     if (grid > kFfnMaxGrid) return hipErrorNotSupported;
     const int p1 = a.nc <= kFfnWaves ? 1 : a.nc / kFfnWaves;
     const bool b7 = a.n_pts <= 128;
-#define GSD_FFN(P, B, R) \
-    if (p1 == P && b7 == B && r2 == R) hipLaunchKernelGGL((ffn_kernel<P, B, R>), dim3(grid), dim3(1024), 0, st, a)
-    GSD_FFN(1, true, true);
-    else GSD_FFN(1, true, false);
-    else GSD_FFN(1, false, true);
-    else GSD_FFN(1, false, false);
-    else GSD_FFN(2, true, true);
-    else GSD_FFN(2, true, false);
-    else GSD_FFN(2, false, true);
-    else GSD_FFN(2, false, false);
-    else GSD_FFN(4, true, true);
-    else GSD_FFN(4, true, false);
-    else GSD_FFN(4, false, true);
-    else GSD_FFN(4, false, false);
+#define GSD_FFN(P, B, R, O)                                                   \
+    if (p1 == P && b7 == B && r2 == R && of == O)                             \
+    hipLaunchKernelGGL((ffn_kernel<P, B, R, O>), dim3(grid), dim3(1024), 0, st, a)
+#define GSD_FFN4(P, B) \
+    GSD_FFN(P, B, true, true); else GSD_FFN(P, B, true, false); else GSD_FFN(P, B, false, true); else GSD_FFN(P, B, false, false)
+    GSD_FFN4(1, true);
+    else GSD_FFN4(1, false);
+    else GSD_FFN4(2, true);
+    else GSD_FFN4(2, false);
+    else GSD_FFN4(4, true);
+    else GSD_FFN4(4, false);
+#undef GSD_FFN4
 #undef GSD_FFN
     return hipGetLastError();
 }

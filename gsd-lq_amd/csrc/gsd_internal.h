@@ -165,11 +165,24 @@ struct FfnArgs {
     const uint16_t* gVt;
     const uint16_t* uVt;
     const uint16_t* dVt;
+    // OF (ocodes non-null): the o projection first, x += W_o attn (o in
+    // the tiled layout, qd == hidden columns), its rows formed by block
+    // s < nslices 16 at a time and handed to every block as tagged words
+    const unsigned char* ocodes;
+    const uint32_t* oscales;
+    const uint32_t* o_rp;
+    const uint16_t* o_kc;
+    const float* o_kd;
+    const uint16_t* oU;
+    const float* oS;
+    const uint16_t* oVt;
+    const float* attn;
+    int qd;
     float* x;                    // residual stream: read, then x += W_down h
     const float* norm_w;         // ffn_norm
     float eps;
     float* h;                    // the SwiGLU values (written for inspection)
-    unsigned long long* words;   // [nb][hpad] partials, [nb][2] rank words, [ffn] h words
+    unsigned long long* words;   // [nb][hpad] partials, [nb][2] rank words, [ffn] h words, [hidden] x words
     unsigned* ctr;               // [grid] launch counters, one per block
     unsigned* err;
     int hidden, ffn;

@@ -313,13 +313,16 @@ int gsdh_model_read_codes(gsdh_model* m, int layer, int slot, uint8_t* codes_out
  * full-shape parity tests of each launch. */
 int gsdh_model_run_linear(gsdh_model* m, int layer, int mask);
 
-/* 1 when gate/up + down of `layer` run as one fused FFN launch (mask 4 | 8 of
- * gsdh_model_run_linear and every decode token): h of each block's 64 FFN
+/* How `layer`'s o, gate/up and down projections run (no counterpart entry
+ * point): 2 = o, gate/up and down in one launch (mask 2 | 4 | 8 of
+ * gsdh_model_run_linear and every decode token: each block forms 16 rows of
+ * x + W_o attn and hands them over as tagged words, then h of its 64 FFN
  * rows, then that block's 64 columns of W_down as partial sums that the
- * launch reduces in block order (gsd_lq_cpu_runtime.py:384-404; no
- * counterpart entry point).  0 where the two launches run (GSD_FUSED_FFN=0,
- * shapes beyond the launch's grid, tensors of different radii or of ranks
- * other than all 0 / all 2), negative on a bad argument. */
+ * launch reduces in block order; gsd_lq_cpu_runtime.py:376-404); 1 = gate/up
+ * and down in one launch, o in its own (GSD_FUSED_OFFN=0, o not square or
+ * of another radius or rank; also mask 4 | 8 without 2); 0 = three launches
+ * (GSD_FUSED_FFN=0, shapes beyond the launch's grid, tensors of different
+ * radii or of ranks other than all 0 / all 2); negative on a bad argument. */
 int gsdh_model_fused_ffn(gsdh_model* m, int layer);
 
 /* Activation vectors of the model context (f32): x [hidden], q [n_heads*hd],

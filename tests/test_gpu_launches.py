@@ -206,7 +206,7 @@ def test_ffn_launch_full_shape(layer7b):
     launch, the decode's and the benchmark's): h, the down product and the
     new x against the oracle at the 7B shape."""
     mode, gpu, ref = layer7b
-    assert gpu.cl.lib.gsdh_model_fused_ffn(gpu._m, 0) == 1
+    assert gpu.cl.lib.gsdh_model_fused_ffn(gpu._m, 0) == 2
     rng = np.random.default_rng(108)
     x = rng.standard_normal(gpu.hidden).astype(np.float32)
     _put(gpu, "x", x)
@@ -219,17 +219,44 @@ def test_ffn_launch_full_shape(layer7b):
     _check(f"{mode} FFN launch: x + down", got, want)
 
 
+def test_o_ffn_launch_full_shape(layer7b):
+    """o, gate/up and down in one launch (the decode's): x + W_o attn formed
+    16 rows per block and handed over as tagged words, then the FFN on it;
+    against the oracle's o matvec + residual, then its FFN, at the 7B
+    shape."""
+    mode, gpu, ref = layer7b
+    rng = np.random.default_rng(111)
+    x = rng.standard_normal(gpu.hidden).astype(np.float32)
+    att = rng.standard_normal(gpu.n_heads * gpu.head_dim).astype(np.float32)
+    _put(gpu, "x", x)
+    _put(gpu, "attn", att)
+    gpu.cl.lib.gsdh_model_run_linear(gpu._m, 0, 14)
+    got = _get(gpu, "x", gpu.hidden)
+    yo = np.empty(gpu.hidden, np.float32)
+    ref.matvec(att, ref.layers[0]["o"], yo)
+    x1 = x + yo
+    hr, y, want = _ffn_ref(ref, x1)
+    _check(f"{mode} o + FFN launch: h", _get(gpu, "h", gpu.ffn_size), hr)
+    _check(f"{mode} o + FFN launch: x + o + down", got, want)
+    _check(f"{mode} o + FFN launch: down (4096x14336) without residual", got - x1, y)
+
+
 def test_ffn_launch_repeat_bit_identical(layer7b):
     """The fused FFN's cross-block sums run in a fixed block order: runs on
-    the same x give the same bits (each launch with a new tag)."""
+    the same x (and attn) give the same bits (each launch with a new tag),
+    with and without the o projection in the launch."""
     mode, gpu, _ = layer7b
-    x = np.random.default_rng(109).standard_normal(gpu.hidden).astype(np.float32)
-    outs = []
-    for _ in range(3):
-        _put(gpu, "x", x)
-        gpu.cl.lib.gsdh_model_run_linear(gpu._m, 0, 12)
-        outs.append(_get(gpu, "x", gpu.hidden))
-    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+    rng = np.random.default_rng(109)
+    x = rng.standard_normal(gpu.hidden).astype(np.float32)
+    att = rng.standard_normal(gpu.n_heads * gpu.head_dim).astype(np.float32)
+    for mask in (12, 14):
+        outs = []
+        for _ in range(3):
+            _put(gpu, "x", x)
+            _put(gpu, "attn", att)
+            gpu.cl.lib.gsdh_model_run_linear(gpu._m, 0, mask)
+            outs.append(_get(gpu, "x", gpu.hidden))
+        assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2]), mask
 
 
 @pytest.mark.parametrize("mode", ["turbo", "precision"])
@@ -237,7 +264,8 @@ def test_ffn_launch_ragged_kinks(mode):
     """The fused FFN at hidden 2048 / ffn 5056 (79 row blocks of 64, 128
     reducing slices, one chunk of x per wave) with kink terms in gate, up and
     down (down's read h of other blocks through the tagged h words), alone
-    and after an o launch."""
+    (mask 12) and with the o projection in the launch (mask 14: o's kinks
+    too, gate / up's kinks reading x + W_o attn from the tagged x words)."""
     from gsdlq import synth
     import run_gpu_native_chat as chat
     banner(f"fused FFN 2048 / 5056 {mode}, kinks")
@@ -247,7 +275,7 @@ def test_ffn_launch_ragged_kinks(mode):
     gpu = chat.GPUMistralV2Model(src, max_seq_len=16, verbose=False)
     ref = O.OracleModel(src, kind="port", max_seq_len=16)
     try:
-        assert gpu.cl.lib.gsdh_model_fused_ffn(gpu._m, 0) == 1
+        assert gpu.cl.lib.gsdh_model_fused_ffn(gpu._m, 0) == 2
         rng = np.random.default_rng(110)
         for mask in (12, 14):
             x = rng.standard_normal(gpu.hidden).astype(np.float32)

@@ -241,36 +241,36 @@ def test_fused_attention_matches_two_launches(mode, shape, monkeypatch):
     ("precision", dict(codebook_radius=5, kinks_per_row=1)),                  # 91-point codebook, 7-bit tiles
 ])
 def test_fused_ffn_matches_two_launches(mode, shape, monkeypatch):
-    """Every decode token runs gate/up + down as one fused FFN launch where it
-    covers the model; with GSD_FUSED_FFN=0 the model issues the gate/up and
-    the down launches instead.  Both match the oracle at every checked
-    position, and each other closely; greedy tokens are equal."""
-    banner(f"fused FFN vs two launches {mode} {shape}")
+    """Every decode token runs o, gate/up and down as one launch where it
+    covers the model (2), or gate/up + down as one (1); with GSD_FUSED_FFN=0
+    the model issues the o, gate/up and down launches.  All match the oracle
+    at every checked position, and each other closely; greedy tokens are
+    equal."""
+    banner(f"fused FFN vs separate launches {mode} {shape}")
     from gsdlq import synth
     import run_gpu_native_chat as chat
     src = synth.SynthSource(_spec(mode=mode, **shape))
     models = []
-    for ff in ("1", "0"):
+    for ff, of in (("1", "1"), ("1", "0"), ("0", "1")):
         monkeypatch.setenv("GSD_FUSED_FFN", ff)
+        monkeypatch.setenv("GSD_FUSED_OFFN", of)
         models.append(chat.GPUMistralV2Model(src, max_seq_len=128, verbose=False))
-    fused, plain = models
-    assert fused.cl.lib.gsdh_model_fused_ffn(fused._m, 0) == 1
-    assert plain.cl.lib.gsdh_model_fused_ffn(plain._m, 0) == 0
+    kinds = [m.cl.lib.gsdh_model_fused_ffn(m._m, 0) for m in models]
+    square = src.config["n_heads"] * src.config["head_dim"] == src.config["hidden_size"]
+    assert kinds == [2 if square else 1, 1, 0], kinds
     ref = O.OracleModel(src, kind="port", max_seq_len=128)
-    toks = np.random.default_rng(8).integers(0, fused.vocab_size, 40).tolist()
+    toks = np.random.default_rng(8).integers(0, models[0].vocab_size, 40).tolist()
     for pos, t in enumerate(toks):
         want = pos % 5 == 0 or pos == len(toks) - 1
-        a = fused.forward_token(t, pos, return_logits=want)
-        b = plain.forward_token(t, pos, return_logits=want)
+        outs = [m.forward_token(t, pos, return_logits=want) for m in models]
         r = ref.forward_token(t, pos, return_logits=want)
         if want:
-            assert rel_l2(a, r) < 1e-3, pos
-            assert rel_l2(b, r) < 1e-3, pos
-            assert rel_l2(a, b) < 1e-4, pos
-    ta, _ = fused.generate_greedy(toks[:5], 12)
-    tb, _ = plain.generate_greedy(toks[:5], 12)
+            for o in outs:
+                assert rel_l2(o, r) < 1e-3, pos
+                assert rel_l2(o, outs[-1]) < 1e-4, pos
     tr, _ = ref.generate_greedy(toks[:5], 12)
-    assert ta == tr and tb == tr
+    for m in models:
+        assert m.generate_greedy(toks[:5], 12)[0] == tr
     for m in models:
         m.close()
 
