@@ -234,7 +234,9 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
             cw[i] = tile_load(cp + lto);
             sw[i] = sp[lso];
         };
-        if (nsteps > 0) {
+        // (OF: the FFN's first code steps go out after the o steps, so that
+        // they do not share the HBM with o's code loads)
+        if (!OF && nsteps > 0) {
 #pragma unroll
             for (int i = 0; i < D; i++) issue(i);
         }
@@ -393,6 +395,10 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                     acc = fmaf(r0, h2f((uint16_t)(osw[p] & 0xFFFFu)), acc);
                     acc = fmaf(r1, h2f((uint16_t)(osw[p] >> 16)), acc);
                 }
+                if (nsteps > 0) {
+#pragma unroll
+                    for (int i = 0; i < D; i++) issue(i);
+                }
                 if (lane < 16) red[wid][0][lane] = acc * dno;
                 lds_barrier();
                 if (wid == 0) {
@@ -423,6 +429,10 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                 }
             }
             if (work) {
+                if (!doO && nsteps > 0) {
+#pragma unroll
+                    for (int i = 0; i < D; i++) issue(i);
+                }
                 // ---- x = x + W_o attn of every row the wave's chunks cover,
                 // from the blocks that formed them (bounded wait); with it
                 // the norm weights and rank-2 rows
