@@ -4,8 +4,8 @@ Workload (the metric's configuration): the full Mistral-7B linear set of one
 layer -- q 4096x4096, k/v 1024x4096, o 4096x4096, gate/up 14336x4096,
 down 4096x14336 -- packed in Turbo mode (radius 8, ~4.26 bpw), batch 1, fp32
 activations.  A step is one pass of the layer's fused unpack-matvec launches
-(qkv with fused RMSNorm, o + residual, and one FFN launch: RMSNorm, gate/up,
-SwiGLU, down split over the FFN rows, residual).  Steps rotate over
+(qkv with fused RMSNorm; one launch for o + residual, RMSNorm, gate/up,
+SwiGLU, down split over the FFN rows and residual).  Steps rotate over
 `--layers` distinct packed layers
 (> 256 MB) so the Infinity Cache cannot serve the weights, and are timed with
 HIP events around a captured HIP graph on the engine's stream.
@@ -16,8 +16,8 @@ byte each for radius 8, seven bits for radius <= 6) + fp16 scales + row_ptr +
 6 B per kink + low-rank factors + x (4 B/col) + y (4 B/row).
 
 Also reported: the same for Precision mode (radius 6: 7-bit codes, rank 2),
-the dominant kernel's roofline (the fused FFN launch: 2 x 14336x4096 +
-4096x14336 of weights, x in and out), decode attention with RoPE + K/V append at contexts 512 / 2048 /
+the dominant kernel's roofline (the fused o + FFN launch: 4096x4096 +
+2 x 14336x4096 + 4096x14336 of weights, attn and x in, x out), decode attention with RoPE + K/V append at contexts 512 / 2048 /
 8192 (GB/s of K/V cache read), end-to-end greedy decode tok/s of a 32-layer
 7B-shaped model, and the reference CPU engine timed on this host's cores on a
 bounded sample.
@@ -72,10 +72,12 @@ def alg_bytes(f):
     return weight_bytes(f) + 4 * f["cols"] + 4 * f["rows"]
 
 
-def ffn_bytes(bank, l):
-    """Algorithmic bytes of the fused FFN launch of layer l: the gate, up and
-    down weights, x read once and x written (h stays inside the launch)."""
-    return sum(weight_bytes(bank.packed[(l, t)]) for t in ("ffn_gate", "ffn_up", "ffn_down")) + 8 * H
+def ffn_bytes(bank, l, with_o=True):
+    """Algorithmic bytes of the fused o + FFN launch of layer l: the o, gate,
+    up and down weights, attn read, x read once and x written (x + W_o attn
+    and h stay inside the launch); with_o=False: the FFN launch alone."""
+    b = sum(weight_bytes(bank.packed[(l, t)]) for t in ("ffn_gate", "ffn_up", "ffn_down")) + 8 * H
+    return b + (weight_bytes(bank.packed[(l, "attn_output")]) + 4 * H if with_o else 0)
 
 
 class LayerBank:
@@ -159,19 +161,19 @@ def bench_linear(bank, steps, warmup):
     ms = time_graph(model, ge, 1)
     ms_step = ms / steps
     gbs = sum(bank.layer_bytes[i % L] for i in range(steps)) / (ms * 1e-3) / 1e9
-    # dominant kernel: the fused FFN launch (RMSNorm, gate/up 2 x 14336 x
-    # 4096, SwiGLU, down 4096 x 14336, residual), timed alone over 128
-    # launches rotating the distinct layers
+    # dominant kernel: the fused o + FFN launch (o 4096 x 4096 + residual,
+    # RMSNorm, gate/up 2 x 14336 x 4096, SwiGLU, down 4096 x 14336 +
+    # residual), timed alone over 128 launches rotating the distinct layers
     ng = 128
-    assert lib.gsdh_model_fused_ffn(model._m, 0) == 1, "the fused FFN launch does not cover this model"
-    gu = capture(model, lambda: [lib.gsdh_model_run_linear(model._m, i % L, 12) for i in range(ng)])
+    assert lib.gsdh_model_fused_ffn(model._m, 0) == 2, "the fused o + FFN launch does not cover this model"
+    gu = capture(model, lambda: [lib.gsdh_model_run_linear(model._m, i % L, 14) for i in range(ng)])
     time_graph(model, gu, 1)
     gms = time_graph(model, gu, 1)
     per_launch_ms = gms / ng
     fb = sum(ffn_bytes(bank, i % L) for i in range(ng)) / ng
     ach = fb / (per_launch_ms * 1e-3) / 1e9
-    roof = {"kernel": "ffn_kernel (MFMA fused RMSNorm + gate/up + SwiGLU + split-K down + residual, "
-                      "2x14336x4096 + 4096x14336)",
+    roof = {"kernel": "ffn_kernel (MFMA fused o + residual, RMSNorm + gate/up + SwiGLU + split-K down + "
+                      "residual: 4096x4096 + 2x14336x4096 + 4096x14336)",
             "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(),
             "launch_us": round(per_launch_ms * 1e3, 2), "alg_bytes_per_launch": int(fb),
@@ -429,8 +431,8 @@ def cpu_decode(bank, n_prompt=2, n_new=6):
 def probe(kind: str, n: int, ctx: int = 8192, m: int = 128):
     """Launch one kernel repeatedly for counter collection under rocprofv3:
     'gateup' = the fused gate/up matvec over 8 rotated Turbo layers,
-    'ffn' = the fused FFN launch (gate/up + SwiGLU + down + residual) over 8
-    rotated Turbo layers,
+    'ffn' = the fused o + FFN launch (o + residual, gate/up + SwiGLU + down +
+    residual) over 8 rotated Turbo layers,
     'copy' = a 256 MiB device copy (the calibration of FETCH/WRITE_SIZE),
     'attn' = RoPE + K/V append and decode attention at context `ctx`,
     'prefill' = the batched projection of 8 Turbo layer sets for `m` tokens,
@@ -484,12 +486,12 @@ def probe(kind: str, n: int, ctx: int = 8192, m: int = 128):
     bank = LayerBank("turbo", 8)
     model = build_model(bank, bank.n)
     model.forward_token(1, 0)
-    mask = 12 if kind == "ffn" else 4
+    mask = 14 if kind == "ffn" else 4
     for i in range(n):
         lib.gsdh_model_run_linear(model._m, i % bank.n, mask)
     lib.gsdh_stream_sync(lib.gsdh_model_stream(model._m))
     if kind == "ffn":
-        print(f"[probe] FFN launches {n}, algorithmic bytes per launch {ffn_bytes(bank, 0)}", flush=True)
+        print(f"[probe] o + FFN launches {n}, algorithmic bytes per launch {ffn_bytes(bank, 0)}", flush=True)
     else:
         gu = sum(alg_bytes(bank.packed[(0, t)]) for t in ("ffn_gate", "ffn_up")) - 4 * H
         print(f"[probe] gate/up launches {n}, algorithmic bytes per launch {gu}", flush=True)
