@@ -303,7 +303,8 @@ int gsdh_model_read_codes(gsdh_model* m, int layer, int slot, uint8_t* codes_out
 
 /* Runs the model's fused matvec launches of `layer` on the model stream with
  * the current activations, without attention or synchronisation.  Mask bit i
- * = launch i of {qkv, o, gate+up, down}:
+ * = projection set i of {qkv, o, gate+up, down} (4 | 8 together run as one
+ * launch, and 2 | 4 | 8 too, where gsdh_model_fused_ffn says so):
  *   1: q, k, v of rmsnorm(x) * attn_norm, RoPE(q) -> q, fp16 RoPE(k) and v
  *      appended to the cache at the step position (run_gpu_native_chat.py:
  *      899-925);  2: x += W_o attn;  4: h = silu(W_gate x') * (W_up x') with
