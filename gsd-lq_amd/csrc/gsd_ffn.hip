@@ -227,15 +227,19 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
         uint4 cw[D];
         uint32_t sw[D];
         int ls = 0;
+        // (no loads past the wave's last step: the slice reduction's polls
+        // would return behind them)
         auto issue = [&](int i) {
+            if (ls >= nsteps) return;
             const unsigned char* cp;
             const uint32_t* sp;
             step_ptr(ls++, cp, sp);
             cw[i] = tile_load(cp + lto);
             sw[i] = sp[lso];
         };
-        // (OF: the FFN's first code steps go out after the o steps, so that
-        // they do not share the HBM with o's code loads)
+        // (OF: the FFN's first code steps go out once the new x is in: a
+        // load returns after every load the wave issued before it, so steps
+        // issued earlier would hold back each poll of the new x)
         if (!OF && nsteps > 0) {
 #pragma unroll
             for (int i = 0; i < D; i++) issue(i);
@@ -395,10 +399,6 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                     acc = fmaf(r0, h2f((uint16_t)(osw[p] & 0xFFFFu)), acc);
                     acc = fmaf(r1, h2f((uint16_t)(osw[p] >> 16)), acc);
                 }
-                if (nsteps > 0) {
-#pragma unroll
-                    for (int i = 0; i < D; i++) issue(i);
-                }
                 if (lane < 16) red[wid][0][lane] = acc * dno;
                 lds_barrier();
                 if (wid == 0) {
@@ -429,10 +429,6 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                 }
             }
             if (work) {
-                if (!doO && nsteps > 0) {
-#pragma unroll
-                    for (int i = 0; i < D; i++) issue(i);
-                }
                 // ---- x = x + W_o attn of every row the wave's chunks cover,
                 // from the blocks that formed them (bounded wait); with it
                 // the norm weights and rank-2 rows
@@ -456,6 +452,10 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                         }
                         __builtin_amdgcn_s_sleep(2);
                     }
+                }
+                if (nsteps > 0) {
+#pragma unroll
+                    for (int i = 0; i < D; i++) issue(i);
                 }
                 stage_x();
                 if (R2 && wid == 0) hu[2][lane] = frow < ffn ? (dv0 | (dv1 << 16)) : 0u;
