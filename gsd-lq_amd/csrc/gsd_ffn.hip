@@ -101,14 +101,13 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     __shared__ float ssq[NW];
     __shared__ float vtp[NW][4];
     __shared__ float ovtp[NW][2];          // OF: each wave's attn . Vt_o[j]
-    __shared__ float sS[8];                // OF, R2: S_o[j] at 6 + j
+    __shared__ float sS[8];                // R2: S[j] of gate at j, up at 2 + j; OF: S_o[j] at 6 + j
     __shared__ uint32_t hu[3][64];         // R2, lane l: U of gate / up row 64 b + l, down Vt column 64 b + l
     __shared__ float hsc;                  // descale of the h operands
     __shared__ float tk[2];                // down's rank values S[j] * (Vt[j] . h)
     __shared__ uint32_t pres[2][16];       // the slice's rows: residual x (bits), down's U row
 
     using KU32 = const __attribute__((address_space(4))) uint32_t;
-    using KF32 = const __attribute__((address_space(4))) float;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int b = blockIdx.x;
@@ -201,14 +200,18 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
             load_x_aux();
         }
         // wave 0: U rows of the block's gate and up rows, down's Vt columns
-        // of the block's slab (lane l: FFN row / column 64 b + l)
+        // of the block's slab (lane l: FFN row / column 64 b + l), and the S
+        // values of gate (lanes 0-1) and up (lanes 2-3), which read at h time
+        // would each put a memory round trip there
         const int frow = 64 * b + lane, fr = min(frow, ffn - 1);
         uint32_t gur = 0u, uur = 0u, dv0 = 0u, dv1 = 0u;
+        float gus = 0.f;
         if (R2 && work && wid == 0) {
             gur = reinterpret_cast<const uint32_t*>(ka->gU)[fr];
             uur = reinterpret_cast<const uint32_t*>(ka->uU)[fr];
             dv0 = ka->dVt[fr];
             dv1 = ka->dVt[ffn + fr];
+            gus = (lane & 2 ? a.uS : a.gS)[lane & 1];
         }
 
         auto step_ptr = [&](int s, const unsigned char*& cp, const uint32_t*& sp) {
@@ -368,6 +371,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
             hu[0][lane] = gur;
             hu[1][lane] = uur;
             if (!OF) hu[2][lane] = frow < ffn ? (dv0 | (dv1 << 16)) : 0u;
+            if (lane < 4) sS[lane] = gus;
         }
         if (!OF && reduces && wid == 0 && lane < 16) {
             pres[0][lane] = xres;
@@ -552,8 +556,8 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
                         e1 += vtp[w][3];
                     }
                     // tmp_k[j] = S[j] * (x' . Vt[j]) (gsd_lq_cpu_engine.c:110-127)
-                    const float tg0 = ((KF32*)ka->gS)[0] * (d0 * inv), tg1 = ((KF32*)ka->gS)[1] * (d1 * inv);
-                    const float tu0 = ((KF32*)ka->uS)[0] * (e0 * inv), tu1 = ((KF32*)ka->uS)[1] * (e1 * inv);
+                    const float tg0 = sS[0] * (d0 * inv), tg1 = sS[1] * (d1 * inv);
+                    const float tu0 = sS[2] * (e0 * inv), tu1 = sS[3] * (e1 * inv);
                     const uint32_t gw = hu[0][lane], uw = hu[1][lane];
                     g += h2f((uint16_t)(gw & 0xFFFFu)) * tg0;
                     g += h2f((uint16_t)(gw >> 16)) * tg1;
@@ -678,6 +682,8 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
         v = swap_add32(v, v, false);  // + the lanes 32 apart
         if (lane < 16) rsum[wid][lane] = v;
         if (R2 && wid == 1) {
+            // down's S (issued ahead of the polls, whose round trip it shares)
+            const float ds0 = a.dS[0], ds1 = a.dS[1];
             // rank words: lane l, blocks l + 64 i, both j in one 16-byte load
             int ro[NI];
             bool rok[NI];
@@ -715,8 +721,8 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
             d0 = wave_sum_valu(d0);
             d1 = wave_sum_valu(d1);
             if (lane == 0) {
-                tk[0] = ((KF32*)ka->dS)[0] * d0;
-                tk[1] = ((KF32*)ka->dS)[1] * d1;
+                tk[0] = ds0 * d0;
+                tk[1] = ds1 * d1;
             }
         }
     }
