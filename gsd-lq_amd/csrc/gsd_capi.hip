@@ -421,6 +421,15 @@ int gsdh_greedy_argmax(void* stream, const float* logits, int n, int* token_out,
     return 0;
 }
 
+int gsdh_greedy_argmax_split(void* stream, const float* logits, int n, int* token_out, float* margin_out,
+                             uint64_t* words, uint32_t* counters) {
+    if (n <= 0) return fail(-1, "argmax_split: n %d", n);
+    if (!logits || !token_out || !margin_out || !words || !counters) return fail(-1, "argmax_split: null argument");
+    HIPCHK(launch_argmax(logits, n, nullptr, token_out, margin_out, 0, S(stream),
+                         reinterpret_cast<unsigned long long*>(words), counters));
+    return 0;
+}
+
 }  // extern "C"
 
 // ---------------------------------------------------------------------------
@@ -490,6 +499,9 @@ struct gsdh_model {
     unsigned long long* fa_words = nullptr;
     unsigned* fa_epoch = nullptr;
     bool fa_on = true;                   // GSD_FUSED_ATTN=0 turns it off (A/B)
+    // the greedy step's hand-off words and per-block launch counters
+    unsigned long long* am_words = nullptr;
+    unsigned* am_ctr = nullptr;
     // the fused FFN launch (gate/up + SwiGLU + down + residual): its partial
     // words and per-block launch counters
     unsigned long long* ffn_words = nullptr;
@@ -707,7 +719,8 @@ int issue_head(gsdh_model* m, bool greedy) {
     int rc = prep_lowrank(m, a);
     if (rc) return rc;
     HIPCHK(launch_hexmv4(a, m->stream));
-    if (greedy) HIPCHK(launch_argmax(m->logits, c.vocab, m->st, m->gen_tok, m->gen_margin, 1, m->stream));
+    if (greedy)
+        HIPCHK(launch_argmax(m->logits, c.vocab, m->st, m->gen_tok, m->gen_margin, 1, m->stream, m->am_words, m->am_ctr));
     return 0;
 }
 
@@ -996,6 +1009,8 @@ int gsdh_model_create(const gsdh_model_config* cfg, gsdh_model** out) {
     A((void**)&m->pub, (size_t)m->pub_words * 8);
     A((void**)&m->fa_words, (qd + kvd) * 8);
     A((void**)&m->fa_epoch, 4);
+    A((void**)&m->am_words, 3 * kArgBlocks * 8);
+    A((void**)&m->am_ctr, kArgBlocks * 4);
     {
         const char* fe = std::getenv("GSD_FUSED_ATTN");
         m->fa_on = !(fe && fe[0] == '0');
@@ -1040,6 +1055,8 @@ int gsdh_model_create(const gsdh_model_config* cfg, gsdh_model** out) {
         if (e == hipSuccess) e = launch_fill_u32((unsigned*)m->pub, 0u, 2 * (size_t)m->pub_words, m->stream);
         if (e == hipSuccess) e = launch_fill_u32((unsigned*)m->fa_words, 0u, 2 * (qd + kvd), m->stream);
         if (e == hipSuccess) e = launch_fill_u32(m->fa_epoch, 0u, 1, m->stream);
+        if (e == hipSuccess) e = launch_fill_u32((unsigned*)m->am_words, 0u, 6 * kArgBlocks, m->stream);
+        if (e == hipSuccess) e = launch_fill_u32(m->am_ctr, 0u, kArgBlocks, m->stream);
         if (e == hipSuccess && m->ffn_on)
             e = launch_fill_u32((unsigned*)m->ffn_words, 0u, 2 * ffn_words(c.hidden, c.ffn), m->stream);
         if (e == hipSuccess && m->ffn_on) e = launch_fill_u32(m->ffn_ctr, 0u, kFfnMaxGrid, m->stream);

@@ -436,8 +436,12 @@ struct StepState {
     unsigned err;       // nonzero: a bounded in-kernel wait timed out
     int pad[3];
 };
+// words (3 kArgBlocks) and ctr (kArgBlocks, zero at first use, used by one
+// launch at a time): the multi-block form; otherwise one block
+constexpr int kArgBlocks = 32;
 hipError_t launch_argmax(const float* logits, int n, StepState* st, int* gen_tokens,
-                         float* gen_margins, int advance, hipStream_t stream);
+                         float* gen_margins, int advance, hipStream_t stream,
+                         unsigned long long* words = nullptr, unsigned* ctr = nullptr);
 // st->token, pos = (token, pos), gen_count = 0; err cleared only with reset_err
 hipError_t launch_set_step(StepState* st, int token, int pos, int reset_err, hipStream_t stream);
 hipError_t launch_fill_u32(unsigned* p, unsigned v, size_t n, hipStream_t stream);

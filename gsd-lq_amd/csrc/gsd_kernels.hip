@@ -1478,6 +1478,26 @@ __global__ void embed_kernel(const uint16_t* embed, const int* token, float* x, 
 }
 
 
+// the greedy step's outputs: the token and margin (stand-alone call, st
+// null), or the step state, the generated token list and the position
+__device__ __forceinline__ void argmax_finish(const Top2 r, StepState* st, int* gen_tok, float* gen_margin, int advance,
+                                              int c0, int p0) {
+    const float margin = r.v1 - r.v2;
+    if (!st) {
+        gen_tok[0] = r.i1;
+        gen_margin[0] = margin;
+        return;
+    }
+    st->token = r.i1;
+    if (gen_tok) {
+        gen_tok[c0] = r.i1;
+        gen_margin[c0] = margin;
+        st->gen_count = c0 + 1;
+    }
+    if (advance) st->pos = p0 + 1;
+    st->margin_bits = __float_as_int(margin);
+}
+
 __global__ void __launch_bounds__(1024) argmax_kernel(const float* logits, int n, StepState* st, int* gen_tok,
                                                       float* gen_margin, int advance) {
     __shared__ Top2 sw[16];
@@ -1515,20 +1535,104 @@ __global__ void __launch_bounds__(1024) argmax_kernel(const float* logits, int n
     if (tid == 0) {
         Top2 r = sw[0];
         for (int w = 1; w < (int)(blockDim.x >> 6); w++) r = merge(r, sw[w]);
-        const float margin = r.v1 - r.v2;
-        if (!st) {   // stand-alone call: the token and margin only
-            gen_tok[0] = r.i1;
-            gen_margin[0] = margin;
-            return;
+        argmax_finish(r, st, gen_tok, gen_margin, advance, c0, p0);
+    }
+}
+
+// The greedy step of the decode graph over kArgBlocks blocks: one block's
+// loads of a 32768-entry vocabulary (128 KB through one CU's outstanding
+// misses) took ~11 us.  Block b takes entries b * per .. b * per + per - 1,
+// keeps (top1, top2, first index of top1) in index order, and hands it over
+// as three tagged words (tag: the block's launch count + 1, as every block
+// runs each launch); the last block (dispatched last, so every other block
+// has started) polls the others' words (bounded: a wait that runs out sets
+// st->err), merges them and its own, and finishes as argmax_kernel.  Merging is order-free: the largest value
+// with the lowest index is a total order, the runner-up the second largest
+// of the union.
+__device__ __forceinline__ Top2 top2_add(Top2 t, float c, int i) {
+    // i above every index seen: a tie keeps the earlier index
+    const bool gt = c > t.v1;
+    t.v2 = fmaxf(t.v2, fminf(t.v1, c));
+    t.v1 = gt ? c : t.v1;
+    t.i1 = gt ? i : t.i1;
+    return t;
+}
+__device__ __forceinline__ Top2 wave_top2(Top2 t) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        Top2 u{__shfl_xor(t.v1, o, 64), __shfl_xor(t.v2, o, 64), __shfl_xor(t.i1, o, 64)};
+        t = merge(t, u);
+    }
+    return t;
+}
+__global__ void __launch_bounds__(256) argmax_blocks_kernel(const float* logits, int n, StepState* st, int* gen_tok,
+                                                            float* gen_margin, int advance, unsigned long long* words,
+                                                            unsigned* ctr) {
+    __shared__ Top2 sw[4];
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int b = blockIdx.x, nb = gridDim.x;
+    const bool last = b == nb - 1;
+    const unsigned tag = ctr[b] + 1u;   // (the block's own word)
+    int c0 = 0, p0 = 0;
+    if (last && tid == 0 && st) {
+        c0 = st->gen_count;
+        p0 = st->pos;
+    }
+    const int per = (n + nb - 1) / nb, e0 = b * per, e1 = min(n, e0 + per);
+    Top2 t{-INFINITY, -INFINITY, 0x7FFFFFFF};
+    constexpr int K = 8;
+    for (int base = e0 + tid; base < e1; base += 256 * K) {
+        float v[K];
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            const int i = base + 256 * k;
+            v[k] = i < e1 ? logits[i] : 0.f;
         }
-        st->token = r.i1;
-        if (gen_tok) {
-            gen_tok[c0] = r.i1;
-            gen_margin[c0] = margin;
-            st->gen_count = c0 + 1;
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            const int i = base + 256 * k;
+            if (i < e1) t = top2_add(t, clean(v[k]), i);
         }
-        if (advance) st->pos = p0 + 1;
-        st->margin_bits = __float_as_int(margin);
+    }
+    t = wave_top2(t);
+    if (lane == 0) sw[wid] = t;
+    __syncthreads();
+    if (!last) {
+        if (tid == 0) {
+            const Top2 r = merge(merge(sw[0], sw[1]), merge(sw[2], sw[3]));
+            unsigned long long* w = words + 3 * (size_t)b;
+            const unsigned long long tg = (unsigned long long)tag << 32;
+            __hip_atomic_store(w, tg | __float_as_uint(r.v1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(w + 1, tg | __float_as_uint(r.v2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(w + 2, tg | (unsigned)r.i1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ctr[b] = tag;
+        }
+        return;
+    }
+    if (wid != 0) return;
+    // lane j < nb - 1: block j's words, polled until all carry this tag
+    Top2 o{-INFINITY, -INFINITY, 0x7FFFFFFF};
+    if (lane < nb - 1) {
+        const unsigned long long* w = words + 3 * (size_t)lane;
+        unsigned long long a0, a1, a2;
+        for (int spins = 0;; spins++) {
+            a0 = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            a1 = __hip_atomic_load(w + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            a2 = __hip_atomic_load(w + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if ((unsigned)(a0 >> 32) == tag && (unsigned)(a1 >> 32) == tag && (unsigned)(a2 >> 32) == tag) break;
+            if (spins == (1 << 16)) {   // (bounded, ~65 ms)
+                if (st) st->err = 1u;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        o = Top2{__uint_as_float((unsigned)a0), __uint_as_float((unsigned)a1), (int)(unsigned)a2};
+    }
+    o = wave_top2(o);
+    if (lane == 0) {
+        const Top2 r = merge(o, merge(merge(sw[0], sw[1]), merge(sw[2], sw[3])));
+        ctr[b] = tag;
+        argmax_finish(r, st, gen_tok, gen_margin, advance, c0, p0);
     }
 }
 
@@ -1905,7 +2009,7 @@ __device__ __forceinline__ void attn_fa_block(const FaIn a, int kvh, unsigned ta
 // per KV head); the matvec blocks are the others and run a.mv.nw waves each
 // (the attention runs 8), and the RoPE + K/V epilogue also publishes q and
 // the new K/V rows as tagged words (HexArgs::FusedAttn).
-template <int TB, int LR, int EPI, int FAHD = 0, int FAG = 0>
+template <int TB, int LR, int EPI, int FAHD = 0, int FAG = 0, int DEP = kMv4Depth>
 __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) hexmv4_kernel(const HexArgs a) {
     constexpr bool FA = FAHD > 0;
     if constexpr (FA) {
@@ -2019,7 +2123,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     // this wave's steps: P chunks (wr, wr + WR, ...) of each of the block's
     // units in turn (units u0, u0 + nblk, ...); P is the same for every wave
     // (WR divides nc), so unit ends, and their barriers, fall on the same step
-    // in all waves.  The load cursor runs kMv4Depth steps ahead of the compute
+    // in all waves.  The load cursor runs DEP steps ahead of the compute
     // cursor; both advance by compare-and-reset, and per-unit base pointers
     // are recomputed only when a unit starts.  Past the block's last unit
     // the load cursor stays on that unit (valid addresses, unused data,
@@ -2287,11 +2391,11 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
         }
     }
 
-    uint4 cw[kMv4Depth];
-    uint32_t sw[kMv4Depth];
+    uint4 cw[DEP];
+    uint32_t sw[DEP];
     lset(0);
 #pragma unroll
-    for (int i = 0; i < kMv4Depth; i++) lissue(cw[i], sw[i]);
+    for (int i = 0; i < DEP; i++) lissue(cw[i], sw[i]);
 
     // codebook copies: entry e of lane l at byte e * 256 + l * 4.  Wave w
     // writes entries 16w .. 16w + 15 (waves 16 apart when fewer than 16
@@ -2615,13 +2719,13 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
             cg = seg_of(min(cu, nunits - 1));
         }
     };
-    // kMv4Depth steps in flight at all times: buffer i holds the steps s
-    // with s % kMv4Depth == i; every load is issued (the cursor clamps past
+    // DEP steps in flight at all times: buffer i holds the steps s
+    // with s % DEP == i; every load is issued (the cursor clamps past
     // the end), and the last group may compute steps past the end that no
     // unit end collects
-    for (int s = 0; s < nsteps; s += kMv4Depth) {
+    for (int s = 0; s < nsteps; s += DEP) {
 #pragma unroll
-        for (int i = 0; i < kMv4Depth; i++) {
+        for (int i = 0; i < DEP; i++) {
             step(cg, cj + cp0, cw[i], sw[i], acc);
             lissue(cw[i], sw[i]);
             cadvance();
@@ -3493,19 +3597,20 @@ static bool half_units_reach(const HexArgs& a) {
            span((uint64_t)(uintptr_t)g.scales_t, (uint64_t)(uintptr_t)u.scales_t, nrb * nc * 64) < (1ull << 32);
 }
 
-template <int TB, int LR, int EPI>
+template <int TB, int LR, int EPI, int DEP = kMv4Depth>
 hipError_t launch_hexmv4_t(const HexArgs& a0, hipStream_t st, int nw, size_t lds, int nunits, int nlead) {
     static int per_cu = 0;
     static size_t attr_lds = 0;
     if (lds > attr_lds) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&hexmv4_kernel<TB, LR, EPI>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&hexmv4_kernel<TB, LR, EPI, 0, 0, DEP>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         attr_lds = lds;
         per_cu = 0;
     }
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, hexmv4_kernel<TB, LR, EPI>, nw * 64, lds) != hipSuccess || n < 1)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, hexmv4_kernel<TB, LR, EPI, 0, 0, DEP>, nw * 64, lds) != hipSuccess ||
+        n < 1)
         return hipErrorInvalidConfiguration;
     per_cu = n;
     const int ncu = device_cu_count() > 0 ? device_cu_count() : 256;
@@ -3533,7 +3638,7 @@ hipError_t launch_hexmv4_t(const HexArgs& a0, hipStream_t st, int nw, size_t lds
             a.mv.su_u0 = a.mv.units_q * grid;
         }
     }
-    hipLaunchKernelGGL((hexmv4_kernel<TB, LR, EPI>), dim3(grid + nlead), dim3(nw * 64), lds, st, a);
+    hipLaunchKernelGGL((hexmv4_kernel<TB, LR, EPI, 0, 0, DEP>), dim3(grid + nlead), dim3(nw * 64), lds, st, a);
     return hipGetLastError();
 }
 
@@ -3644,10 +3749,18 @@ hipError_t launch_hexmv4(const HexArgs& a, hipStream_t st) {
 #undef GSD_QA
         return hipErrorNotSupported;
     }
-    // the shared-codebook kernels are specialised on the epilogue as well
+    // the shared-codebook kernels are specialised on the epilogue as well.
+    // Many units per block (the output projection: 2048 units on 256 CUs)
+    // stream at a ring depth of 4: at 2, each CU's 16 waves keep 32 KB in
+    // flight, which at the memory latency is about half the HBM rate
+    const bool deep = nunits >= 6 * (device_cu_count() > 0 ? device_cu_count() : 256);
 #define GSD_MV4(T, E)                                                                           \
     {                                                                                           \
         const size_t lds = xbytes + (T == 0 ? (size_t)tab_bytes : 0);                           \
+        if constexpr (T > 0 && E == kEpiStore) {                                                \
+            if (deep && !lr) return launch_hexmv4_t<T, 0, E, 4>(ap, st, nw, lds, nunits, 0);     \
+            if (deep && inblock && all2) return launch_hexmv4_t<T, 3, E, 4>(ap, st, nw, lds, nunits, 0); \
+        }                                                                                       \
         if (!lr) return launch_hexmv4_t<T, 0, E>(ap, st, nw, lds, nunits, 0);                   \
         if (inblock && all2) return launch_hexmv4_t<T, 3, E>(ap, st, nw, lds, nunits, 0);       \
         if (inblock) return launch_hexmv4_t<T, 1, E>(ap, st, nw, lds, nunits, 0);               \
@@ -4018,8 +4131,12 @@ hipError_t launch_set_step(StepState* stt, int token, int pos, int reset_err, hi
 }
 
 hipError_t launch_argmax(const float* logits, int n, StepState* stt, int* gen_tokens, float* gen_margins,
-                         int advance, hipStream_t st) {
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, st, logits, n, stt, gen_tokens, gen_margins, advance);
+                         int advance, hipStream_t st, unsigned long long* words, unsigned* ctr) {
+    if (words && ctr)
+        hipLaunchKernelGGL(argmax_blocks_kernel, dim3(kArgBlocks), dim3(256), 0, st, logits, n, stt, gen_tokens,
+                           gen_margins, advance, words, ctr);
+    else
+        hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, st, logits, n, stt, gen_tokens, gen_margins, advance);
     return hipGetLastError();
 }
 

@@ -63,6 +63,7 @@ SIGNATURES = {
     "gsdh_graph_destroy": [vp],
     "gsdh_graph_time": [vp, vp, i32, ctypes.POINTER(f32)],
     "gsdh_greedy_argmax": [vp, vp, i32, vp, vp],
+    "gsdh_greedy_argmax_split": [vp, vp, i32, vp, vp, vp, vp],
     "gsdh_model_vector": [vp, i32, i32, vp, u64],
     "gsdh_model_set_step": [vp, i32, i32],
     "gsdh_model_read_kv": [vp, i32, i32, vp, vp],

@@ -185,9 +185,17 @@ int gsdh_unpack_codes(void* stream, const uint8_t* codes, int64_t n, int radius,
 /* Greedy branch of sample_token (gsd_lq_cpu_runtime.py:422-425):
  * nan_to_num(nan=-1e4, posinf=100, neginf=-1e4), then the first index of the
  * maximum.  logits: device f32 [n]; writes the token to device *token_out and
- * the top1 - top2 margin of the cleaned values to device *margin_out.  The
- * same kernel ends every greedy step of the model context. */
+ * the top1 - top2 margin of the cleaned values to device *margin_out.  One
+ * block: calls on any streams may overlap. */
 int gsdh_greedy_argmax(void* stream, const float* logits, int n, int* token_out, float* margin_out);
+/* The same greedy step over 32 blocks, the form that ends every greedy step
+ * of the model context (one block's loads of a 32768-entry vocabulary are
+ * bound by one CU's outstanding misses).  words: device u64 [96], counters:
+ * device u32 [32], both zero before their first call; calls that share them
+ * must not overlap (one stream).  Same outputs as gsdh_greedy_argmax
+ * (gsd_lq_cpu_runtime.py:422-425). */
+int gsdh_greedy_argmax_split(void* stream, const float* logits, int n, int* token_out, float* margin_out,
+                             uint64_t* words, uint32_t* counters);
 
 /* ------------------------------------------------------------------------ */
 /* 2. Model context (replaces GPUMistralV2Model's device side)              */

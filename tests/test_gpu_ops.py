@@ -372,18 +372,31 @@ def _argmax_cases():
     return cases
 
 
+@pytest.mark.parametrize("split", [False, True], ids=["one_block", "split"])
 @pytest.mark.parametrize("name", sorted(_argmax_cases()))
-def test_greedy_argmax_special_values(lib, name):
+def test_greedy_argmax_special_values(lib, name, split):
     """The device greedy step against gsd_lq_cpu_runtime.py:422-425:
     nan_to_num(nan=-1e4, posinf=100, neginf=-1e4), then the first index of
-    the maximum; the margin is top1 - top2 of the cleaned values."""
+    the maximum; the margin is top1 - top2 of the cleaned values.  split: the
+    32-block form of the model's decode graph, called twice on one workspace
+    (the second call's hand-off words carry the next tag); a case's ties and
+    special values then fall in different blocks (1024 entries each at 32768)."""
     lg = _argmax_cases()[name]
     want = O.OracleModel.greedy(lg)
     clean = np.nan_to_num(lg, nan=-1e4, posinf=100.0, neginf=-1e4)
     srt = np.sort(clean)
     want_margin = np.float32(srt[-1] - (srt[-2] if clean.size > 1 else -np.inf))
     d = D(lg)
-    tok, mg = E(4), E(4)
-    lib.gsdh_greedy_argmax(None, p(d), lg.size, p(tok), p(mg))
-    assert int(H(tok, np.int32, 1)[0]) == want, name
-    assert H(mg, np.float32, 1)[0] == want_margin, name
+    if not split:
+        tok, mg = E(4), E(4)
+        lib.gsdh_greedy_argmax(None, p(d), lg.size, p(tok), p(mg))
+        assert int(H(tok, np.int32, 1)[0]) == want, name
+        assert H(mg, np.float32, 1)[0] == want_margin, name
+        return
+    words, ctr = D(np.zeros(96, np.uint64)), D(np.zeros(32, np.uint32))
+    for call in range(2):
+        tok, mg = D(np.full(1, -7, np.int32)), E(4)
+        assert lib.gsdh_greedy_argmax_split(None, p(d), lg.size, p(tok), p(mg), p(words), p(ctr)) == 0
+        assert int(H(tok, np.int32, 1)[0]) == want, (name, call)
+        assert H(mg, np.float32, 1)[0] == want_margin, (name, call)
+    assert np.all(H(ctr, np.uint32) == 2), name
