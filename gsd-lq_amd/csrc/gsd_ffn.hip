@@ -377,6 +377,13 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
             pres[0][lane] = xres;
             pres[1][lane] = dur;
         }
+        // the argument line of the kink tables (first read at the h step,
+        // where a scalar-cache miss would wait behind the streaming loads)
+        // into the scalar cache while the launch waits here anyway
+        {
+            const uint32_t* t = ka->g_rp;
+            __asm__ volatile("" ::"s"(t));
+        }
         // the codebook and every wave's own operands in LDS
         lds_barrier();
 
