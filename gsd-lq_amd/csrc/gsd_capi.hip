@@ -585,7 +585,7 @@ HexArgs qkv_args(gsdh_model* m, int l) {
 // q, k, v of layer l and the decode attention of positions < 256 in one
 // launch (sets *fused); *fused = false, with nothing launched, where the
 // fused kernel does not cover the model (the caller then issues the two).
-int issue_qkv_attention(gsdh_model* m, int l, bool* fused) {
+int issue_qkv_attention(gsdh_model* m, int l, int span, bool* fused) {
     const auto& c = m->c;
     *fused = false;
     if (!m->fa_on || !m->fa_words || !c.rope_interleaved) return 0;
@@ -596,6 +596,7 @@ int issue_qkv_attention(gsdh_model* m, int l, bool* fused) {
     a.fa.words = m->fa_words; a.fa.out = m->attn; a.fa.epoch_dev = m->fa_epoch;
     a.fa.sm_scale = 1.0f / (float)std::sqrt((double)c.head_dim);
     a.fa.nkv = c.n_kv_heads;
+    a.fa.span = span;
     a.err = &m->st->err;
     const hipError_t e = launch_hexmv4(a, m->stream);
     if (e == hipErrorNotSupported) {
@@ -734,7 +735,7 @@ int issue_token(gsdh_model* m, bool with_head, int short_chunk) {
     for (int l = 0; l < c.n_layers; l++) {
         // positions < 256: the attention in the q/k/v launch where it covers the model
         bool fused = false;
-        int rc = short_chunk ? issue_qkv_attention(m, l, &fused) : 0;
+        int rc = short_chunk ? issue_qkv_attention(m, l, short_chunk, &fused) : 0;
         if (rc) return rc;
         if (fused) {
             rc = issue_linear(m, l, 2 | 4 | 8);

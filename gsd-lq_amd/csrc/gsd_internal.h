@@ -93,6 +93,7 @@ struct HexArgs {
         const unsigned* epoch_dev;
         float sm_scale;
         int nkv;                     // 0: no attention blocks
+        int span;                    // positions the blocks cover: 64, 128 or 256 (0: 256)
     } fa;
     // hexmv4 launch plan, filled in by launch_hexmv4 (callers leave it zero):
     // per-launch constants the kernel would otherwise derive with integer

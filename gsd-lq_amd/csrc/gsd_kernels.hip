@@ -1749,8 +1749,11 @@ __device__ __forceinline__ void mv4_publish(const HexArgs& a, int lead, float* s
 // arguments.
 // ------------------------------------------------------------------------
 // Decode attention of one KV head inside the q/k/v launch, positions
-// 0 .. pos with pos < 256 (gsd_lq_cpu_engine.c:264-330): the arithmetic of
-// attn_dec_body for one split of 8 waves x 32 positions, with q and the new
+// 0 .. pos with pos < 8 PW (gsd_lq_cpu_engine.c:264-330): the arithmetic of
+// attn_dec_body for one split of 8 waves x PW positions (PW 8, 16 or 32: the
+// short-context graph's tier of 64, 128 or 256 positions, so that a wave's
+// share of the V weighting and of the matrix-core steps follows the
+// context), with q and the new
 // K / V rows taken from the words the q/k/v epilogue publishes (that launch
 // is still writing them), and the cache rows of the earlier positions
 // loaded at the start, while the matvec blocks run.  The part after the wait
@@ -1778,9 +1781,10 @@ __device__ __forceinline__ uint4 gload4(const __attribute__((address_space(1))) 
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-template <int HD, int G>
+template <int HD, int G, int PW>
 __device__ __forceinline__ void attn_fa_block(const FaIn a, int kvh, unsigned tag) {
-    constexpr int NW = 8, PW = 32, NGRP = 2, NJ = HD / 32, LPR = HD / 8, RPI = 64 / LPR, NV = PW / RPI;
+    constexpr int NW = 8, NGRP = (PW + 15) / 16, NJ = HD / 32, LPR = HD / 8, RPI = 64 / LPR, NV = PW / RPI;
+    static_assert(PW == 8 || PW == 16 || PW == 32, "positions per wave");
     constexpr int NQ = G * HD, NT = NQ + HD;   // words taken: q rows, then K and V pairs
     constexpr float kLog2e = 1.44269504088896340736f;
     static_assert(G == 1 || G == 2 || G == 4, "query heads per KV head");
@@ -1910,8 +1914,11 @@ __device__ __forceinline__ void attn_fa_block(const FaIn a, int kvh, unsigned ta
                 alo[j][e] = (_Float16)(s - (float)h);
             }
         }
-        // scores of the wave's 32 positions: lanes 0-15, element g = head g
-        float sv[NGRP][4];
+        // scores of the wave's positions: lanes 0-15, element g = head g
+        // (PW <= 16: one group, the second all -inf)
+        float sv[2][4];
+#pragma unroll
+        for (int gg = 0; gg < 4; gg++) sv[1][gg] = -INFINITY;
 #pragma unroll
         for (int grp = 0; grp < NGRP; grp++) {
             float4v dd = {0.f, 0.f, 0.f, 0.f};
@@ -2004,12 +2011,12 @@ __device__ __forceinline__ void attn_fa_block(const FaIn a, int kvh, unsigned ta
     }
 }
 
-// FAHD > 0: the q/k/v launch with the decode attention of positions < 256 in
-// its last a.fa.nkv blocks (one per KV head, head dim FAHD, FAG query heads
+// FAHD > 0: the q/k/v launch with the decode attention of positions < 8 FAPW
+// in its last a.fa.nkv blocks (one per KV head, head dim FAHD, FAG query heads
 // per KV head); the matvec blocks are the others and run a.mv.nw waves each
 // (the attention runs 8), and the RoPE + K/V epilogue also publishes q and
 // the new K/V rows as tagged words (HexArgs::FusedAttn).
-template <int TB, int LR, int EPI, int FAHD = 0, int FAG = 0, int DEP = kMv4Depth>
+template <int TB, int LR, int EPI, int FAHD = 0, int FAG = 0, int DEP = kMv4Depth, int FAPW = 32>
 __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) hexmv4_kernel(const HexArgs a) {
     constexpr bool FA = FAHD > 0;
     if constexpr (FA) {
@@ -2019,7 +2026,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
             const unsigned tag = *(KU32c*)a.fa.epoch_dev * 64u + (unsigned)a.rope.layer + 1u;
             const FaIn fi{a.rope.k_cache, a.rope.v_cache, a.rope.pos_dev, a.fa.words, a.fa.out, a.err,
                           a.rope.layer, a.rope.max_seq, a.rope.n_kv, a.rope.n_heads, a.fa.sm_scale};
-            attn_fa_block<FAHD, FAG>(fi, (int)blockIdx.x - nmv, tag);
+            attn_fa_block<FAHD, FAG, FAPW>(fi, (int)blockIdx.x - nmv, tag);
             return;
         }
         if ((int)(threadIdx.x >> 6) >= a.mv.nw) return;
@@ -3647,18 +3654,18 @@ hipError_t launch_hexmv4_t(const HexArgs& a0, hipStream_t st, int nw, size_t lds
 // wait for words of matvec blocks); blocks of max(nw, 8) waves (the
 // attention runs 8).  hipErrorNotSupported before any launch when that does
 // not fit.
-template <int TB, int LR, int HD, int G>
+template <int TB, int LR, int HD, int G, int PW>
 hipError_t launch_qkva_t(const HexArgs& a0, hipStream_t st, int nw, size_t lds, int nunits) {
     const int nt = (nw > 8 ? nw : 8) * 64;
     static size_t attr_lds = 0;
     if (lds > attr_lds) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&hexmv4_kernel<TB, LR, kEpiRopeKV, HD, G>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&hexmv4_kernel<TB, LR, kEpiRopeKV, HD, G, kMv4Depth, PW>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         attr_lds = lds;
     }
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, hexmv4_kernel<TB, LR, kEpiRopeKV, HD, G>, nt, lds) != hipSuccess || per_cu < 1)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, hexmv4_kernel<TB, LR, kEpiRopeKV, HD, G, kMv4Depth, PW>, nt, lds) != hipSuccess || per_cu < 1)
         return hipErrorNotSupported;
     const int ncu = device_cu_count() > 0 ? device_cu_count() : 256;
     int grid = ncu * per_cu - a0.fa.nkv;   // matvec blocks
@@ -3668,7 +3675,7 @@ hipError_t launch_qkva_t(const HexArgs& a0, hipStream_t st, int nw, size_t lds, 
     a.mv.units_q = nunits / grid;
     a.mv.units_r = nunits % grid;
     a.mv.nw = nw;
-    hipLaunchKernelGGL((hexmv4_kernel<TB, LR, kEpiRopeKV, HD, G>), dim3(grid + a.fa.nkv), dim3(nt), lds, st, a);
+    hipLaunchKernelGGL((hexmv4_kernel<TB, LR, kEpiRopeKV, HD, G, kMv4Depth, PW>), dim3(grid + a.fa.nkv), dim3(nt), lds, st, a);
     return hipGetLastError();
 }
 
@@ -3736,10 +3743,16 @@ hipError_t launch_hexmv4(const HexArgs& a, hipStream_t st) {
             !a.rope.pos_dev || a.fa.nkv != a.rope.n_kv || gq * a.rope.n_kv != a.rope.n_heads || a.rope.layer < 0 ||
             a.rope.layer >= 64)
             return hipErrorNotSupported;
+#define GSD_QAP(T, L, HD, G)                                                                                    \
+    {                                                                                                           \
+        if (a.fa.span == 64) return launch_qkva_t<T, L, HD, G, 8>(ap, st, nw, xbytes, nunits);                  \
+        if (a.fa.span == 128) return launch_qkva_t<T, L, HD, G, 16>(ap, st, nw, xbytes, nunits);                \
+        return launch_qkva_t<T, L, HD, G, 32>(ap, st, nw, xbytes, nunits);                                      \
+    }
 #define GSD_QA(T, L)                                                                                            \
     {                                                                                                           \
-        if (a.rope.hd == 128 && gq == 4) return launch_qkva_t<T, L, 128, 4>(ap, st, nw, xbytes, nunits);        \
-        if (a.rope.hd == 64 && gq == 2) return launch_qkva_t<T, L, 64, 2>(ap, st, nw, xbytes, nunits);          \
+        if (a.rope.hd == 128 && gq == 4) GSD_QAP(T, L, 128, 4)                                                  \
+        if (a.rope.hd == 64 && gq == 2) GSD_QAP(T, L, 64, 2)                                                    \
         return hipErrorNotSupported;                                                                            \
     }
         if (a.seg[0].n_pts == 217 && lrm == 0) GSD_QA(217, 0)
@@ -3747,6 +3760,7 @@ hipError_t launch_hexmv4(const HexArgs& a, hipStream_t st) {
         if (a.seg[0].n_pts == 127 && lrm == 0) GSD_QA(127, 0)
         if (a.seg[0].n_pts == 127 && lrm == 3) GSD_QA(127, 3)
 #undef GSD_QA
+#undef GSD_QAP
         return hipErrorNotSupported;
     }
     // the shared-codebook kernels are specialised on the epilogue as well.
